@@ -1,0 +1,6 @@
+"""MiniPrefix CPU oracle -- test infrastructure only.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import
+this package, and only as the checker. The product path never does.
+"""
+from .oracle import Oracle, OracleModel, load, ref_library  # noqa: F401

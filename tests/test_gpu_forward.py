@@ -1,0 +1,114 @@
+"""HIP forward vs the CPU oracle on identical seeded inputs.
+
+The oracle restates the reference CPU path (miniprefix/src/backend/cpu/
+llama_runner.cpp:10-104) op for op; the HIP kernels keep its floating-point
+order, so logits are compared bit for bit (max relative
+error 1e-3, is asserted as well to report how far off a failure is)."""
+import numpy as np
+import pytest
+
+from oracle import Oracle, OracleModel
+from tinyinfer_amd.backend import HipBackend, paged_attention_decode
+
+from .helpers import pool_elements, smollm_config, tiny_config, upload_model
+
+pytestmark = pytest.mark.gpu
+
+
+def _logits_match(got, want):
+    assert np.all(np.isfinite(got))
+    rel = np.max(np.abs(got - want) / np.maximum(np.abs(want), 1e-30))
+    assert rel <= 1e-3, f"max relative error {rel}"
+    mism = np.count_nonzero(got.view(np.uint32) != want.view(np.uint32))
+    assert mism == 0, f"{mism} logits differ in bits (max rel {rel})"
+    assert int(np.argmax(got)) == int(np.argmax(want))
+
+
+def test_config1_paged_attention_decode(torch_cuda):
+    """T=503 (31 full pages + 7), 256-page pool, seeded
+    permutation table, Q/K/V ~ N(0,1), scale 1/sqrt(64)."""
+    torch = torch_cuda
+    o = Oracle()
+    seed, bt, pages, heads, kvh, dim, T = 2024, 16, 256, 9, 3, 64, 503
+    kvw = kvh * dim
+    keys = o.fill_normal(pages * bt * kvw, seed, 2001)
+    values = o.fill_normal(pages * bt * kvw, seed, 2002)
+    q = o.fill_normal(heads * dim, seed, 2003)
+    table = o.permutation(pages, seed, 2004)[:32].copy()
+    want = o.attention(q, keys, values, table, T - 1, 1, 0, 1, bt, heads, kvh, dim)[0]
+    dev = lambda a: torch.from_numpy(a).cuda()
+    dq, dk, dv, dt = dev(q), dev(keys), dev(values), dev(table)
+    out = torch.empty(heads * dim, dtype=torch.float32, device="cuda")
+    paged_attention_decode(dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), dt.data_ptr(), T, 0, 1, bt, heads, kvh,
+                           dim, out.data_ptr(), None)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    assert np.max(np.abs(got - want)) <= 1e-4
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def _run_sequence(model, backend, bt, chunks, table, slot=0):
+    """Append `chunks` (lists of token ids) to one sequence on both sides."""
+    c = model.config
+    n = pool_elements(c, bt, backend.max_blocks)
+    keys = np.zeros(n, dtype=np.float32)
+    values = np.zeros(n, dtype=np.float32)
+    used = 0
+    backend.table_write(slot, 0, table)
+    for chunk in chunks:
+        want = model.append(keys, values, bt, table, used, chunk)
+        am, got = backend.forward([(slot, used, len(chunk))], chunk)
+        _logits_match(got[0], want)
+        assert am[0] == int(np.argmax(want))
+        used += len(chunk)
+    return keys, values
+
+
+def test_tiny_model_chunks(torch_cuda):
+    cfg = tiny_config()
+    model = OracleModel(cfg, seed=7, stddev=0.15)
+    backend = HipBackend(cfg, block_tokens=4, max_blocks=8, max_sequences=4)
+    upload_model(backend, model)
+    table = np.array([5, 2, 7, 0, 3, 1, 6, 4], dtype=np.int32)
+    _run_sequence(model, backend, 4, [[1, 2, 3], [4], [5, 6, 7, 8, 9], [10], [11]], table)
+
+
+def test_smollm_shape_two_layers(torch_cuda):
+    cfg = smollm_config(layers=2, context=256)
+    model = OracleModel(cfg, seed=11)
+    backend = HipBackend(cfg, block_tokens=16, max_blocks=32, max_sequences=4)
+    upload_model(backend, model)
+    o = Oracle()
+    prompt = o.fill_tokens(37, 11, 3000, cfg["vocabulary"])
+    table = o.permutation(32, 11, 3001)[:16].copy()
+    chunks = [list(prompt[:16]), list(prompt[16:37])] + [[int(t)] for t in o.fill_tokens(5, 11, 3002, 49152)]
+    _run_sequence(model, backend, 16, chunks, table)
+
+
+def test_batched_rows_match_single_sequences(torch_cuda):
+    """Several sequences in one forward call == each appended alone."""
+    cfg = smollm_config(layers=2, context=256)
+    model = OracleModel(cfg, seed=5)
+    bt, max_blocks = 16, 64
+    backend = HipBackend(cfg, block_tokens=bt, max_blocks=max_blocks, max_sequences=8)
+    upload_model(backend, model)
+    o = Oracle()
+    perm = o.permutation(max_blocks, 5, 4000)
+    n = pool_elements(cfg, bt, max_blocks)
+    keys = np.zeros(n, dtype=np.float32)
+    values = np.zeros(n, dtype=np.float32)
+    lengths = [20, 3, 33, 16, 1, 7]
+    tables = [perm[8 * i: 8 * i + 8].copy() for i in range(len(lengths))]
+    used = [0] * len(lengths)
+    for i, t in enumerate(tables):
+        backend.table_write(i, 0, t)
+    for step in range(3):
+        chunks = [list(o.fill_tokens(lengths[i] if step == 0 else 1, 5, 5000 + 10 * step + i, 49152))
+                  for i in range(len(lengths))]
+        want = [model.append(keys, values, bt, tables[i], used[i], chunks[i]) for i in range(len(lengths))]
+        steps = [(i, used[i], len(chunks[i])) for i in range(len(lengths))]
+        am, got = backend.forward(steps, [t for ch in chunks for t in ch])
+        for i in range(len(lengths)):
+            _logits_match(got[i], want[i])
+            assert am[i] == int(np.argmax(want[i]))
+            used[i] += len(chunks[i])

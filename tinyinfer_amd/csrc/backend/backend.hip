@@ -1,0 +1,521 @@
+// C ABI of the MI355X device backend (include/mp_hip.h).
+//
+// One context owns: the resident weights (Q|K|V concatenated per layer into a
+// [hidden, q+2kv] matrix, everything else as the reference stores it, plus a
+// [hidden, vocab] head), the K and V page pools, the block-table arena, the
+// RoPE cos/sin table, a grow-only workspace and one stream. It corresponds to
+// the device half of CudaRunner (miniprefix/src/backend/cuda/llama_runner.cu:51-186)
+// and its resources (resources.cpp:13-45).
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "../../../include/mp_hip.h"
+#include "kernels.h"
+
+namespace {
+
+using mphip::Epilogue;
+
+struct DeviceBuffer {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+};
+
+}  // namespace
+
+struct mp_hip {
+    mp_model_desc model{};
+    mp_kv_desc kv{};
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::string error;
+    mp_hip_counters stats{};
+    // weights
+    float* embedding = nullptr;      // [vocab, hidden]
+    float* head = nullptr;           // [hidden, vocab]
+    float* final_norm = nullptr;     // [hidden]
+    std::vector<float*> input_norm, post_norm, qkv, o, gate, up, down;
+    std::vector<unsigned char> uploaded;  // per (layer, slot) + model tensors
+    // paged KV
+    float* keys = nullptr;
+    float* values = nullptr;
+    size_t pool_elements = 0;
+    int32_t* tables = nullptr;
+    // RoPE
+    float* cos_table = nullptr;
+    float* sin_table = nullptr;
+    // workspace (grow-only, sized in rows)
+    int workspace_rows = 0;
+    int workspace_seqs = 0;
+    float *x = nullptr, *xn = nullptr, *qkv_out = nullptr, *ctx = nullptr, *ffn = nullptr;
+    float *last = nullptr, *logits = nullptr, *scratch = nullptr;
+    size_t scratch_floats = 0;
+    int32_t* meta = nullptr;  // tokens | row_seq | row_pos | seq_slot | seq_last_row
+    int32_t* results = nullptr;  // argmax[seqs] | nonfinite
+    std::vector<int32_t> host_meta;
+    std::vector<void*> allocations;
+};
+
+namespace {
+
+int fail(mp_hip* h, int status, const std::string& message) {
+    if (h) h->error = message;
+    return status;
+}
+
+int check(mp_hip* h, hipError_t e, const char* what) {
+    if (e == hipSuccess) return MP_OK;
+    return fail(h, e == hipErrorOutOfMemory ? MP_OUT_OF_MEMORY : MP_DEVICE_ERROR,
+                std::string(what) + ": " + hipGetErrorString(e));
+}
+
+int device_alloc(mp_hip* h, void** out, size_t bytes, const char* what) {
+    void* p = nullptr;
+    const hipError_t e = hipMalloc(&p, bytes ? bytes : 4);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return check(h, e, what);
+    }
+    h->allocations.push_back(p);
+    ++h->stats.device_allocations;
+    *out = p;
+    return MP_OK;
+}
+
+void device_free(mp_hip* h, void* p) {
+    if (!p) return;
+    for (auto& a : h->allocations)
+        if (a == p) {
+            a = nullptr;
+            break;
+        }
+    (void)hipFree(p);
+}
+
+int kv_width(const mp_model_desc& m) { return m.kv_heads * (m.hidden / m.heads); }
+int qkv_width(const mp_model_desc& m) { return m.hidden + 2 * kv_width(m); }
+
+bool valid_model(const mp_model_desc& c) {
+    // ModelConfig::validate (miniprefix/src/model/model.cpp:9-15), minus eos.
+    return !(c.layers < 1 || c.layers > 128 || c.hidden < 2 || c.hidden > 8192 ||
+             c.intermediate < 1 || c.intermediate > 65536 || c.heads < 1 || c.kv_heads < 1 ||
+             c.hidden % c.heads || c.heads % c.kv_heads || (c.hidden / c.heads) % 2 ||
+             c.hidden / c.heads > 256 || c.vocabulary < 2 || c.vocabulary > 262144 ||
+             c.context < 1 || c.context > 131072 || !std::isfinite(c.rms_epsilon) ||
+             c.rms_epsilon <= 0 || !std::isfinite(c.rope_theta) || c.rope_theta <= 1);
+}
+
+size_t tensor_elements(const mp_model_desc& c, int layer, int slot) {
+    const size_t hd = c.hidden, kv = kv_width(c), in = c.intermediate;
+    if (layer < 0) {
+        if (slot == MP_TENSOR_EMBEDDING) return (size_t)c.vocabulary * hd;
+        if (slot == MP_TENSOR_FINAL_NORM) return hd;
+        if (slot == MP_TENSOR_LM_HEAD) return c.tied ? 0 : hd * c.vocabulary;
+        return 0;
+    }
+    switch (slot) {
+    case MP_TENSOR_INPUT_NORM: case MP_TENSOR_POST_NORM: return hd;
+    case MP_TENSOR_Q: case MP_TENSOR_O: return hd * hd;
+    case MP_TENSOR_K: case MP_TENSOR_V: return hd * kv;
+    case MP_TENSOR_GATE: case MP_TENSOR_UP: case MP_TENSOR_DOWN: return hd * in;
+    default: return 0;
+    }
+}
+
+int uploaded_index(const mp_model_desc& c, int layer, int slot) {
+    if (layer >= 0) return layer * 9 + slot;
+    return c.layers * 9 + (slot - MP_TENSOR_EMBEDDING);
+}
+
+// RoPE angles exactly as llama_runner.cpp:19-20 evaluates them (float pow,
+// cos, sin of the host C library), for positions 0..context-1.
+void rope_tables(const mp_model_desc& c, std::vector<float>& cs, std::vector<float>& sn) {
+    const int dim = c.hidden / c.heads, half = dim / 2;
+    cs.resize((size_t)c.context * half);
+    sn.resize(cs.size());
+    for (int p = 0; p < c.context; ++p)
+        for (int d = 0; d < half; ++d) {
+            const float angle = float(p) / std::pow(c.rope_theta, float(2 * d) / float(dim));
+            cs[(size_t)p * half + d] = std::cos(angle);
+            sn[(size_t)p * half + d] = std::sin(angle);
+        }
+}
+
+int ensure_workspace(mp_hip* h, int rows, int seqs, int max_length) {
+    const mp_model_desc& c = h->model;
+    const int group = c.heads / c.kv_heads;
+    const size_t need_scratch =
+        (size_t)group * (size_t)((max_length + 3) & ~3) > (size_t)mphip::kAttentionLdsScores
+            ? (size_t)rows * c.kv_heads * group * (size_t)((max_length + 3) & ~3)
+            : 0;
+    if (rows <= h->workspace_rows && seqs <= h->workspace_seqs && need_scratch <= h->scratch_floats)
+        return MP_OK;
+    int status = mp_hip_sync(h);
+    if (status) return status;
+    const int R = rows > h->workspace_rows ? rows : h->workspace_rows;
+    const int S = seqs > h->workspace_seqs ? seqs : h->workspace_seqs;
+    for (void* p : {(void*)h->x, (void*)h->xn, (void*)h->qkv_out, (void*)h->ctx, (void*)h->ffn,
+                    (void*)h->last, (void*)h->logits, (void*)h->meta, (void*)h->results})
+        device_free(h, p);
+    h->x = h->xn = h->qkv_out = h->ctx = h->ffn = h->last = h->logits = nullptr;
+    h->meta = h->results = nullptr;
+    h->workspace_rows = h->workspace_seqs = 0;
+    const size_t hd = c.hidden;
+    struct Item { void** p; size_t bytes; };
+    const Item items[] = {
+        {(void**)&h->x, sizeof(float) * R * hd},
+        {(void**)&h->xn, sizeof(float) * R * hd},
+        {(void**)&h->qkv_out, sizeof(float) * R * (size_t)qkv_width(c)},
+        {(void**)&h->ctx, sizeof(float) * R * hd},
+        {(void**)&h->ffn, sizeof(float) * R * (size_t)c.intermediate},
+        {(void**)&h->last, sizeof(float) * S * hd},
+        {(void**)&h->logits, sizeof(float) * S * (size_t)c.vocabulary},
+        {(void**)&h->meta, sizeof(int32_t) * (3 * (size_t)R + 2 * (size_t)S)},
+        {(void**)&h->results, sizeof(int32_t) * ((size_t)S + 1)},
+    };
+    size_t total = 0;
+    for (const auto& it : items) {
+        if ((status = device_alloc(h, it.p, it.bytes, "allocate workspace"))) return status;
+        total += it.bytes;
+    }
+    if (need_scratch > h->scratch_floats) {
+        device_free(h, h->scratch);
+        h->scratch = nullptr;
+        h->scratch_floats = 0;
+        if ((status = device_alloc(h, (void**)&h->scratch, sizeof(float) * need_scratch,
+                                   "allocate attention scratch")))
+            return status;
+        h->scratch_floats = need_scratch;
+    }
+    h->workspace_rows = R;
+    h->workspace_seqs = S;
+    h->stats.device_workspace_bytes = total + sizeof(float) * h->scratch_floats;
+    return MP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mp_hip_create(const mp_model_desc* model, const mp_kv_desc* kv, mp_hip** out) {
+    if (!model || !kv || !out) return MP_INVALID_ARGUMENT;
+    *out = nullptr;
+    mp_hip* h = new (std::nothrow) mp_hip();
+    if (!h) return MP_OUT_OF_MEMORY;
+    h->model = *model;
+    h->kv = *kv;
+    const mp_model_desc& c = h->model;
+    if (!valid_model(c) || kv->block_tokens < 1 || kv->max_blocks < 1 || kv->max_sequences < 1 ||
+        kv->max_sequence_blocks < 1) {
+        delete h;
+        return MP_INVALID_ARGUMENT;
+    }
+    int status = check(h, hipGetDevice(&h->device), "get device");
+    if (!status) status = check(h, hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking), "create model stream");
+    const size_t hd = c.hidden;
+    h->input_norm.assign(c.layers, nullptr);
+    h->post_norm.assign(c.layers, nullptr);
+    h->qkv.assign(c.layers, nullptr);
+    h->o.assign(c.layers, nullptr);
+    h->gate.assign(c.layers, nullptr);
+    h->up.assign(c.layers, nullptr);
+    h->down.assign(c.layers, nullptr);
+    h->uploaded.assign((size_t)c.layers * 9 + 3, 0);
+    if (c.tied) h->uploaded[(size_t)c.layers * 9 + 2] = 1;
+    auto alloc_weights = [&](float** p, size_t elements) {
+        if (status) return;
+        status = device_alloc(h, (void**)p, elements * sizeof(float), "allocate weights");
+        if (!status) h->stats.device_weight_bytes += elements * sizeof(float);
+    };
+    alloc_weights(&h->embedding, (size_t)c.vocabulary * hd);
+    alloc_weights(&h->head, (size_t)c.vocabulary * hd);
+    alloc_weights(&h->final_norm, hd);
+    for (int l = 0; l < c.layers; ++l) {
+        alloc_weights(&h->input_norm[l], hd);
+        alloc_weights(&h->post_norm[l], hd);
+        alloc_weights(&h->qkv[l], hd * qkv_width(c));
+        alloc_weights(&h->o[l], hd * hd);
+        alloc_weights(&h->gate[l], hd * c.intermediate);
+        alloc_weights(&h->up[l], hd * c.intermediate);
+        alloc_weights(&h->down[l], hd * c.intermediate);
+    }
+    // Pools: [block][layer][slot][kv_width] (miniprefix/src/kv/paged_kv.cpp:53-56).
+    h->pool_elements = (size_t)kv->max_blocks * c.layers * kv->block_tokens * kv_width(c);
+    if (!status) status = device_alloc(h, (void**)&h->keys, h->pool_elements * sizeof(float), "allocate keys");
+    if (!status) status = device_alloc(h, (void**)&h->values, h->pool_elements * sizeof(float), "allocate values");
+    if (!status) status = check(h, hipMemsetAsync(h->keys, 0, h->pool_elements * sizeof(float), h->stream), "clear keys");
+    if (!status) status = check(h, hipMemsetAsync(h->values, 0, h->pool_elements * sizeof(float), h->stream), "clear values");
+    h->stats.kv_pool_bytes = 2 * h->pool_elements * sizeof(float);
+    const size_t table_bytes = sizeof(int32_t) * (size_t)kv->max_sequences * kv->max_sequence_blocks;
+    if (!status) status = device_alloc(h, (void**)&h->tables, table_bytes, "allocate block tables");
+    if (!status) status = check(h, hipMemsetAsync(h->tables, 0, table_bytes, h->stream), "clear block tables");
+    h->stats.block_table_device_bytes = table_bytes;
+    if (!status) {
+        std::vector<float> cs, sn;
+        rope_tables(c, cs, sn);
+        status = device_alloc(h, (void**)&h->cos_table, cs.size() * sizeof(float), "allocate rope table");
+        if (!status) status = device_alloc(h, (void**)&h->sin_table, sn.size() * sizeof(float), "allocate rope table");
+        if (!status) status = check(h, hipMemcpyAsync(h->cos_table, cs.data(), cs.size() * sizeof(float), hipMemcpyHostToDevice, h->stream), "upload rope table");
+        if (!status) status = check(h, hipMemcpyAsync(h->sin_table, sn.data(), sn.size() * sizeof(float), hipMemcpyHostToDevice, h->stream), "upload rope table");
+        if (!status) status = check(h, hipStreamSynchronize(h->stream), "rope table completion");
+    }
+    if (status) {
+        const int s = status;
+        std::fprintf(stderr, "mp_hip_create: %s\n", h->error.c_str());
+        mp_hip_destroy(h);
+        return s;
+    }
+    *out = h;
+    return MP_OK;
+}
+
+int mp_hip_destroy(mp_hip* h) {
+    if (!h) return MP_OK;
+    if (h->stream) (void)hipStreamSynchronize(h->stream);
+    for (void* p : h->allocations)
+        if (p) (void)hipFree(p);
+    if (h->stream) (void)hipStreamDestroy(h->stream);
+    delete h;
+    return MP_OK;
+}
+
+const char* mp_hip_last_error(const mp_hip* h) { return h ? h->error.c_str() : "null context"; }
+
+int mp_hip_upload_tensor(mp_hip* h, int32_t layer, int32_t slot, const float* data, size_t count) {
+    if (!h || !data) return fail(h, MP_INVALID_ARGUMENT, "null tensor");
+    const mp_model_desc& c = h->model;
+    if (layer < -1 || layer >= c.layers) return fail(h, MP_INVALID_ARGUMENT, "invalid tensor layer");
+    if ((layer >= 0 && (slot < 0 || slot > MP_TENSOR_DOWN)) ||
+        (layer < 0 && (slot < MP_TENSOR_EMBEDDING || slot > MP_TENSOR_LM_HEAD)))
+        return fail(h, MP_INVALID_ARGUMENT, "invalid tensor slot");
+    const size_t expected = tensor_elements(c, layer, slot);
+    if (!expected || count != expected) return fail(h, MP_INVALID_ARGUMENT, "tensor shape mismatch");
+    for (size_t i = 0; i < count; ++i)
+        if (!std::isfinite(data[i])) return fail(h, MP_INVALID_ARGUMENT, "nonfinite weights");
+    const size_t bytes = count * sizeof(float);
+    const size_t hd = c.hidden, kvw = kv_width(c), qw = qkv_width(c);
+    hipError_t e = hipSuccess;
+    const hipMemcpyKind h2d = hipMemcpyHostToDevice;
+    if (layer < 0) {
+        if (slot == MP_TENSOR_EMBEDDING) {
+            e = hipMemcpyAsync(h->embedding, data, bytes, h2d, h->stream);
+            // Tied head: the [hidden, vocab] transpose of the embedding, read
+            // with the same sequential-k order as the reference's packed
+            // transposed RHS (matmul_kernel.cpp:172-189).
+            if (e == hipSuccess && c.tied)
+                e = mphip::launch_transpose(h->stream, h->embedding, h->head, c.vocabulary, c.hidden);
+        } else if (slot == MP_TENSOR_FINAL_NORM) {
+            e = hipMemcpyAsync(h->final_norm, data, bytes, h2d, h->stream);
+        } else {
+            e = hipMemcpyAsync(h->head, data, bytes, h2d, h->stream);
+        }
+    } else {
+        switch (slot) {
+        case MP_TENSOR_INPUT_NORM: e = hipMemcpyAsync(h->input_norm[layer], data, bytes, h2d, h->stream); break;
+        case MP_TENSOR_POST_NORM: e = hipMemcpyAsync(h->post_norm[layer], data, bytes, h2d, h->stream); break;
+        case MP_TENSOR_Q:
+            e = hipMemcpy2DAsync(h->qkv[layer], qw * 4, data, hd * 4, hd * 4, hd, h2d, h->stream);
+            break;
+        case MP_TENSOR_K:
+            e = hipMemcpy2DAsync(h->qkv[layer] + hd, qw * 4, data, kvw * 4, kvw * 4, hd, h2d, h->stream);
+            break;
+        case MP_TENSOR_V:
+            e = hipMemcpy2DAsync(h->qkv[layer] + hd + kvw, qw * 4, data, kvw * 4, kvw * 4, hd, h2d, h->stream);
+            break;
+        case MP_TENSOR_O: e = hipMemcpyAsync(h->o[layer], data, bytes, h2d, h->stream); break;
+        case MP_TENSOR_GATE: e = hipMemcpyAsync(h->gate[layer], data, bytes, h2d, h->stream); break;
+        case MP_TENSOR_UP: e = hipMemcpyAsync(h->up[layer], data, bytes, h2d, h->stream); break;
+        case MP_TENSOR_DOWN: e = hipMemcpyAsync(h->down[layer], data, bytes, h2d, h->stream); break;
+        }
+    }
+    int status = check(h, e, "upload weights");
+    if (!status) status = check(h, hipStreamSynchronize(h->stream), "weight upload completion");
+    if (status) return status;
+    h->uploaded[uploaded_index(c, layer, slot)] = 1;
+    h->stats.weight_uploaded_bytes += bytes;
+    return MP_OK;
+}
+
+int mp_hip_ready(const mp_hip* h, int32_t* ready) {
+    if (!h || !ready) return MP_INVALID_ARGUMENT;
+    *ready = 1;
+    for (unsigned char u : h->uploaded)
+        if (!u) *ready = 0;
+    return MP_OK;
+}
+
+int mp_hip_table_write(mp_hip* h, int32_t slot, int32_t first, const int32_t* blocks, int32_t count) {
+    if (!h) return MP_INVALID_ARGUMENT;
+    if (slot < 0 || slot >= h->kv.max_sequences || first < 0 || count < 0 ||
+        (int64_t)first + count > h->kv.max_sequence_blocks || (count && !blocks))
+        return fail(h, MP_INVALID_ARGUMENT, "invalid block table write");
+    for (int32_t i = 0; i < count; ++i)
+        if (blocks[i] < 0 || blocks[i] >= h->kv.max_blocks)
+            return fail(h, MP_INVALID_ARGUMENT, "block id out of range");
+    if (!count) return MP_OK;
+    int32_t* dst = h->tables + (size_t)slot * h->kv.max_sequence_blocks + first;
+    const int status = check(h, hipMemcpyAsync(dst, blocks, sizeof(int32_t) * count,
+                                               hipMemcpyHostToDevice, h->stream),
+                             "upload block table entries");
+    if (!status) h->stats.block_table_uploaded_bytes += sizeof(int32_t) * count;
+    return status;
+}
+
+int mp_hip_copy_tail(mp_hip* h, const mp_tail_region* r) {
+    if (!h || !r) return MP_INVALID_ARGUMENT;
+    if (!r->rows || !r->width) return MP_OK;
+    const uint64_t span = (r->rows - 1) * r->pitch + r->width;
+    if (r->width > r->pitch || r->destination + span > h->pool_elements ||
+        r->source + span > h->pool_elements)
+        return fail(h, MP_INVALID_ARGUMENT, "tail copy region out of range");
+    const int status = check(h, mphip::launch_copy_region(h->stream, h->keys, h->values,
+                                                          r->destination, r->source, r->pitch,
+                                                          r->width, r->rows),
+                             "COW copy");
+    if (!status) {
+        ++h->stats.cow_copies;
+        h->stats.cow_bytes += 2 * r->width * r->rows * sizeof(float);
+    }
+    return status;
+}
+
+int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int32_t* tokens,
+                   float* logits, int32_t* argmax) {
+    if (!h || !steps || nseq < 1 || !tokens || !argmax)
+        return fail(h, MP_INVALID_ARGUMENT, "invalid forward arguments");
+    const mp_model_desc& c = h->model;
+    int32_t ready = 0;
+    mp_hip_ready(h, &ready);
+    if (!ready) return fail(h, MP_INVALID_ARGUMENT, "weights not uploaded");
+    int64_t rows = 0;
+    int max_length = 1;
+    for (int s = 0; s < nseq; ++s) {
+        const mp_seq_step& st = steps[s];
+        if (st.table_slot < 0 || st.table_slot >= h->kv.max_sequences || st.count < 1 ||
+            st.used < 0 || (int64_t)st.used + st.count > c.context ||
+            ((int64_t)st.used + st.count + h->kv.block_tokens - 1) / h->kv.block_tokens >
+                h->kv.max_sequence_blocks)
+            return fail(h, MP_INVALID_ARGUMENT, "invalid sequence step");
+        rows += st.count;
+        if (st.used + st.count > max_length) max_length = st.used + st.count;
+    }
+    if (rows > (1 << 20)) return fail(h, MP_INVALID_ARGUMENT, "too many rows");
+    const int R = (int)rows;
+    for (int i = 0; i < R; ++i)
+        if (tokens[i] < 0 || tokens[i] >= c.vocabulary) return fail(h, MP_INVALID_ARGUMENT, "invalid token");
+    int status = ensure_workspace(h, R, nseq, max_length);
+    if (status) return status;
+    // Row metadata: tokens | row_seq | row_pos | seq_slot | seq_last_row.
+    auto& m = h->host_meta;
+    m.resize(3 * (size_t)R + 2 * (size_t)nseq + 1);
+    int32_t* m_tokens = m.data();
+    int32_t* m_seq = m_tokens + R;
+    int32_t* m_pos = m_seq + R;
+    int32_t* m_slot = m_pos + R;
+    int32_t* m_last = m_slot + nseq;
+    int r = 0;
+    for (int s = 0; s < nseq; ++s) {
+        for (int i = 0; i < steps[s].count; ++i, ++r) {
+            m_tokens[r] = tokens[r];
+            m_seq[r] = s;
+            m_pos[r] = steps[s].used + i;
+        }
+        m_slot[s] = steps[s].table_slot;
+        m_last[s] = r - 1;
+    }
+    status = check(h, hipMemcpyAsync(h->meta, m.data(), sizeof(int32_t) * (3 * (size_t)R + 2 * (size_t)nseq),
+                                     hipMemcpyHostToDevice, h->stream), "upload input tokens");
+    if (status) return status;
+    h->stats.token_uploaded_bytes += sizeof(int32_t) * R;
+    mphip::RowMeta meta{h->meta, h->meta + R, h->meta + 2 * (size_t)R, h->meta + 3 * (size_t)R,
+                        h->meta + 3 * (size_t)R + nseq};
+    const int dim = c.hidden / c.heads, kvw = kv_width(c), qw = qkv_width(c);
+    mphip::PagedKv kv{h->keys, h->values, h->tables, h->kv.max_sequence_blocks,
+                      c.layers, h->kv.block_tokens, kvw};
+    const size_t scratch_row = (size_t)(c.heads / c.kv_heads) * (size_t)((max_length + 3) & ~3);
+    hipStream_t s = h->stream;
+    hipError_t e = mphip::launch_embed(s, h->embedding, meta.tokens, h->x, R, c.hidden);
+    for (int l = 0; l < c.layers && e == hipSuccess; ++l) {
+        e = mphip::launch_rms(s, h->x, c.hidden, nullptr, h->input_norm[l], h->xn, c.hidden, R, c.hidden, c.rms_epsilon);
+        if (e == hipSuccess) e = mphip::launch_gemm(s, mphip::kStore, h->xn, c.hidden, R, c.hidden, h->qkv[l], nullptr, qw, qw, h->qkv_out, qw);
+        if (e == hipSuccess) e = mphip::launch_rope_append(s, h->qkv_out, qw, R, c.heads, c.kv_heads, dim, h->cos_table, h->sin_table, meta, kv, l);
+        if (e == hipSuccess) e = mphip::launch_attention(s, h->qkv_out, qw, R, c.heads, c.kv_heads, dim, meta, kv, l, h->ctx, c.hidden, h->scratch, scratch_row);
+        if (e == hipSuccess) e = mphip::launch_gemm(s, mphip::kResidual, h->ctx, c.hidden, R, c.hidden, h->o[l], nullptr, c.hidden, c.hidden, h->x, c.hidden);
+        if (e == hipSuccess) e = mphip::launch_rms(s, h->x, c.hidden, nullptr, h->post_norm[l], h->xn, c.hidden, R, c.hidden, c.rms_epsilon);
+        if (e == hipSuccess) e = mphip::launch_gemm(s, mphip::kSwiglu, h->xn, c.hidden, R, c.hidden, h->gate[l], h->up[l], c.intermediate, c.intermediate, h->ffn, c.intermediate);
+        if (e == hipSuccess) e = mphip::launch_gemm(s, mphip::kResidual, h->ffn, c.intermediate, R, c.intermediate, h->down[l], nullptr, c.hidden, c.hidden, h->x, c.hidden);
+    }
+    if (e == hipSuccess) e = mphip::launch_rms(s, h->x, c.hidden, meta.seq_last_row, h->final_norm, h->last, c.hidden, nseq, c.hidden, c.rms_epsilon);
+    if (e == hipSuccess) e = mphip::launch_gemm(s, mphip::kStore, h->last, c.hidden, nseq, c.hidden, h->head, nullptr, c.vocabulary, c.vocabulary, h->logits, c.vocabulary);
+    if (e == hipSuccess) e = hipMemsetAsync(h->results + nseq, 0, sizeof(int32_t), s);
+    if (e == hipSuccess) e = mphip::launch_argmax(s, h->logits, nseq, c.vocabulary, h->results, h->results + nseq);
+    if ((status = check(h, e, "model kernel launch"))) return status;
+    std::vector<int32_t> results((size_t)nseq + 1);
+    status = check(h, hipMemcpyAsync(results.data(), h->results, sizeof(int32_t) * (nseq + 1), hipMemcpyDeviceToHost, s), "download argmax");
+    if (!status && logits) {
+        status = check(h, hipMemcpyAsync(logits, h->logits, sizeof(float) * (size_t)nseq * c.vocabulary, hipMemcpyDeviceToHost, s), "download logits");
+        if (!status) h->stats.logits_downloaded_bytes += sizeof(float) * (size_t)nseq * c.vocabulary;
+    }
+    if (!status) status = check(h, hipStreamSynchronize(s), "model completion");
+    if (status) return status;
+    std::memcpy(argmax, results.data(), sizeof(int32_t) * nseq);
+    ++h->stats.forward_calls;
+    h->stats.forward_rows += R;
+    if (results[nseq]) return fail(h, MP_NONFINITE, "nonfinite HIP logits");
+    return MP_OK;
+}
+
+int mp_hip_paged_attention_decode(const float* q, const float* keys, const float* values,
+                                  const int32_t* table, int32_t length, int32_t layer,
+                                  int32_t layers, int32_t block_tokens, int32_t heads,
+                                  int32_t kv_heads, int32_t dim, float* out, void* stream) {
+    if (!q || !keys || !values || !table || !out || length < 1 || layer < 0 || layer >= layers ||
+        block_tokens < 1 || heads < 1 || kv_heads < 1 || heads % kv_heads || dim < 4 || dim % 4 ||
+        dim > 256 || heads / kv_heads > 8)
+        return MP_INVALID_ARGUMENT;
+    const int group = heads / kv_heads;
+    float* scratch = nullptr;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if ((size_t)group * (size_t)((length + 3) & ~3) > (size_t)mphip::kAttentionLdsScores) {
+        // Long rows keep their scores in global memory; synchronous so the
+        // temporary can be released before returning.
+        const size_t floats = (size_t)kv_heads * group * (size_t)((length + 3) & ~3);
+        if (hipMalloc(&scratch, floats * sizeof(float)) != hipSuccess) return MP_OUT_OF_MEMORY;
+    }
+    hipError_t e = mphip::launch_attention_single(s, q, keys, values, table, length, layer, layers,
+                                                  block_tokens, heads, kv_heads, dim, out, scratch);
+    if (scratch) {
+        if (e == hipSuccess) e = hipStreamSynchronize(s);
+        (void)hipFree(scratch);
+    }
+    return e == hipSuccess ? MP_OK : MP_DEVICE_ERROR;
+}
+
+int mp_hip_sync(mp_hip* h) {
+    if (!h) return MP_INVALID_ARGUMENT;
+    return check(h, hipStreamSynchronize(h->stream), "model completion");
+}
+
+int mp_hip_stats(const mp_hip* h, mp_hip_counters* out) {
+    if (!h || !out) return MP_INVALID_ARGUMENT;
+    *out = h->stats;
+    return MP_OK;
+}
+
+int mp_hip_kv_pools(const mp_hip* h, float** keys, float** values, size_t* elements) {
+    if (!h) return MP_INVALID_ARGUMENT;
+    if (keys) *keys = h->keys;
+    if (values) *values = h->values;
+    if (elements) *elements = h->pool_elements;
+    return MP_OK;
+}
+
+void* mp_hip_stream(const mp_hip* h) { return h ? (void*)h->stream : nullptr; }
+
+}  // extern "C"
