@@ -147,13 +147,16 @@ void rope_tables(const mp_model_desc& c, std::vector<float>& cs, std::vector<flo
         }
 }
 
+int score_stride(int max_length) { return (max_length + 15) & ~15; }
+int score_chunks(int max_length) { return (max_length + 255) / 256; }
+// Score rows and per-256-token chunk maxima of every (row, head).
+size_t attention_scratch_floats(const mp_model_desc& c, int rows, int max_length) {
+    return (size_t)rows * c.heads * ((size_t)score_stride(max_length) + score_chunks(max_length));
+}
+
 int ensure_workspace(mp_hip* h, int rows, int seqs, int max_length) {
     const mp_model_desc& c = h->model;
-    const int group = c.heads / c.kv_heads;
-    const size_t need_scratch =
-        (size_t)group * (size_t)((max_length + 3) & ~3) > (size_t)mphip::kAttentionLdsScores
-            ? (size_t)rows * c.kv_heads * group * (size_t)((max_length + 3) & ~3)
-            : 0;
+    const size_t need_scratch = attention_scratch_floats(c, rows, max_length);
     if (rows <= h->workspace_rows && seqs <= h->workspace_seqs && need_scratch <= h->scratch_floats)
         return MP_OK;
     int status = mp_hip_sync(h);
@@ -211,8 +214,11 @@ int mp_hip_create(const mp_model_desc* model, const mp_kv_desc* kv, mp_hip** out
     h->model = *model;
     h->kv = *kv;
     const mp_model_desc& c = h->model;
-    if (!valid_model(c) || kv->block_tokens < 1 || kv->max_blocks < 1 || kv->max_sequences < 1 ||
-        kv->max_sequence_blocks < 1) {
+    // Pages are streamed as float4 runs of tokens: the device path needs a
+    // page size that is a multiple of 4 tokens and fits one V batch buffer.
+    if (!valid_model(c) || kv->block_tokens < 4 || kv->block_tokens % 4 ||
+        kv->block_tokens * (c.hidden / c.heads) > 16384 || kv->max_blocks < 1 ||
+        kv->max_sequences < 1 || kv->max_sequence_blocks < 1 || kv->max_sequence_blocks > 2048) {
         delete h;
         return MP_INVALID_ARGUMENT;
     }
@@ -438,14 +444,15 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
     const int dim = c.hidden / c.heads, kvw = kv_width(c), qw = qkv_width(c);
     mphip::PagedKv kv{h->keys, h->values, h->tables, h->kv.max_sequence_blocks,
                       c.layers, h->kv.block_tokens, kvw};
-    const size_t scratch_row = (size_t)(c.heads / c.kv_heads) * (size_t)((max_length + 3) & ~3);
+    const mphip::AttentionScratch scratch{h->scratch, h->scratch + (size_t)R * c.heads * score_stride(max_length),
+                                          score_stride(max_length), score_chunks(max_length)};
     hipStream_t s = h->stream;
     hipError_t e = mphip::launch_embed(s, h->embedding, meta.tokens, h->x, R, c.hidden);
     for (int l = 0; l < c.layers && e == hipSuccess; ++l) {
         e = mphip::launch_rms(s, h->x, c.hidden, nullptr, h->input_norm[l], h->xn, c.hidden, R, c.hidden, c.rms_epsilon);
         if (e == hipSuccess) e = mphip::launch_gemm(s, mphip::kStore, h->xn, c.hidden, R, c.hidden, h->qkv[l], nullptr, qw, qw, h->qkv_out, qw);
         if (e == hipSuccess) e = mphip::launch_rope_append(s, h->qkv_out, qw, R, c.heads, c.kv_heads, dim, h->cos_table, h->sin_table, meta, kv, l);
-        if (e == hipSuccess) e = mphip::launch_attention(s, h->qkv_out, qw, R, c.heads, c.kv_heads, dim, meta, kv, l, h->ctx, c.hidden, h->scratch, scratch_row);
+        if (e == hipSuccess) e = mphip::launch_attention(s, h->qkv_out, qw, R, c.heads, c.kv_heads, dim, meta, kv, l, h->ctx, c.hidden, scratch);
         if (e == hipSuccess) e = mphip::launch_gemm(s, mphip::kResidual, h->ctx, c.hidden, R, c.hidden, h->o[l], nullptr, c.hidden, c.hidden, h->x, c.hidden);
         if (e == hipSuccess) e = mphip::launch_rms(s, h->x, c.hidden, nullptr, h->post_norm[l], h->xn, c.hidden, R, c.hidden, c.rms_epsilon);
         if (e == hipSuccess) e = mphip::launch_gemm(s, mphip::kSwiglu, h->xn, c.hidden, R, c.hidden, h->gate[l], h->up[l], c.intermediate, c.intermediate, h->ffn, c.intermediate);
@@ -482,10 +489,10 @@ int mp_hip_paged_attention_decode(const float* q, const float* keys, const float
     const int group = heads / kv_heads;
     float* scratch = nullptr;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    if ((size_t)group * (size_t)((length + 3) & ~3) > (size_t)mphip::kAttentionLdsScores) {
+    if ((size_t)group * (size_t)((length + 15) & ~15) > (size_t)mphip::kAttentionLdsScores) {
         // Long rows keep their scores in global memory; synchronous so the
         // temporary can be released before returning.
-        const size_t floats = (size_t)kv_heads * group * (size_t)((length + 3) & ~3);
+        const size_t floats = (size_t)kv_heads * group * (size_t)((length + 15) & ~15);
         if (hipMalloc(&scratch, floats * sizeof(float)) != hipSuccess) return MP_OUT_OF_MEMORY;
     }
     hipError_t e = mphip::launch_attention_single(s, q, keys, values, table, length, layer, layers,

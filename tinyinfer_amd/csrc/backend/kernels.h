@@ -52,21 +52,26 @@ hipError_t launch_rope_append(hipStream_t s, float* qkv, int ldqkv, int rows, in
                               const float* sin_table, const RowMeta& meta, const PagedKv& kv,
                               int layer);
 
-// Causal GQA attention, one work-group per (row, kv head), reference
-// two-pass softmax order. q rows at qkv (stride ldq); out rows stride ldo.
-// `scratch` holds score rows that do not fit in LDS (may be null when
-// every row's length is within the LDS capacity).
+// Causal GQA attention for every row in the reference two-pass softmax
+// order. q rows at qkv (stride ldq); out rows stride ldo. Scratch holds
+// rows*heads score rows of `stride` floats (max length padded to 16) and
+// rows*heads*chunks chunk maxima (chunks = ceil(max length / 256)).
+struct AttentionScratch {
+    float* scores;
+    float* chunk_max;
+    int stride;
+    int chunks;
+};
 hipError_t launch_attention(hipStream_t s, const float* qkv, int ldq, int rows, int heads,
                             int kv_heads, int dim, const RowMeta& meta, const PagedKv& kv,
-                            int layer, float* out, int ldo, float* scratch,
-                            size_t scratch_row_floats);
+                            int layer, float* out, int ldo, const AttentionScratch& scratch);
 // Stand-alone single-row variant over a caller page table.
 hipError_t launch_attention_single(hipStream_t s, const float* q, const float* keys,
                                    const float* values, const int32_t* table, int length,
                                    int layer, int layers, int block_tokens, int heads,
                                    int kv_heads, int dim, float* out, float* scratch);
 // Score floats per row that fit in LDS.
-constexpr int kAttentionLdsScores = 12288;
+constexpr int kAttentionLdsScores = 10240;
 
 // First index of the maximum of each row of logits (std::max_element), and
 // a flag set to 1 when any value is not finite.

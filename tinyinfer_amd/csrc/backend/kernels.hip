@@ -24,12 +24,68 @@ __device__ __forceinline__ int xcd_tile(int block, int tiles) {
     return xcd * q + (xcd < rem ? xcd : rem) + i;
 }
 
+// Zeroes a loaded value without a select on the load itself: selects of a
+// load are turned into exec-masked branches by the backend, which then
+// drains every outstanding load at the branch. The mask is all ones or 0.
+__device__ __forceinline__ float keep_if(float v, uint32_t mask) {
+    return __uint_as_float(__float_as_uint(v) & mask);
+}
+__device__ __forceinline__ float4 keep_if(float4 v, uint32_t mask) {
+    return make_float4(keep_if(v.x, mask), keep_if(v.y, mask), keep_if(v.z, mask), keep_if(v.w, mask));
+}
+__device__ __forceinline__ uint32_t mask_of(bool in) { return in ? 0xffffffffu : 0u; }
+
 __global__ void embed_kernel(const float* __restrict__ embedding, const int32_t* __restrict__ tokens,
                              float* __restrict__ x, int hidden) {
     const int r = blockIdx.x;
     const float* src = embedding + (size_t)tokens[r] * hidden;
     float* dst = x + (size_t)r * hidden;
     for (int i = threadIdx.x; i < hidden; i += blockDim.x) dst[i] = src[i];
+}
+
+// Sequential float sum of n values (n a multiple of 4, 16-byte aligned) in
+// the calling lane, in index order, starting from `sum`. Two blocks of
+// sixteen ping-pong: one is read while the other is added.
+__device__ __forceinline__ void sum_block(const float4 (&a)[4], float& sum) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        sum = sum + a[j].x;
+        sum = sum + a[j].y;
+        sum = sum + a[j].z;
+        sum = sum + a[j].w;
+    }
+}
+
+__device__ __forceinline__ float sequential_sum(const float* v, int n, float sum = 0.0f) {
+    const float4* v4 = reinterpret_cast<const float4*>(v);
+    const int n4 = n / 4;
+    int i = 0;
+    if (n4 >= 4) {
+        float4 a[4], b[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) a[j] = v4[j];
+        for (; i + 8 <= n4; i += 8) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) b[j] = v4[i + 4 + j];
+            sum_block(a, sum);
+            const int in = min(i + 8, n4 - 4);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) a[j] = v4[in + j];
+            sum_block(b, sum);
+        }
+        if (i + 4 <= n4) {  // `a` holds the block at i
+            sum_block(a, sum);
+            i += 4;
+        }
+    }
+    for (; i < n4; ++i) {
+        const float4 a = v4[i];
+        sum = sum + a.x;
+        sum = sum + a.y;
+        sum = sum + a.z;
+        sum = sum + a.w;
+    }
+    return sum;
 }
 
 // One wave per row. Squares are formed in parallel (each is a single
@@ -44,24 +100,14 @@ __global__ __launch_bounds__(64) void rms_kernel(const float* __restrict__ x, in
     __shared__ float scale_shared;
     const int r = blockIdx.x;
     const float* xr = x + (size_t)(row_map ? row_map[r] : r) * ldx;
-    for (int i = threadIdx.x; i < width; i += kWave) {
-        const float v = xr[i];
+    const int padded = (width + 3) & ~3;
+    for (int i = threadIdx.x; i < padded; i += kWave) {
+        const float v = i < width ? xr[i] : 0.0f;
         squares[i] = v * v;
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        float sum = 0;
-        int d = 0;
-        for (; d + 4 <= width; d += 4) {
-            const float4 v = *reinterpret_cast<const float4*>(squares + d);
-            sum = sum + v.x;
-            sum = sum + v.y;
-            sum = sum + v.z;
-            sum = sum + v.w;
-        }
-        for (; d < width; ++d) sum = sum + squares[d];
-        scale_shared = 1.0f / sqrtf(sum / (float)width + eps);
-    }
+    // Zero padding leaves the non-negative running sum unchanged.
+    if (threadIdx.x == 0) scale_shared = 1.0f / sqrtf(sequential_sum(squares, padded) / (float)width + eps);
     __syncthreads();
     const float scale = scale_shared;
     float* o = out + (size_t)r * ldo;
@@ -80,13 +126,84 @@ __device__ __forceinline__ void store_result(float* out, float acc, float acc2) 
     }
 }
 
+// acc += x[k]*w[k] for k = 0..n-1 in order (and acc2 with u when DUAL),
+// multiply and add rounded separately. x, w and u live in LDS; w and u are
+// strided by STRIDE floats (0: by `runtime_stride`). Two 16-step register
+// blocks ping-pong: one is read from LDS while the other is summed, with no
+// register copies between them.
+template <bool DUAL>
+struct ChainBlock {
+    float4 x[4];
+    float w[16];
+    float u[DUAL ? 16 : 1];
+};
+
+template <bool DUAL>
+__device__ __forceinline__ void chain_load(ChainBlock<DUAL>& b, const float* x, const float* w,
+                                           const float* u, int k, int stride) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) b.x[j] = reinterpret_cast<const float4*>(x + k)[j];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        b.w[j] = w[(k + j) * stride];
+        if (DUAL) b.u[j] = u[(k + j) * stride];
+    }
+}
+
+template <bool DUAL>
+__device__ __forceinline__ void chain_sum(const ChainBlock<DUAL>& b, float& acc, float& acc2) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        acc = acc + b.x[j].x * b.w[4 * j + 0];
+        acc = acc + b.x[j].y * b.w[4 * j + 1];
+        acc = acc + b.x[j].z * b.w[4 * j + 2];
+        acc = acc + b.x[j].w * b.w[4 * j + 3];
+        if (DUAL) {
+            acc2 = acc2 + b.x[j].x * b.u[4 * j + 0];
+            acc2 = acc2 + b.x[j].y * b.u[4 * j + 1];
+            acc2 = acc2 + b.x[j].z * b.u[4 * j + 2];
+            acc2 = acc2 + b.x[j].w * b.u[4 * j + 3];
+        }
+    }
+}
+
+template <bool DUAL, int STRIDE>
+__device__ __forceinline__ void chain_dot(const float* x, const float* w, const float* u, int n,
+                                          float& acc, float& acc2, int runtime_stride = 0) {
+    const int stride = STRIDE ? STRIDE : runtime_stride;
+    int k = 0;
+    if (n >= 16) {
+        ChainBlock<DUAL> a, b;
+        chain_load(a, x, w, u, 0, stride);
+        for (; k + 32 <= n; k += 32) {
+            chain_load(b, x, w, u, k + 16, stride);
+            chain_sum(a, acc, acc2);
+            // Next `a`; on the last pass any aligned in-range block is read and
+            // left unused.
+            chain_load(a, x, w, u, min(k + 32, (n - 16) & ~3), stride);
+            chain_sum(b, acc, acc2);
+        }
+        if (k + 16 <= n) {  // `a` holds the block at k
+            chain_sum(a, acc, acc2);
+            k += 16;
+        }
+    }
+    for (; k < n; ++k) {
+        acc = acc + x[k] * w[k * stride];
+        if (DUAL) acc2 = acc2 + x[k] * u[k * stride];
+    }
+}
+
 // Few rows (decode of one to four sequences): 16 columns per work-group so
 // that even a 576-column projection spreads over 36 CUs. All four waves
-// stage a K-chunk of the 16-column weight slab into LDS with coalesced
-// loads; lanes (row, column) of wave 0 then walk k in order.
+// stage a K-chunk of the 16-column weight slab (and of x) into LDS; the
+// next chunk's loads are issued before the current chunk is summed. Lanes
+// (row, column) of wave 0 walk k in order.
 constexpr int kSmallColumns = 16;
 constexpr int kSmallRows = 4;
 constexpr int kSmallChunk = 384;
+constexpr int kSmallWLoads = kSmallChunk * kSmallColumns / 256;  // per thread per matrix
+constexpr int kSmallXLoads = kSmallRows * kSmallChunk / 256;
 
 template <int EPI>
 __global__ __launch_bounds__(256) void gemm_small_kernel(const float* __restrict__ x, int ldx,
@@ -95,65 +212,80 @@ __global__ __launch_bounds__(256) void gemm_small_kernel(const float* __restrict
                                                          const float* __restrict__ w2,
                                                          int columns, int ldw, float* out, int ldo,
                                                          int tiles) {
+    constexpr bool kDual = EPI == kSwiglu;
     __shared__ float xs[kSmallRows * kSmallChunk];
     __shared__ float ws[kSmallChunk * kSmallColumns];
-    __shared__ float ws2[EPI == kSwiglu ? kSmallChunk * kSmallColumns : 1];
+    __shared__ float ws2[kDual ? kSmallChunk * kSmallColumns : 1];
     const int tid = threadIdx.x;
     const int n0 = xcd_tile(blockIdx.x, tiles) * kSmallColumns;
     const int r = tid / kSmallColumns, c = tid % kSmallColumns;
     const int n = n0 + c;
+    float wreg[kSmallWLoads], ureg[kDual ? kSmallWLoads : 1], xreg[kSmallXLoads];
+    // Issue: raw loads from clamped in-range addresses (masked on commit).
+    auto issue = [&](int k0) {
+        const int kc = min(kSmallChunk, inner - k0);
+#pragma unroll
+        for (int j = 0; j < kSmallWLoads; ++j) {
+            const int e = tid + j * 256;
+            const int kk = e / kSmallColumns, cc = e % kSmallColumns;
+            const bool in = kk < kc && n0 + cc < columns;
+            const size_t off = in ? (size_t)(k0 + kk) * ldw + n0 + cc : 0;
+            wreg[j] = w[off];
+            if (kDual) ureg[j] = w2[off];
+        }
+#pragma unroll
+        for (int j = 0; j < kSmallXLoads; ++j) {
+            const int e = tid + j * 256;
+            const int rr = e / kSmallChunk, kk = e % kSmallChunk;
+            const bool in = rr < rows && kk < kc;
+            xreg[j] = x[in ? (size_t)rr * ldx + k0 + kk : 0];
+        }
+    };
+    auto commit = [&](int k0) {
+        const int kc = min(kSmallChunk, inner - k0);
+#pragma unroll
+        for (int j = 0; j < kSmallWLoads; ++j) {
+            const int e = tid + j * 256;
+            const int kk = e / kSmallColumns, cc = e % kSmallColumns;
+            const uint32_t m = mask_of(kk < kc && n0 + cc < columns);
+            ws[e] = keep_if(wreg[j], m);
+            if (kDual) ws2[e] = keep_if(ureg[j], m);
+        }
+#pragma unroll
+        for (int j = 0; j < kSmallXLoads; ++j) {
+            const int e = tid + j * 256;
+            const int rr = e / kSmallChunk, kk = e % kSmallChunk;
+            xs[e] = keep_if(xreg[j], mask_of(rr < rows && kk < kc));
+        }
+    };
     float acc = 0.0f, acc2 = 0.0f;
+    issue(0);
     for (int k0 = 0; k0 < inner; k0 += kSmallChunk) {
         const int kc = min(kSmallChunk, inner - k0);
-        for (int i = tid; i < rows * kc; i += 256) {
-            const int rr = i / kc, kk = i - rr * kc;
-            xs[rr * kSmallChunk + kk] = x[(size_t)rr * ldx + k0 + kk];
-        }
-        for (int i = tid; i < kc * kSmallColumns; i += 256) {
-            const int kk = i / kSmallColumns, cc = i % kSmallColumns;
-            const bool in = n0 + cc < columns;
-            const size_t off = (size_t)(k0 + kk) * ldw + n0 + cc;
-            ws[i] = in ? w[off] : 0.0f;
-            if (EPI == kSwiglu) ws2[i] = in ? w2[off] : 0.0f;
-        }
+        commit(k0);
+        if (k0 + kSmallChunk < inner) issue(k0 + kSmallChunk);
         __syncthreads();
-        if (r < rows) {
-            const float* xr = xs + r * kSmallChunk;
-            int k = 0;
-            for (; k + 4 <= kc; k += 4) {
-                const float4 xv = *reinterpret_cast<const float4*>(xr + k);
-                const float* wk = ws + k * kSmallColumns + c;
-                acc = acc + xv.x * wk[0];
-                acc = acc + xv.y * wk[kSmallColumns];
-                acc = acc + xv.z * wk[2 * kSmallColumns];
-                acc = acc + xv.w * wk[3 * kSmallColumns];
-                if (EPI == kSwiglu) {
-                    const float* uk = ws2 + k * kSmallColumns + c;
-                    acc2 = acc2 + xv.x * uk[0];
-                    acc2 = acc2 + xv.y * uk[kSmallColumns];
-                    acc2 = acc2 + xv.z * uk[2 * kSmallColumns];
-                    acc2 = acc2 + xv.w * uk[3 * kSmallColumns];
-                }
-            }
-            for (; k < kc; ++k) {
-                acc = acc + xr[k] * ws[k * kSmallColumns + c];
-                if (EPI == kSwiglu) acc2 = acc2 + xr[k] * ws2[k * kSmallColumns + c];
-            }
-        }
+        if (r < rows)
+            chain_dot<kDual, kSmallColumns>(xs + r * kSmallChunk, ws + c, ws2 + (kDual ? c : 0), kc,
+                                            acc, acc2);
         __syncthreads();
     }
     if (r < rows && n < columns) store_result<EPI>(out + (size_t)r * ldo + n, acc, acc2);
 }
 
-// Many rows (batched decode, prefill chunks): 64 columns x 16 rows per
-// 1024-thread work-group, one output chain per lane (lane = column,
-// wave = row). A K-chunk of the weight tile is shared by the 16 waves
-// through LDS and double-buffered through registers.
+// Many rows (batched decode, prefill chunks): 64 columns x 4 rows per
+// 256-thread work-group, one output chain per lane (lane = column,
+// wave = row), so even a 576-column projection of 64 rows spans 144 CUs.
+// K-chunks of the weight tile are shared by the 4 waves through LDS; the
+// global loads of the next kRing chunks stay in flight in a register ring
+// so the short per-chunk compute does not wait on memory.
+constexpr int kWideThreads = 256;
 constexpr int kWideColumns = 64;
-constexpr int kWideRows = 16;
+constexpr int kWideRows = kWideThreads / 64;
+constexpr int kRing = 4;
 
-template <int EPI>
-__global__ __launch_bounds__(1024) void gemm_wide_kernel(const float* __restrict__ x, int ldx,
+template <int EPI, bool FULL>
+__global__ __launch_bounds__(kWideThreads) void gemm_wide_kernel(const float* __restrict__ x, int ldx,
                                                          int rows, int inner,
                                                          const float* __restrict__ w,
                                                          const float* __restrict__ w2,
@@ -161,7 +293,7 @@ __global__ __launch_bounds__(1024) void gemm_wide_kernel(const float* __restrict
                                                          int column_tiles) {
     constexpr int kDual = EPI == kSwiglu ? 2 : 1;
     constexpr int kChunk = EPI == kSwiglu ? 32 : 64;          // k rows per chunk
-    constexpr int kPerThread = kChunk * kWideColumns / 1024;  // weight floats per thread
+    constexpr int kPerThread = kChunk * kWideColumns / kWideThreads;  // weight floats per thread
     constexpr int kXThreads = kWideRows * kChunk / 4;         // threads staging x (float4 each)
     __shared__ float ws[2][kDual][kChunk * kWideColumns];
     __shared__ float4 xs4[2][kXThreads];
@@ -171,68 +303,88 @@ __global__ __launch_bounds__(1024) void gemm_wide_kernel(const float* __restrict
     const int n0 = column_tile * kWideColumns, r0 = blockIdx.y * kWideRows;
     const int n = n0 + lane, row = r0 + wave;
     const int lr = tid / (kChunk / 4), lk = (tid % (kChunk / 4)) * 4;
-    float wreg[kDual][kPerThread];
-    float4 xreg = make_float4(0.f, 0.f, 0.f, 0.f);
-    auto fetch = [&](int k0) {
+    float wring[kRing][kDual][kPerThread];
+    float4 xring[kRing];
+    // Thread element j of a chunk is weight row (tid/64 + rows_per_pass*j),
+    // column tid%64 of the tile; offsets are 32-bit from the matrix base.
+    constexpr int kRowsPerPass = kWideThreads / kWideColumns;
+    const uint32_t thread_off = (uint32_t)(tid / kWideColumns) * (uint32_t)ldw + (uint32_t)(n0 + tid % kWideColumns);
+    auto fetch = [&](int k0, float (&wreg)[kDual][kPerThread], float4& xreg) {
 #pragma unroll
         for (int m = 0; m < kDual; ++m) {
             const float* src = m == 0 ? w : w2;
 #pragma unroll
             for (int j = 0; j < kPerThread; ++j) {
-                const int e = tid + j * 1024;
-                const int kk = e / kWideColumns, cc = e % kWideColumns;
-                const bool in = (k0 + kk < inner) && (n0 + cc < columns);
-                wreg[m][j] = in ? src[(size_t)(k0 + kk) * ldw + n0 + cc] : 0.0f;
+                if (FULL) {
+                    wreg[m][j] = src[thread_off + (uint32_t)(k0 + kRowsPerPass * j) * (uint32_t)ldw];
+                } else {
+                    const int e = tid + j * kWideThreads;
+                    const int kk = e / kWideColumns, cc = e % kWideColumns;
+                    const bool in = (k0 + kk < inner) && (n0 + cc < columns);
+                    // Raw load from an in-range address; masked when stashed, so
+                    // the ring's loads stay in flight.
+                    wreg[m][j] = src[in ? (size_t)(k0 + kk) * ldw + n0 + cc : 0];
+                }
             }
         }
         if (tid < kXThreads) {
             const int gr = r0 + lr;
-            float v[4];
+            if (FULL) {
+                xreg = *reinterpret_cast<const float4*>(x + (size_t)(gr < rows ? gr : 0) * ldx + k0 + lk);
+            } else {
+                float v[4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                v[j] = (gr < rows && k0 + lk + j < inner) ? x[(size_t)gr * ldx + k0 + lk + j] : 0.0f;
-            xreg = make_float4(v[0], v[1], v[2], v[3]);
+                for (int j = 0; j < 4; ++j) {
+                    const bool in = gr < rows && k0 + lk + j < inner;
+                    v[j] = x[in ? (size_t)gr * ldx + k0 + lk + j : 0];
+                }
+                xreg = make_float4(v[0], v[1], v[2], v[3]);
+            }
         }
-    };
-    auto stash = [&](int buffer) {
-#pragma unroll
-        for (int m = 0; m < kDual; ++m)
-#pragma unroll
-            for (int j = 0; j < kPerThread; ++j) ws[buffer][m][tid + j * 1024] = wreg[m][j];
-        if (tid < kXThreads) xs4[buffer][tid] = xreg;
     };
     float acc = 0.0f, acc2 = 0.0f;
     const int chunks = (inner + kChunk - 1) / kChunk;
-    fetch(0);
-    stash(0);
-    __syncthreads();
-    for (int chunk = 0; chunk < chunks; ++chunk) {
-        const int buffer = chunk & 1;
-        if (chunk + 1 < chunks) fetch((chunk + 1) * kChunk);
-        const int kc = min(kChunk, inner - chunk * kChunk);
-        const float* xr = reinterpret_cast<const float*>(xs4[buffer]) + wave * kChunk;
-        const float* wk = ws[buffer][0] + lane;
-        const float* uk = ws[buffer][kDual - 1] + lane;
-        int k = 0;
-        for (; k + 4 <= kc; k += 4) {
-            const float4 xv = *reinterpret_cast<const float4*>(xr + k);
-            acc = acc + xv.x * wk[(k + 0) * kWideColumns];
-            acc = acc + xv.y * wk[(k + 1) * kWideColumns];
-            acc = acc + xv.z * wk[(k + 2) * kWideColumns];
-            acc = acc + xv.w * wk[(k + 3) * kWideColumns];
-            if (EPI == kSwiglu) {
-                acc2 = acc2 + xv.x * uk[(k + 0) * kWideColumns];
-                acc2 = acc2 + xv.y * uk[(k + 1) * kWideColumns];
-                acc2 = acc2 + xv.z * uk[(k + 2) * kWideColumns];
-                acc2 = acc2 + xv.w * uk[(k + 3) * kWideColumns];
+#pragma unroll
+    for (int j = 0; j < kRing; ++j)
+        if (j < chunks) fetch(j * kChunk, wring[j], xring[j]);
+    for (int c0 = 0; c0 < chunks; c0 += kRing) {
+#pragma unroll
+        for (int j = 0; j < kRing; ++j) {
+            const int chunk = c0 + j;
+            if (chunk >= chunks) break;
+            const int buffer = chunk & 1;
+            const int k0 = chunk * kChunk;
+#pragma unroll
+            for (int m = 0; m < kDual; ++m)
+#pragma unroll
+                for (int e = 0; e < kPerThread; ++e) {
+                    const int el = tid + e * kWideThreads;
+                    if (FULL) {
+                        ws[buffer][m][el] = wring[j][m][e];
+                    } else {
+                        const int kk = el / kWideColumns, cc = el % kWideColumns;
+                        ws[buffer][m][el] = keep_if(wring[j][m][e], mask_of(k0 + kk < inner && n0 + cc < columns));
+                    }
+                }
+            if (tid < kXThreads) {
+                const int gr = r0 + lr;
+                const float4 xv = xring[j];
+                if (FULL)
+                    xs4[buffer][tid] = gr < rows ? xv : make_float4(0.f, 0.f, 0.f, 0.f);
+                else
+                    xs4[buffer][tid] = make_float4(keep_if(xv.x, mask_of(gr < rows && k0 + lk + 0 < inner)),
+                                                   keep_if(xv.y, mask_of(gr < rows && k0 + lk + 1 < inner)),
+                                                   keep_if(xv.z, mask_of(gr < rows && k0 + lk + 2 < inner)),
+                                                   keep_if(xv.w, mask_of(gr < rows && k0 + lk + 3 < inner)));
             }
+            if (chunk + kRing < chunks) fetch((chunk + kRing) * kChunk, wring[j], xring[j]);
+            __syncthreads();
+            const int kc = min(kChunk, inner - chunk * kChunk);
+            const float* xr = reinterpret_cast<const float*>(xs4[buffer]) + wave * kChunk;
+            const float* wk = ws[buffer][0] + lane;
+            const float* uk = ws[buffer][kDual - 1] + lane;
+            chain_dot<EPI == kSwiglu, kWideColumns>(xr, wk, uk, kc, acc, acc2);
         }
-        for (; k < kc; ++k) {
-            acc = acc + xr[k] * wk[k * kWideColumns];
-            if (EPI == kSwiglu) acc2 = acc2 + xr[k] * uk[k * kWideColumns];
-        }
-        if (chunk + 1 < chunks) stash(buffer ^ 1);
-        __syncthreads();
     }
     if (row < rows && n < columns) store_result<EPI>(out + (size_t)row * ldo + n, acc, acc2);
 }
@@ -292,6 +444,7 @@ __device__ __forceinline__ float block_max(float v, float* shared) {
 constexpr int kAttentionThreads = 256;
 constexpr int kMaxGroup = 8;
 constexpr int kMaxDim = 256;
+constexpr int kLdsTable = 2048;
 
 // One work-group per (row, kv head): the group's query heads share every K
 // and V byte. Reference order per (row, head) (llama_runner.cpp:86-92):
@@ -300,7 +453,8 @@ constexpr int kMaxDim = 256;
 //   e_t = expf(s_t - m);  den = sum_t e_t, sequential t
 //   out_d = sum_t (e_t/den) * v_td, sequential t
 // Scores are parallel over t; the denominator runs in one lane per head and
-// each (head, d) output chain in one lane.
+// each (head, d) output chain in one lane, streaming V page by page with the
+// next page's loads already in flight. BT is the page size (0: runtime).
 struct AttentionRow {
     const float* q;
     const int32_t* table;
@@ -308,38 +462,66 @@ struct AttentionRow {
     float* out;
 };
 
-__device__ void attention_row(const AttentionRow& row, const float* keys, const float* values,
-                              int layer, int layers, int block_tokens, int kv_width, int group,
-                              int dim, int kh, float* scores_global) {
+struct AttentionGeometry {
+    int layer, layers, block_tokens, kv_width, group, dim, kh;
+};
+
+template <int BT>
+__device__ void attention_row(const AttentionRow& row, const float* __restrict__ keys,
+                              const float* __restrict__ values, const AttentionGeometry& g,
+                              float* scores_global) {
     __shared__ float qs[kMaxGroup * kMaxDim];
     __shared__ float lds_scores[kAttentionLdsScores];
+    __shared__ int32_t lds_table[kLdsTable];
     __shared__ float reduce[kAttentionThreads / kWave];
     __shared__ float den_shared[kMaxGroup];
     __shared__ float max_shared[kMaxGroup];
     const int tid = threadIdx.x;
-    const int length = row.length;
-    // Score rows padded to a multiple of 4 for vector reads.
-    const int stride = (length + 3) & ~3;
+    const int bt = BT ? BT : g.block_tokens;
+    const int length = row.length, group = g.group, dim = g.dim;
+    const int pages = (length + bt - 1) / bt;
+    // Score rows padded to a multiple of 16; the padding holds zeros, which
+    // leave the sequential sums unchanged (x + 0 == x for the non-negative
+    // running sums here).
+    const int stride = (length + 15) & ~15;
     float* scores = group * stride <= kAttentionLdsScores ? lds_scores : scores_global;
+    const int32_t* table = row.table;
+    if (pages <= kLdsTable) {
+        for (int i = tid; i < pages; i += kAttentionThreads) lds_table[i] = row.table[i];
+        table = lds_table;
+    }
     for (int i = tid; i < group * dim; i += kAttentionThreads) qs[i] = row.q[i];
     __syncthreads();
+    const size_t layer_stride = (size_t)bt * g.kv_width;
+    auto token_offset = [&](int t) -> size_t {
+        const int page = t / bt, slot = t - page * bt;
+        return ((size_t)table[page] * g.layers + g.layer) * layer_stride + (size_t)slot * g.kv_width +
+               (size_t)g.kh * dim;
+    };
     // Scores: one token per thread, `group` sequential dot products.
     float local_max[kMaxGroup];
     for (int h = 0; h < group; ++h) local_max[h] = -INFINITY;
     const float root = sqrtf((float)dim);
     for (int t = tid; t < length; t += kAttentionThreads) {
-        const float* k = keys + pool_offset(row.table, t, layer, layers, block_tokens, kv_width) +
-                         (size_t)kh * dim;
+        const float* k = keys + token_offset(t);
         float s[kMaxGroup];
         for (int h = 0; h < group; ++h) s[h] = 0.0f;
-        for (int d = 0; d < dim; d += 4) {
-            const float4 kv4 = *reinterpret_cast<const float4*>(k + d);
+        for (int d0 = 0; d0 < dim; d0 += 16) {
+            float4 kv4[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                kv4[j] = d0 + 4 * j < dim ? *reinterpret_cast<const float4*>(k + d0 + 4 * j)
+                                          : make_float4(0.f, 0.f, 0.f, 0.f);
             for (int h = 0; h < group; ++h) {
-                const float* qh = qs + h * dim + d;
-                s[h] = s[h] + qh[0] * kv4.x;
-                s[h] = s[h] + qh[1] * kv4.y;
-                s[h] = s[h] + qh[2] * kv4.z;
-                s[h] = s[h] + qh[3] * kv4.w;
+                const float* qh = qs + h * dim + d0;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    if (d0 + 4 * j >= dim) break;
+                    s[h] = s[h] + qh[4 * j + 0] * kv4[j].x;
+                    s[h] = s[h] + qh[4 * j + 1] * kv4[j].y;
+                    s[h] = s[h] + qh[4 * j + 2] * kv4[j].z;
+                    s[h] = s[h] + qh[4 * j + 3] * kv4[j].w;
+                }
             }
         }
         for (int h = 0; h < group; ++h) {
@@ -355,24 +537,11 @@ __device__ void attention_row(const AttentionRow& row, const float* keys, const 
     __syncthreads();
     for (int h = 0; h < group; ++h) {
         const float m = max_shared[h];
-        for (int t = tid; t < length; t += kAttentionThreads)
-            scores[h * stride + t] = ref_expf(scores[h * stride + t] - m);
+        for (int t = tid; t < stride; t += kAttentionThreads)
+            scores[h * stride + t] = t < length ? ref_expf(scores[h * stride + t] - m) : 0.0f;
     }
     __syncthreads();
-    if (tid < group) {
-        const float* e = scores + tid * stride;
-        float den = 0.0f;
-        int t = 0;
-        for (; t + 4 <= length; t += 4) {
-            const float4 v = *reinterpret_cast<const float4*>(e + t);
-            den = den + v.x;
-            den = den + v.y;
-            den = den + v.z;
-            den = den + v.w;
-        }
-        for (; t < length; ++t) den = den + e[t];
-        den_shared[tid] = den;
-    }
+    if (tid < group) den_shared[tid] = sequential_sum(scores + tid * stride, stride);
     __syncthreads();
     for (int h = 0; h < group; ++h) {
         const float den = den_shared[h];
@@ -384,44 +553,49 @@ __device__ void attention_row(const AttentionRow& row, const float* keys, const 
     for (int chain = tid; chain < group * dim; chain += kAttentionThreads) {
         const int h = chain / dim, d = chain % dim;
         const float* p = scores + h * stride;
-        const float* vbase = values + (size_t)kh * dim + d;
+        const float* vbase = values + (size_t)g.kh * dim + d;
         float total = 0.0f;
-        int t = 0;
-        for (; t + 4 <= length; t += 4) {
-            const float v0 = vbase[pool_offset(row.table, t + 0, layer, layers, block_tokens, kv_width)];
-            const float v1 = vbase[pool_offset(row.table, t + 1, layer, layers, block_tokens, kv_width)];
-            const float v2 = vbase[pool_offset(row.table, t + 2, layer, layers, block_tokens, kv_width)];
-            const float v3 = vbase[pool_offset(row.table, t + 3, layer, layers, block_tokens, kv_width)];
-            const float4 pv = *reinterpret_cast<const float4*>(p + t);
-            total = total + pv.x * v0;
-            total = total + pv.y * v1;
-            total = total + pv.z * v2;
-            total = total + pv.w * v3;
+        if (BT) {
+            // Page-structured stream: a page's BT loads are independent; the
+            // next page is loaded while this one is summed.
+            float bufa[BT ? BT : 1], bufb[BT ? BT : 1];
+            auto load_page = [&](int page, float* buf) {
+                if (page >= pages) return;
+                const float* src = vbase + ((size_t)table[page] * g.layers + g.layer) * layer_stride;
+                const int valid = min(BT, length - page * BT);
+#pragma unroll
+                for (int j = 0; j < BT; ++j) buf[j] = j < valid ? src[(size_t)j * g.kv_width] : 0.0f;
+            };
+            auto sum_page = [&](int page, const float* buf) {
+                if (page >= pages) return;
+                const float4* p4 = reinterpret_cast<const float4*>(p + page * BT);
+                const int valid = min(BT, length - page * BT);
+#pragma unroll
+                for (int j4 = 0; j4 < BT / 4; ++j4) {
+                    const float4 pv = p4[j4];
+                    if (4 * j4 + 0 < valid) total = total + pv.x * buf[4 * j4 + 0];
+                    if (4 * j4 + 1 < valid) total = total + pv.y * buf[4 * j4 + 1];
+                    if (4 * j4 + 2 < valid) total = total + pv.z * buf[4 * j4 + 2];
+                    if (4 * j4 + 3 < valid) total = total + pv.w * buf[4 * j4 + 3];
+                }
+            };
+            load_page(0, bufa);
+            load_page(1, bufb);
+            for (int page = 0; page < pages; page += 2) {
+                sum_page(page, bufa);
+                load_page(page + 2, bufa);
+                sum_page(page + 1, bufb);
+                load_page(page + 3, bufb);
+            }
+        } else {
+            for (int t = 0; t < length; ++t) total = total + p[t] * vbase[token_offset(t) - (size_t)g.kh * dim];
         }
-        for (; t < length; ++t)
-            total = total + p[t] * vbase[pool_offset(row.table, t, layer, layers, block_tokens, kv_width)];
         row.out[h * dim + d] = total;
     }
     __syncthreads();
 }
 
-__global__ __launch_bounds__(kAttentionThreads) void attention_kernel(
-    const float* __restrict__ qkv, int ldq, int heads, int kv_heads, int dim, RowMeta meta,
-    PagedKv kv, int layer, float* __restrict__ out, int ldo, float* scratch,
-    size_t scratch_row_floats) {
-    const int r = blockIdx.x, kh = blockIdx.y;
-    const int group = heads / kv_heads;
-    AttentionRow row;
-    row.q = qkv + (size_t)r * ldq + (size_t)kh * group * dim;
-    row.table = kv.tables + (size_t)meta.seq_slot[meta.row_seq[r]] * kv.table_stride;
-    row.length = meta.row_pos[r] + 1;
-    row.out = out + (size_t)r * ldo + (size_t)kh * group * dim;
-    float* scores_global =
-        scratch ? scratch + ((size_t)r * kv_heads + kh) * scratch_row_floats : nullptr;
-    attention_row(row, kv.keys, kv.values, layer, kv.layers, kv.block_tokens, kv.kv_width, group,
-                  dim, kh, scores_global);
-}
-
+template <int BT>
 __global__ __launch_bounds__(kAttentionThreads) void attention_single_kernel(
     const float* __restrict__ q, const float* __restrict__ keys, const float* __restrict__ values,
     const int32_t* __restrict__ table, int length, int layer, int layers, int block_tokens,
@@ -433,10 +607,257 @@ __global__ __launch_bounds__(kAttentionThreads) void attention_single_kernel(
     row.table = table;
     row.length = length;
     row.out = out + (size_t)kh * group * dim;
-    const size_t stride = (size_t)((length + 3) & ~3) * group;
-    float* scores_global = scratch ? scratch + (size_t)kh * stride : nullptr;
-    attention_row(row, keys, values, layer, layers, block_tokens, kv_heads * dim, group, dim, kh,
-                  scores_global);
+    float* scores_global =
+        scratch ? scratch + (size_t)kh * group * (size_t)((length + 15) & ~15) : nullptr;
+    const AttentionGeometry g{layer, layers, block_tokens, kv_heads * dim, group, dim, kh};
+    attention_row<BT>(row, keys, values, g, scores_global);
+}
+
+// ---------------------------------------------------------------------------
+// Forward attention as three kernels, same arithmetic as attention_row:
+//   scores  : grid (row, kv head, 256-token chunk) -- every K byte of a layer
+//             is requested at once; per-chunk maxima.
+//   softmax : grid (row, head) -- max of chunk maxima, e = expf(s - m),
+//             sequential denominator, p = e / den (in place).
+//   pv      : grid (row, kv head) -- V pages streamed through a 2 x 64 KB
+//             LDS double buffer by all waves while the chain lanes
+//             (head, d) sum the previous batch in token order.
+// Score rows are `stride` floats (length padded to 16, padding zero).
+constexpr int kScoreChunk = 256;
+constexpr int kPvBufferFloats = 16384;  // one V batch buffer (64 KB)
+constexpr int kPvMaxBatchTokens = 256;  // p values staged per head per batch
+
+template <int BT>
+__global__ __launch_bounds__(kScoreChunk) void attn_scores_kernel(
+    const float* __restrict__ qkv, int ldq, int heads, int kv_heads, int dim, RowMeta meta,
+    PagedKv kv, int layer, float* __restrict__ scores, int stride, float* __restrict__ chunk_max,
+    int chunks) {
+    __shared__ float qs[kMaxGroup * kMaxDim];
+    __shared__ float reduce[kScoreChunk / kWave];
+    const int r = blockIdx.x, kh = blockIdx.y, chunk = blockIdx.z;
+    const int length = meta.row_pos[r] + 1;
+    if (chunk * kScoreChunk >= length) return;
+    const int group = heads / kv_heads, tid = threadIdx.x;
+    const int bt = BT ? BT : kv.block_tokens;
+    const float* q = qkv + (size_t)r * ldq + (size_t)kh * group * dim;
+    const int32_t* table = kv.tables + (size_t)meta.seq_slot[meta.row_seq[r]] * kv.table_stride;
+    for (int i = tid; i < group * dim; i += kScoreChunk) qs[i] = q[i];
+    __syncthreads();
+    const int t = chunk * kScoreChunk + tid;
+    float s[kMaxGroup];
+    for (int h = 0; h < group; ++h) s[h] = -INFINITY;
+    if (t < length) {
+        const int page = t / bt, slot = t - page * bt;
+        const float* k = kv.keys +
+                         (((size_t)table[page] * kv.layers + layer) * bt + slot) * kv.kv_width +
+                         (size_t)kh * dim;
+        for (int h = 0; h < group; ++h) s[h] = 0.0f;
+        // All of a 64-wide block of the key row is requested before the
+        // dot products start.
+        for (int d0 = 0; d0 < dim; d0 += 64) {
+            float4 k4[16];
+#pragma unroll
+            for (int j = 0; j < 16; ++j)
+                k4[j] = d0 + 4 * j < dim ? *reinterpret_cast<const float4*>(k + d0 + 4 * j)
+                                         : make_float4(0.f, 0.f, 0.f, 0.f);
+            for (int h = 0; h < group; ++h) {
+                const float* qh = qs + h * dim + d0;
+                float acc = s[h];
+#pragma unroll
+                for (int j = 0; j < 16; ++j) {
+                    if (d0 + 4 * j >= dim) break;
+                    const float4 q4 = *reinterpret_cast<const float4*>(qh + 4 * j);
+                    acc = acc + q4.x * k4[j].x;
+                    acc = acc + q4.y * k4[j].y;
+                    acc = acc + q4.z * k4[j].z;
+                    acc = acc + q4.w * k4[j].w;
+                }
+                s[h] = acc;
+            }
+        }
+        const float root = sqrtf((float)dim);
+        for (int h = 0; h < group; ++h) {
+            s[h] = s[h] / root;
+            scores[((size_t)r * heads + kh * group + h) * stride + t] = s[h];
+        }
+    }
+    for (int h = 0; h < group; ++h) {
+        const float m = block_max(s[h], reduce);
+        if (tid == 0) chunk_max[((size_t)r * heads + kh * group + h) * chunks + chunk] = m;
+    }
+}
+
+constexpr int kSoftmaxThreads = 256;
+constexpr int kSoftmaxStage = 4096;
+
+__global__ __launch_bounds__(kSoftmaxThreads) void attn_softmax_kernel(
+    float* __restrict__ scores, int stride, const float* __restrict__ chunk_max, int chunks,
+    RowMeta meta, int heads) {
+    __shared__ float stage[kSoftmaxStage];
+    __shared__ float reduce[kSoftmaxThreads / kWave];
+    __shared__ float den_shared;
+    const int r = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+    const int length = meta.row_pos[r] + 1;
+    float* row = scores + ((size_t)r * heads + h) * stride;
+    const float* cm = chunk_max + ((size_t)r * heads + h) * chunks;
+    const int used = (length + kScoreChunk - 1) / kScoreChunk;
+    float local = -INFINITY;
+    for (int c = tid; c < used; c += kSoftmaxThreads) local = local < cm[c] ? cm[c] : local;
+    const float m = block_max(local, reduce);
+    // e = expf(s - m) staged through LDS; the denominator runs in token order
+    // in one lane over each staged block.
+    float den = 0.0f;
+    for (int c0 = 0; c0 < stride; c0 += kSoftmaxStage) {
+        const int n = min(kSoftmaxStage, stride - c0);
+        for (int i = tid; i < n; i += kSoftmaxThreads) {
+            const int t = c0 + i;
+            const float e = t < length ? ref_expf(row[t] - m) : 0.0f;
+            stage[i] = e;
+            if (stride > kSoftmaxStage) row[t] = e;
+        }
+        __syncthreads();
+        if (tid == 0) den = sequential_sum(stage, n, den);
+        __syncthreads();
+    }
+    if (tid == 0) den_shared = den;
+    __syncthreads();
+    den = den_shared;
+    if (stride <= kSoftmaxStage) {
+        for (int t = tid; t < length; t += kSoftmaxThreads) row[t] = stage[t] / den;
+    } else {
+        for (int t = tid; t < length; t += kSoftmaxThreads) row[t] = row[t] / den;
+    }
+}
+
+constexpr int kPvThreads = 256;
+
+template <int BT, int DIM>
+__global__ __launch_bounds__(kPvThreads) void attn_pv_kernel(
+    const float* __restrict__ probs, int stride, int heads, int kv_heads, int dim, RowMeta meta,
+    PagedKv kv, int layer, float* __restrict__ out, int ldo) {
+    __shared__ float4 vbuf4[2][kPvBufferFloats / 4];
+    __shared__ float4 pbuf4[2][kMaxGroup * kPvMaxBatchTokens / 4];
+    __shared__ int32_t lds_table[kLdsTable];
+    const int r = blockIdx.x, kh = blockIdx.y, tid = threadIdx.x;
+    const int group = heads / kv_heads;
+    const int bt = BT ? BT : kv.block_tokens;
+    const int length = meta.row_pos[r] + 1;
+    const int pages = (length + bt - 1) / bt;
+    const int32_t* table = kv.tables + (size_t)meta.seq_slot[meta.row_seq[r]] * kv.table_stride;
+    // Page table in LDS (at most kLdsTable pages, checked by the host), so V
+    // addresses never wait on a global load.
+    for (int i = tid; i < pages; i += kPvThreads) lds_table[i] = table[i];
+    __syncthreads();
+    // Pages per batch: bounded by the V buffer and by the staged p rows.
+    int batch_pages = kPvBufferFloats / (bt * dim);
+    if (batch_pages * bt > kPvMaxBatchTokens) batch_pages = kPvMaxBatchTokens / bt;
+    const int batch_tokens = batch_pages * bt;
+    const int batches = (pages + batch_pages - 1) / batch_pages;
+    const int vec_per_token = dim / 4;
+    const int vec_per_batch = batch_tokens * vec_per_token;
+    const float* prow = probs + ((size_t)r * heads + (size_t)kh * group) * stride;
+    // Loader: each thread carries up to kLoads float4 of V for the next batch.
+    constexpr int kLoads = kPvBufferFloats / 4 / kPvThreads;  // 16
+    float4 vreg[kLoads];
+    float4 preg[(kMaxGroup * kPvMaxBatchTokens / 4 + kPvThreads - 1) / kPvThreads];
+    // Fast layout (16-token pages, head_dim 64): thread element j is token
+    // 16*j + tid/16 of the batch, float4 tid%16 of its row, i.e. page
+    // batch*16 + j at slot tid/16, read from a wave-uniform page base.
+    constexpr bool kFast = BT == 16 && DIM == 64;
+    const uint32_t fast_off = (uint32_t)(tid / 16) * (uint32_t)kv.kv_width + 4u * (uint32_t)(tid % 16);
+    auto fetch = [&](int batch) {
+        const int t0 = batch * batch_tokens;
+        if (kFast) {
+#pragma unroll
+            for (int j = 0; j < kLoads; ++j) {
+                const int page = min(t0 / 16 + j, pages - 1);
+                const int block = __builtin_amdgcn_readfirstlane(lds_table[page]);
+                const float* base = kv.values + (((size_t)block * kv.layers + layer) * 16) * kv.kv_width +
+                                    (size_t)kh * 64;
+                vreg[j] = *reinterpret_cast<const float4*>(base + fast_off);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < kLoads; ++j) {
+                const int e = tid + j * kPvThreads;
+                const int tok = e / vec_per_token, d4 = e - tok * vec_per_token;
+                const int t = t0 + tok;
+                const bool in = e < vec_per_batch && t < length;
+                const int tc = in ? t : 0;
+                const int page = tc / bt, slot = tc - page * bt;
+                vreg[j] = *reinterpret_cast<const float4*>(
+                    kv.values + (((size_t)lds_table[page] * kv.layers + layer) * bt + slot) * kv.kv_width +
+                    (size_t)kh * dim + 4 * (in ? d4 : 0));
+            }
+        }
+        const int pvec = group * batch_tokens / 4;
+#pragma unroll
+        for (int j = 0; j < (int)(sizeof(preg) / sizeof(preg[0])); ++j) {
+            const int e = tid + j * kPvThreads;
+            const int h = e / (batch_tokens / 4), i4 = e - h * (batch_tokens / 4);
+            const bool in = e < pvec && t0 + 4 * i4 < stride;
+            preg[j] = *reinterpret_cast<const float4*>(prow + (in ? (size_t)h * stride + t0 + 4 * i4 : 0));
+        }
+    };
+    // Masks are applied here, after every load of the batch is in flight;
+    // only a batch that runs past the row's length needs them.
+    auto stash = [&](int batch, int buffer) {
+        const int t0 = batch * batch_tokens;
+        const bool whole = kFast && t0 + batch_tokens <= length;
+#pragma unroll
+        for (int j = 0; j < kLoads; ++j) {
+            const int e = tid + j * kPvThreads;
+            if (whole) {
+                vbuf4[buffer][e] = vreg[j];
+            } else {
+                const int tok = e / vec_per_token;
+                vbuf4[buffer][e] = keep_if(vreg[j], mask_of(e < vec_per_batch && t0 + tok < length));
+            }
+        }
+        const int pvec = group * batch_tokens / 4;
+#pragma unroll
+        for (int j = 0; j < (int)(sizeof(preg) / sizeof(preg[0])); ++j) {
+            const int e = tid + j * kPvThreads;
+            const int h = e / (batch_tokens / 4), i4 = e - h * (batch_tokens / 4);
+            if (e < kMaxGroup * kPvMaxBatchTokens / 4)
+                pbuf4[buffer][e] = keep_if(preg[j], mask_of(e < pvec && t0 + 4 * i4 < stride));
+        }
+    };
+    constexpr int kMaxChains = kMaxGroup * kMaxDim / kPvThreads;
+    float total[kMaxChains];
+#pragma unroll
+    for (int i = 0; i < kMaxChains; ++i) total[i] = 0.0f;
+    fetch(0);
+    stash(0, 0);
+    __syncthreads();
+    for (int b = 0; b < batches; ++b) {
+        const int buffer = b & 1;
+        if (b + 1 < batches) fetch(b + 1);
+        const int n = min(batch_tokens, length - b * batch_tokens);
+        const float* vb = reinterpret_cast<const float*>(vbuf4[buffer]);
+        const float* pb = reinterpret_cast<const float*>(pbuf4[buffer]);
+#pragma unroll
+        for (int i = 0; i < kMaxChains; ++i) {
+            const int chain = tid + i * kPvThreads;
+            if (chain >= group * dim) break;
+            const int h = chain / dim, d = chain - h * dim;
+            const float* ph = pb + h * batch_tokens;
+            const float* vd = vb + d;
+            float acc = total[i];
+            float dummy = 0.0f;
+            chain_dot<false, 0>(ph, vd, nullptr, n, acc, dummy, dim);
+            total[i] = acc;
+        }
+        if (b + 1 < batches) stash(b + 1, buffer ^ 1);
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < kMaxChains; ++i) {
+        const int chain = tid + i * kPvThreads;
+        if (chain >= group * dim) break;
+        const int h = chain / dim, d = chain - h * dim;
+        out[(size_t)r * ldo + ((size_t)kh * group + h) * dim + d] = total[i];
+    }
 }
 
 // std::max_element semantics: the smallest index among the maxima.
@@ -542,11 +963,23 @@ hipError_t launch_gemm(hipStream_t s, Epilogue epilogue, const float* x, int ldx
     } else {
         const int tiles = (columns + kWideColumns - 1) / kWideColumns;
         const dim3 grid(tiles, (rows + kWideRows - 1) / kWideRows);
-        switch (epilogue) {
-        case kStore: gemm_wide_kernel<kStore><<<grid, 1024, 0, s>>>(x, ldx, rows, inner, w, w2, columns, ldw, out, ldo, tiles); break;
-        case kResidual: gemm_wide_kernel<kResidual><<<grid, 1024, 0, s>>>(x, ldx, rows, inner, w, w2, columns, ldw, out, ldo, tiles); break;
-        case kSwiglu: gemm_wide_kernel<kSwiglu><<<grid, 1024, 0, s>>>(x, ldx, rows, inner, w, w2, columns, ldw, out, ldo, tiles); break;
+        const bool full = inner % 64 == 0 && columns % kWideColumns == 0 && ldx % 4 == 0 &&
+                          (size_t)inner * ldw < (1ull << 32);
+#define MP_WIDE(E, F) gemm_wide_kernel<E, F><<<grid, kWideThreads, 0, s>>>(x, ldx, rows, inner, w, w2, columns, ldw, out, ldo, tiles)
+        if (full) {
+            switch (epilogue) {
+            case kStore: MP_WIDE(kStore, true); break;
+            case kResidual: MP_WIDE(kResidual, true); break;
+            case kSwiglu: MP_WIDE(kSwiglu, true); break;
+            }
+        } else {
+            switch (epilogue) {
+            case kStore: MP_WIDE(kStore, false); break;
+            case kResidual: MP_WIDE(kResidual, false); break;
+            case kSwiglu: MP_WIDE(kSwiglu, false); break;
+            }
         }
+#undef MP_WIDE
     }
     return hipGetLastError();
 }
@@ -563,12 +996,23 @@ hipError_t launch_rope_append(hipStream_t s, float* qkv, int ldqkv, int rows, in
 
 hipError_t launch_attention(hipStream_t s, const float* qkv, int ldq, int rows, int heads,
                             int kv_heads, int dim, const RowMeta& meta, const PagedKv& kv,
-                            int layer, float* out, int ldo, float* scratch,
-                            size_t scratch_row_floats) {
+                            int layer, float* out, int ldo, const AttentionScratch& scratch) {
     if (rows <= 0) return hipSuccess;
-    if (heads / kv_heads > kMaxGroup || dim > kMaxDim || dim % 4) return hipErrorInvalidValue;
-    attention_kernel<<<dim3(rows, kv_heads), kAttentionThreads, 0, s>>>(
-        qkv, ldq, heads, kv_heads, dim, meta, kv, layer, out, ldo, scratch, scratch_row_floats);
+    if (heads / kv_heads > kMaxGroup || dim > kMaxDim || dim % 4 || kv.block_tokens * dim > kPvBufferFloats)
+        return hipErrorInvalidValue;
+    const dim3 sgrid(rows, kv_heads, scratch.chunks);
+    if (kv.block_tokens == 16)
+        attn_scores_kernel<16><<<sgrid, kScoreChunk, 0, s>>>(qkv, ldq, heads, kv_heads, dim, meta, kv, layer, scratch.scores, scratch.stride, scratch.chunk_max, scratch.chunks);
+    else
+        attn_scores_kernel<0><<<sgrid, kScoreChunk, 0, s>>>(qkv, ldq, heads, kv_heads, dim, meta, kv, layer, scratch.scores, scratch.stride, scratch.chunk_max, scratch.chunks);
+    attn_softmax_kernel<<<dim3(rows, heads), kSoftmaxThreads, 0, s>>>(scratch.scores, scratch.stride, scratch.chunk_max, scratch.chunks, meta, heads);
+    if (kv.block_tokens == 16)
+        if (dim == 64)
+            attn_pv_kernel<16, 64><<<dim3(rows, kv_heads), kPvThreads, 0, s>>>(scratch.scores, scratch.stride, heads, kv_heads, dim, meta, kv, layer, out, ldo);
+        else
+            attn_pv_kernel<16, 0><<<dim3(rows, kv_heads), kPvThreads, 0, s>>>(scratch.scores, scratch.stride, heads, kv_heads, dim, meta, kv, layer, out, ldo);
+    else
+        attn_pv_kernel<0, 0><<<dim3(rows, kv_heads), kPvThreads, 0, s>>>(scratch.scores, scratch.stride, heads, kv_heads, dim, meta, kv, layer, out, ldo);
     return hipGetLastError();
 }
 
@@ -577,9 +1021,11 @@ hipError_t launch_attention_single(hipStream_t s, const float* q, const float* k
                                    int layer, int layers, int block_tokens, int heads,
                                    int kv_heads, int dim, float* out, float* scratch) {
     if (heads / kv_heads > kMaxGroup || dim > kMaxDim || dim % 4) return hipErrorInvalidValue;
-    attention_single_kernel<<<dim3(1, kv_heads), kAttentionThreads, 0, s>>>(
-        q, keys, values, table, length, layer, layers, block_tokens, heads, kv_heads, dim, out,
-        scratch);
+    const dim3 grid(1, kv_heads);
+    if (block_tokens == 16)
+        attention_single_kernel<16><<<grid, kAttentionThreads, 0, s>>>(q, keys, values, table, length, layer, layers, block_tokens, heads, kv_heads, dim, out, scratch);
+    else
+        attention_single_kernel<0><<<grid, kAttentionThreads, 0, s>>>(q, keys, values, table, length, layer, layers, block_tokens, heads, kv_heads, dim, out, scratch);
     return hipGetLastError();
 }
 
