@@ -110,16 +110,21 @@ int mp_hip_table_write(mp_hip* h, int32_t slot, int32_t first, const int32_t* bl
  * the context's stream; ordered before the next forward. */
 int mp_hip_copy_tail(mp_hip* h, const mp_tail_region* region);
 
+/* Same copy, timed with device events around it (the reference's opt-in
+ * COW timing, llama_runner.cu:129-138,171-172). Synchronous. */
+int mp_hip_copy_tail_timed(mp_hip* h, const mp_tail_region* region, uint64_t* nanoseconds);
+
 /* Chunk forward of `nseq` sequences (CpuRunner::append's device half,
  * llama_runner.cpp:70-102): embeds `tokens` (sum of counts, sequence-major),
  * runs every layer writing K/V at positions used..used+count-1 through each
  * sequence's table, and produces for each sequence the logits of its LAST
  * token. `logits` (nseq*vocab floats) may be NULL; `argmax` (nseq) receives
- * the first index of the maximum logit (std::max_element, engine.cpp:99).
- * Returns MP_NONFINITE if any produced logit is not finite (llama_runner.cu:173);
- * outputs are still written. Synchronous. */
+ * the first index of the maximum logit (std::max_element, engine.cpp:99);
+ * `nonfinite` (nseq, may be NULL) receives 1 for a sequence with any
+ * non-finite logit. Returns MP_NONFINITE if any produced logit is not
+ * finite (llama_runner.cu:173); outputs are still written. Synchronous. */
 int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int32_t* tokens,
-                   float* logits, int32_t* argmax);
+                   float* logits, int32_t* argmax, int32_t* nonfinite);
 
 /* Stand-alone paged GQA decode attention on caller-owned DEVICE buffers
  * (the attention of llama_runner.cpp:85-93 for one query row of length

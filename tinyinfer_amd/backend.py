@@ -54,7 +54,8 @@ def _bind(lib):
     lib.mp_hip_ready.argtypes = [vp, I32P]
     lib.mp_hip_table_write.argtypes = [vp, ctypes.c_int32, ctypes.c_int32, I32P, ctypes.c_int32]
     lib.mp_hip_copy_tail.argtypes = [vp, ctypes.POINTER(TailRegion)]
-    lib.mp_hip_forward.argtypes = [vp, ctypes.POINTER(SeqStep), ctypes.c_int32, I32P, F32P, I32P]
+    lib.mp_hip_forward.argtypes = [vp, ctypes.POINTER(SeqStep), ctypes.c_int32, I32P, F32P, I32P, I32P]
+    lib.mp_hip_copy_tail_timed.argtypes = [vp, ctypes.POINTER(TailRegion), ctypes.POINTER(ctypes.c_uint64)]
     lib.mp_hip_paged_attention_decode.argtypes = [vp, vp, vp, vp] + [ctypes.c_int32] * 7 + [vp, vp]
     lib.mp_hip_sync.argtypes = [vp]
     lib.mp_hip_stats.argtypes = [vp, ctypes.POINTER(Counters)]
@@ -127,7 +128,7 @@ class HipBackend:
         logits = np.empty((n, self.config["vocabulary"]), dtype=np.float32) if want_logits else None
         status = self.lib.mp_hip_forward(self.handle, arr, n, t.ctypes.data_as(I32P),
                                          logits.ctypes.data_as(F32P) if want_logits else None,
-                                         am.ctypes.data_as(I32P))
+                                         am.ctypes.data_as(I32P), None)
         if status == MP_NONFINITE:
             raise FloatingPointError(self.lib.mp_hip_last_error(self.handle).decode())
         self._check(status)

@@ -57,7 +57,7 @@ struct mp_hip {
     float *last = nullptr, *logits = nullptr, *scratch = nullptr;
     size_t scratch_floats = 0;
     int32_t* meta = nullptr;  // tokens | row_seq | row_pos | seq_slot | seq_last_row
-    int32_t* results = nullptr;  // argmax[seqs] | nonfinite
+    int32_t* results = nullptr;  // argmax[seqs] | nonfinite[seqs]
     std::vector<int32_t> host_meta;
     std::vector<void*> allocations;
 };
@@ -180,7 +180,7 @@ int ensure_workspace(mp_hip* h, int rows, int seqs, int max_length) {
         {(void**)&h->last, sizeof(float) * S * hd},
         {(void**)&h->logits, sizeof(float) * S * (size_t)c.vocabulary},
         {(void**)&h->meta, sizeof(int32_t) * (3 * (size_t)R + 2 * (size_t)S)},
-        {(void**)&h->results, sizeof(int32_t) * ((size_t)S + 1)},
+        {(void**)&h->results, sizeof(int32_t) * 2 * (size_t)S},
     };
     size_t total = 0;
     for (const auto& it : items) {
@@ -391,8 +391,25 @@ int mp_hip_copy_tail(mp_hip* h, const mp_tail_region* r) {
     return status;
 }
 
+int mp_hip_copy_tail_timed(mp_hip* h, const mp_tail_region* region, uint64_t* nanoseconds) {
+    if (!h || !nanoseconds) return MP_INVALID_ARGUMENT;
+    hipEvent_t begin = nullptr, end = nullptr;
+    int status = check(h, hipEventCreate(&begin), "COW event begin");
+    if (!status) status = check(h, hipEventCreate(&end), "COW event end");
+    if (!status) status = check(h, hipEventRecord(begin, h->stream), "COW timing begin");
+    if (!status) status = mp_hip_copy_tail(h, region);
+    if (!status) status = check(h, hipEventRecord(end, h->stream), "COW timing end");
+    if (!status) status = check(h, hipEventSynchronize(end), "COW completion");
+    float ms = 0.0f;
+    if (!status) status = check(h, hipEventElapsedTime(&ms, begin, end), "COW elapsed");
+    if (!status) *nanoseconds = (uint64_t)(ms * 1e6);
+    if (begin) (void)hipEventDestroy(begin);
+    if (end) (void)hipEventDestroy(end);
+    return status;
+}
+
 int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int32_t* tokens,
-                   float* logits, int32_t* argmax) {
+                   float* logits, int32_t* argmax, int32_t* nonfinite) {
     if (!h || !steps || nseq < 1 || !tokens || !argmax)
         return fail(h, MP_INVALID_ARGUMENT, "invalid forward arguments");
     const mp_model_desc& c = h->model;
@@ -460,11 +477,10 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
     }
     if (e == hipSuccess) e = mphip::launch_rms(s, h->x, c.hidden, meta.seq_last_row, h->final_norm, h->last, c.hidden, nseq, c.hidden, c.rms_epsilon);
     if (e == hipSuccess) e = mphip::launch_gemm(s, mphip::kStore, h->last, c.hidden, nseq, c.hidden, h->head, nullptr, c.vocabulary, c.vocabulary, h->logits, c.vocabulary);
-    if (e == hipSuccess) e = hipMemsetAsync(h->results + nseq, 0, sizeof(int32_t), s);
     if (e == hipSuccess) e = mphip::launch_argmax(s, h->logits, nseq, c.vocabulary, h->results, h->results + nseq);
     if ((status = check(h, e, "model kernel launch"))) return status;
-    std::vector<int32_t> results((size_t)nseq + 1);
-    status = check(h, hipMemcpyAsync(results.data(), h->results, sizeof(int32_t) * (nseq + 1), hipMemcpyDeviceToHost, s), "download argmax");
+    std::vector<int32_t> results(2 * (size_t)nseq);
+    status = check(h, hipMemcpyAsync(results.data(), h->results, sizeof(int32_t) * 2 * nseq, hipMemcpyDeviceToHost, s), "download argmax");
     if (!status && logits) {
         status = check(h, hipMemcpyAsync(logits, h->logits, sizeof(float) * (size_t)nseq * c.vocabulary, hipMemcpyDeviceToHost, s), "download logits");
         if (!status) h->stats.logits_downloaded_bytes += sizeof(float) * (size_t)nseq * c.vocabulary;
@@ -472,9 +488,11 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
     if (!status) status = check(h, hipStreamSynchronize(s), "model completion");
     if (status) return status;
     std::memcpy(argmax, results.data(), sizeof(int32_t) * nseq);
+    if (nonfinite) std::memcpy(nonfinite, results.data() + nseq, sizeof(int32_t) * nseq);
     ++h->stats.forward_calls;
     h->stats.forward_rows += R;
-    if (results[nseq]) return fail(h, MP_NONFINITE, "nonfinite HIP logits");
+    for (int i = 0; i < nseq; ++i)
+        if (results[(size_t)nseq + i]) return fail(h, MP_NONFINITE, "nonfinite HIP logits");
     return MP_OK;
 }
 

@@ -74,7 +74,7 @@ hipError_t launch_attention_single(hipStream_t s, const float* q, const float* k
 constexpr int kAttentionLdsScores = 10240;
 
 // First index of the maximum of each row of logits (std::max_element), and
-// a flag set to 1 when any value is not finite.
+// per row a flag: 1 when any value of the row is not finite, else 0.
 hipError_t launch_argmax(hipStream_t s, const float* logits, int rows, int vocabulary,
                          int32_t* argmax, int32_t* nonfinite);
 

@@ -891,8 +891,12 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ 
         best_v[wave] = bv;
         best_i[wave] = bi;
     }
-    if (bad) atomicOr(nonfinite, 1);
+    __shared__ int any_bad;
+    if (threadIdx.x == 0) any_bad = 0;
     __syncthreads();
+    if (bad) any_bad = 1;
+    __syncthreads();
+    if (threadIdx.x == 0) nonfinite[blockIdx.x] = any_bad;
     if (threadIdx.x == 0) {
         float v = best_v[0];
         int idx = best_i[0];

@@ -1,0 +1,53 @@
+// Weights and runners of this library for the C entry points.
+#include "harness_backend.h"
+
+#include <cstring>
+
+namespace miniprefix {
+bool hip_runner_sequence(const ModelRunner& runner, const RequestId& id, const PagedSequence** out);
+}
+
+namespace mpx {
+
+std::shared_ptr<miniprefix::ModelWeights> synthetic_weights(const miniprefix::ModelConfig& config, std::uint64_t seed,
+                                                            double stddev) {
+    return miniprefix::ModelWeights::synthetic(config, seed, stddev);
+}
+
+std::shared_ptr<miniprefix::ModelWeights> load_weights(const std::string& path) {
+    return miniprefix::ModelWeights::load(path);
+}
+
+bool weights_tensor(const miniprefix::ModelWeights& weights, const std::string& name, const float** data,
+                    std::size_t* count) {
+    const auto it = weights.tensors.find(name);
+    if (it == weights.tensors.end()) return false;
+    *data = it->second.data.data();
+    *count = it->second.data.size();
+    return true;
+}
+
+bool weights_set(miniprefix::ModelWeights& weights, const std::string& name, const float* data, std::size_t count) {
+    const auto it = weights.tensors.find(name);
+    if (it == weights.tensors.end() || it->second.data.size() != count) return false;
+    std::memcpy(it->second.data.data(), data, count * sizeof(float));
+    return true;
+}
+
+std::unique_ptr<miniprefix::ModelRunner> make_runner(int kind, std::shared_ptr<miniprefix::ModelWeights> weights,
+                                                     int context, miniprefix::KvCacheConfig kv) {
+    if (kind != 0) throw std::invalid_argument("unknown runner kind");
+    return miniprefix::make_hip_runner(std::move(weights), context, kv);
+}
+
+void set_batching(miniprefix::Engine& engine, bool enabled) { engine.set_batching(enabled); }
+
+bool sequence_of(const miniprefix::ModelRunner& runner, const std::string& id, std::vector<int>* blocks, int* used) {
+    const miniprefix::PagedSequence* s = nullptr;
+    if (!miniprefix::hip_runner_sequence(runner, id, &s)) return false;
+    *blocks = s->blocks;
+    *used = s->used;
+    return true;
+}
+
+}  // namespace mpx
