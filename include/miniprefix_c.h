@@ -68,6 +68,9 @@ int mpx_runner_set_cost_timing(void* runner, int32_t enabled);
 /* Committed page table; MPX_LOGIC_ERROR if the runner does not expose it. */
 int mpx_runner_sequence(const void* runner, const char* id, int32_t* blocks, int32_t capacity, int32_t* count,
                         int32_t* used);
+/* The runner's device context (an mp_hip*, include/mp_hip.h), or NULL for a
+ * runner without one; for instrumentation such as mp_hip_set_timing. */
+void* mpx_runner_device(void* runner);
 
 /* Engine; takes ownership of the runner. The runner handle stays usable as
  * a borrowed view (mpx_runner_free ignores it) until mpx_engine_free. */

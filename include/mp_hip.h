@@ -146,6 +146,23 @@ int mp_hip_kv_pools(const mp_hip* h, float** keys, float** values, size_t* eleme
 /* The context's stream (hipStream_t), e.g. for recording events around calls. */
 void* mp_hip_stream(const mp_hip* h);
 
+/* Kernel timing of forward calls with HIP events on the context's stream
+ * (instrumentation; no counterpart in the reference). `classes` is a mask of
+ * MP_TIME_* bits; each enabled class brackets its launches with events and
+ * accumulates their elapsed time when the forward call completes. Setting
+ * the mask resets the totals. One ATTENTION launch is one layer's attention
+ * (score, softmax and value kernels); one PROJECTION launch is one GEMM
+ * (QKV, O, gate/up or down); one HEAD launch is final norm, LM head and
+ * argmax of a call. */
+enum { MP_TIME_ATTENTION = 1, MP_TIME_PROJECTION = 2, MP_TIME_HEAD = 4 };
+typedef struct mp_hip_timing_totals {
+    uint64_t attention_ns, attention_launches;
+    uint64_t projection_ns, projection_launches;
+    uint64_t head_ns, head_launches;
+} mp_hip_timing_totals;
+int mp_hip_set_timing(mp_hip* h, uint32_t classes);
+int mp_hip_kernel_times(const mp_hip* h, mp_hip_timing_totals* out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -160,4 +160,6 @@ bool sequence_of(const ModelRunner& runner, const std::string& id, std::vector<i
     return true;
 }
 
+void* device_of(ModelRunner&) { return nullptr; }
+
 }  // namespace mpx

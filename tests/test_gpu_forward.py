@@ -112,3 +112,46 @@ def test_batched_rows_match_single_sequences(torch_cuda):
             _logits_match(got[i], want[i])
             assert am[i] == int(np.argmax(want[i]))
             used[i] += len(chunks[i])
+
+
+def test_long_prefill_row_blocks(torch_cuda):
+    """Prefill chunks of 256 rows (row blocks of several positions each,
+    several 256-token score chunks) followed by decode rows."""
+    cfg = smollm_config(layers=2, context=1024)
+    model = OracleModel(cfg, seed=13)
+    backend = HipBackend(cfg, block_tokens=16, max_blocks=64, max_sequences=4)
+    upload_model(backend, model)
+    o = Oracle()
+    prompt = [int(t) for t in o.fill_tokens(700, 13, 6000, cfg["vocabulary"])]
+    table = o.permutation(64, 13, 6001)[:48].copy()
+    chunks = [prompt[:256], prompt[256:512], prompt[512:700], [17], [4242]]
+    _run_sequence(model, backend, 16, chunks, table)
+
+
+def test_batched_prefill_and_decode_rows(torch_cuda):
+    """One forward call mixing two prefill chunks (ragged row blocks) with
+    decode rows, as the engine's batched steps do."""
+    cfg = smollm_config(layers=2, context=512)
+    model = OracleModel(cfg, seed=21)
+    bt, max_blocks = 16, 96
+    backend = HipBackend(cfg, block_tokens=bt, max_blocks=max_blocks, max_sequences=8)
+    upload_model(backend, model)
+    o = Oracle()
+    perm = o.permutation(max_blocks, 21, 7000)
+    n = pool_elements(cfg, bt, max_blocks)
+    keys = np.zeros(n, dtype=np.float32)
+    values = np.zeros(n, dtype=np.float32)
+    tables = [perm[24 * i: 24 * i + 24].copy() for i in range(4)]
+    for i, t in enumerate(tables):
+        backend.table_write(i, 0, t)
+    used = [0, 0, 0, 0]
+    plan = [[290, 45, 1, 17], [1, 1, 300, 1], [3, 1, 1, 20]]
+    for step, counts in enumerate(plan):
+        chunks = [[int(t) for t in o.fill_tokens(counts[i], 21, 7100 + 10 * step + i, cfg["vocabulary"])]
+                  for i in range(4)]
+        want = [model.append(keys, values, bt, tables[i], used[i], chunks[i]) for i in range(4)]
+        am, got = backend.forward([(i, used[i], counts[i]) for i in range(4)], [t for ch in chunks for t in ch])
+        for i in range(4):
+            _logits_match(got[i], want[i])
+            assert am[i] == int(np.argmax(want[i]))
+            used[i] += counts[i]

@@ -36,6 +36,14 @@ class Counters(ctypes.Structure):
         "block_table_device_bytes", "kv_pool_bytes", "forward_calls", "forward_rows", "cow_copies", "cow_bytes")]
 
 
+class KernelTimes(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint64) for n in (
+        "attention_ns", "attention_launches", "projection_ns", "projection_launches", "head_ns", "head_launches")]
+
+
+TIME_ATTENTION, TIME_PROJECTION, TIME_HEAD = 1, 2, 4
+
+
 class BackendError(RuntimeError):
     def __init__(self, status: int, message: str):
         super().__init__(message)
@@ -62,6 +70,8 @@ def _bind(lib):
     lib.mp_hip_kv_pools.argtypes = [vp, ctypes.POINTER(vp), ctypes.POINTER(vp), ctypes.POINTER(ctypes.c_size_t)]
     lib.mp_hip_stream.argtypes = [vp]
     lib.mp_hip_stream.restype = vp
+    lib.mp_hip_set_timing.argtypes = [vp, ctypes.c_uint32]
+    lib.mp_hip_kernel_times.argtypes = [vp, ctypes.POINTER(KernelTimes)]
     lib._mp_bound = True
     return lib
 
@@ -149,6 +159,21 @@ class HipBackend:
 
     def stream(self) -> int:
         return self.lib.mp_hip_stream(self.handle)
+
+
+def set_timing(handle: int, classes: int):
+    """Enables HIP-event timing of forward launches of a device context."""
+    status = lib().mp_hip_set_timing(handle, classes)
+    if status:
+        raise BackendError(status, lib().mp_hip_last_error(handle).decode())
+
+
+def kernel_times(handle: int) -> dict:
+    t = KernelTimes()
+    status = lib().mp_hip_kernel_times(handle, ctypes.byref(t))
+    if status:
+        raise BackendError(status, "mp_hip_kernel_times failed")
+    return {n: getattr(t, n) for n, _ in KernelTimes._fields_}
 
 
 def paged_attention_decode(q, keys, values, table, length: int, layer: int, layers: int, block_tokens: int,

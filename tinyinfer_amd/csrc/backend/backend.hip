@@ -60,6 +60,11 @@ struct mp_hip {
     int32_t* results = nullptr;  // argmax[seqs] | nonfinite[seqs]
     std::vector<int32_t> host_meta;
     std::vector<void*> allocations;
+    // kernel timing (mp_hip_set_timing): event pairs of one forward call
+    uint32_t timing = 0;
+    std::vector<hipEvent_t> events;
+    std::vector<uint32_t> spans;  // class of event pair i
+    mp_hip_timing_totals times{};
 };
 
 namespace {
@@ -179,7 +184,7 @@ int ensure_workspace(mp_hip* h, int rows, int seqs, int max_length) {
         {(void**)&h->ffn, sizeof(float) * R * (size_t)c.intermediate},
         {(void**)&h->last, sizeof(float) * S * hd},
         {(void**)&h->logits, sizeof(float) * S * (size_t)c.vocabulary},
-        {(void**)&h->meta, sizeof(int32_t) * (3 * (size_t)R + 2 * (size_t)S)},
+        {(void**)&h->meta, sizeof(int32_t) * (5 * (size_t)R + 2 * (size_t)S)},
         {(void**)&h->results, sizeof(int32_t) * 2 * (size_t)S},
     };
     size_t total = 0;
@@ -215,9 +220,11 @@ int mp_hip_create(const mp_model_desc* model, const mp_kv_desc* kv, mp_hip** out
     h->kv = *kv;
     const mp_model_desc& c = h->model;
     // Pages are streamed as float4 runs of tokens: the device path needs a
-    // page size that is a multiple of 4 tokens and fits one V batch buffer.
-    if (!valid_model(c) || kv->block_tokens < 4 || kv->block_tokens % 4 ||
-        kv->block_tokens * (c.hidden / c.heads) > 16384 || kv->max_blocks < 1 ||
+    // page size that is a multiple of 4 tokens and fits one V batch buffer,
+    // head_dim a multiple of 4 and at most 8 query heads per KV head.
+    if (!valid_model(c) || (c.hidden / c.heads) % 4 || c.heads / c.kv_heads > 8 ||
+        kv->block_tokens < 4 || kv->block_tokens % 4 ||
+        kv->block_tokens * (c.hidden / c.heads) > 8192 || kv->max_blocks < 1 ||
         kv->max_sequences < 1 || kv->max_sequence_blocks < 1 || kv->max_sequence_blocks > 2048) {
         delete h;
         return MP_INVALID_ARGUMENT;
@@ -284,6 +291,7 @@ int mp_hip_create(const mp_model_desc* model, const mp_kv_desc* kv, mp_hip** out
 int mp_hip_destroy(mp_hip* h) {
     if (!h) return MP_OK;
     if (h->stream) (void)hipStreamSynchronize(h->stream);
+    for (hipEvent_t ev : h->events) (void)hipEventDestroy(ev);
     for (void* p : h->allocations)
         if (p) (void)hipFree(p);
     if (h->stream) (void)hipStreamDestroy(h->stream);
@@ -434,9 +442,10 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
         if (tokens[i] < 0 || tokens[i] >= c.vocabulary) return fail(h, MP_INVALID_ARGUMENT, "invalid token");
     int status = ensure_workspace(h, R, nseq, max_length);
     if (status) return status;
-    // Row metadata: tokens | row_seq | row_pos | seq_slot | seq_last_row.
+    // Row metadata: tokens | row_seq | row_pos | seq_slot | seq_last_row |
+    // attention row blocks (first row, rows).
     auto& m = h->host_meta;
-    m.resize(3 * (size_t)R + 2 * (size_t)nseq + 1);
+    m.resize(5 * (size_t)R + 2 * (size_t)nseq + 1);
     int32_t* m_tokens = m.data();
     int32_t* m_seq = m_tokens + R;
     int32_t* m_pos = m_seq + R;
@@ -452,7 +461,15 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
         m_slot[s] = steps[s].table_slot;
         m_last[s] = r - 1;
     }
-    status = check(h, hipMemcpyAsync(h->meta, m.data(), sizeof(int32_t) * (3 * (size_t)R + 2 * (size_t)nseq),
+    const int block_rows = mphip::attention_row_block(c.heads, c.kv_heads, c.hidden / c.heads);
+    int32_t* m_blocks = m_last + nseq;
+    int nblocks = 0;
+    for (int s = 0, first = 0; s < nseq; first += steps[s].count, ++s)
+        for (int i = 0; i < steps[s].count; i += block_rows, ++nblocks) {
+            m_blocks[2 * nblocks] = first + i;
+            m_blocks[2 * nblocks + 1] = std::min(block_rows, steps[s].count - i);
+        }
+    status = check(h, hipMemcpyAsync(h->meta, m.data(), sizeof(int32_t) * (3 * (size_t)R + 2 * (size_t)nseq + 2 * (size_t)nblocks),
                                      hipMemcpyHostToDevice, h->stream), "upload input tokens");
     if (status) return status;
     h->stats.token_uploaded_bytes += sizeof(int32_t) * R;
@@ -462,22 +479,40 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
     mphip::PagedKv kv{h->keys, h->values, h->tables, h->kv.max_sequence_blocks,
                       c.layers, h->kv.block_tokens, kvw};
     const mphip::AttentionScratch scratch{h->scratch, h->scratch + (size_t)R * c.heads * score_stride(max_length),
-                                          score_stride(max_length), score_chunks(max_length)};
+                                          score_stride(max_length), score_chunks(max_length),
+                                          reinterpret_cast<const int2*>(h->meta + 3 * (size_t)R + 2 * (size_t)nseq),
+                                          nblocks};
     hipStream_t s = h->stream;
+    // Launches of an enabled timing class are bracketed by a pair of events
+    // from the pool that mp_hip_set_timing sized for one forward call.
+    h->spans.clear();
+    auto timed = [&](uint32_t cls, auto&& launch) -> hipError_t {
+        if (!(h->timing & cls)) return launch();
+        const size_t pair = 2 * h->spans.size();
+        hipError_t r = hipEventRecord(h->events[pair], s);
+        if (r == hipSuccess) r = launch();
+        if (r == hipSuccess) r = hipEventRecord(h->events[pair + 1], s);
+        h->spans.push_back(cls);
+        return r;
+    };
+    const uint32_t P = MP_TIME_PROJECTION, A = MP_TIME_ATTENTION;
     hipError_t e = mphip::launch_embed(s, h->embedding, meta.tokens, h->x, R, c.hidden);
     for (int l = 0; l < c.layers && e == hipSuccess; ++l) {
         e = mphip::launch_rms(s, h->x, c.hidden, nullptr, h->input_norm[l], h->xn, c.hidden, R, c.hidden, c.rms_epsilon);
-        if (e == hipSuccess) e = mphip::launch_gemm(s, mphip::kStore, h->xn, c.hidden, R, c.hidden, h->qkv[l], nullptr, qw, qw, h->qkv_out, qw);
+        if (e == hipSuccess) e = timed(P, [&] { return mphip::launch_gemm(s, mphip::kStore, h->xn, c.hidden, R, c.hidden, h->qkv[l], nullptr, qw, qw, h->qkv_out, qw); });
         if (e == hipSuccess) e = mphip::launch_rope_append(s, h->qkv_out, qw, R, c.heads, c.kv_heads, dim, h->cos_table, h->sin_table, meta, kv, l);
-        if (e == hipSuccess) e = mphip::launch_attention(s, h->qkv_out, qw, R, c.heads, c.kv_heads, dim, meta, kv, l, h->ctx, c.hidden, scratch);
-        if (e == hipSuccess) e = mphip::launch_gemm(s, mphip::kResidual, h->ctx, c.hidden, R, c.hidden, h->o[l], nullptr, c.hidden, c.hidden, h->x, c.hidden);
+        if (e == hipSuccess) e = timed(A, [&] { return mphip::launch_attention(s, h->qkv_out, qw, R, c.heads, c.kv_heads, dim, meta, kv, l, h->ctx, c.hidden, scratch); });
+        if (e == hipSuccess) e = timed(P, [&] { return mphip::launch_gemm(s, mphip::kResidual, h->ctx, c.hidden, R, c.hidden, h->o[l], nullptr, c.hidden, c.hidden, h->x, c.hidden); });
         if (e == hipSuccess) e = mphip::launch_rms(s, h->x, c.hidden, nullptr, h->post_norm[l], h->xn, c.hidden, R, c.hidden, c.rms_epsilon);
-        if (e == hipSuccess) e = mphip::launch_gemm(s, mphip::kSwiglu, h->xn, c.hidden, R, c.hidden, h->gate[l], h->up[l], c.intermediate, c.intermediate, h->ffn, c.intermediate);
-        if (e == hipSuccess) e = mphip::launch_gemm(s, mphip::kResidual, h->ffn, c.intermediate, R, c.intermediate, h->down[l], nullptr, c.hidden, c.hidden, h->x, c.hidden);
+        if (e == hipSuccess) e = timed(P, [&] { return mphip::launch_gemm(s, mphip::kSwiglu, h->xn, c.hidden, R, c.hidden, h->gate[l], h->up[l], c.intermediate, c.intermediate, h->ffn, c.intermediate); });
+        if (e == hipSuccess) e = timed(P, [&] { return mphip::launch_gemm(s, mphip::kResidual, h->ffn, c.intermediate, R, c.intermediate, h->down[l], nullptr, c.hidden, c.hidden, h->x, c.hidden); });
     }
-    if (e == hipSuccess) e = mphip::launch_rms(s, h->x, c.hidden, meta.seq_last_row, h->final_norm, h->last, c.hidden, nseq, c.hidden, c.rms_epsilon);
-    if (e == hipSuccess) e = mphip::launch_gemm(s, mphip::kStore, h->last, c.hidden, nseq, c.hidden, h->head, nullptr, c.vocabulary, c.vocabulary, h->logits, c.vocabulary);
-    if (e == hipSuccess) e = mphip::launch_argmax(s, h->logits, nseq, c.vocabulary, h->results, h->results + nseq);
+    if (e == hipSuccess) e = timed(MP_TIME_HEAD, [&] {
+        hipError_t r = mphip::launch_rms(s, h->x, c.hidden, meta.seq_last_row, h->final_norm, h->last, c.hidden, nseq, c.hidden, c.rms_epsilon);
+        if (r == hipSuccess) r = mphip::launch_gemm(s, mphip::kStore, h->last, c.hidden, nseq, c.hidden, h->head, nullptr, c.vocabulary, c.vocabulary, h->logits, c.vocabulary);
+        if (r == hipSuccess) r = mphip::launch_argmax(s, h->logits, nseq, c.vocabulary, h->results, h->results + nseq);
+        return r;
+    });
     if ((status = check(h, e, "model kernel launch"))) return status;
     std::vector<int32_t> results(2 * (size_t)nseq);
     status = check(h, hipMemcpyAsync(results.data(), h->results, sizeof(int32_t) * 2 * nseq, hipMemcpyDeviceToHost, s), "download argmax");
@@ -487,6 +522,16 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
     }
     if (!status) status = check(h, hipStreamSynchronize(s), "model completion");
     if (status) return status;
+    for (size_t i = 0; i < h->spans.size(); ++i) {
+        float ms = 0.0f;
+        if ((status = check(h, hipEventElapsedTime(&ms, h->events[2 * i], h->events[2 * i + 1]), "kernel timing")))
+            return status;
+        const uint64_t ns = (uint64_t)((double)ms * 1e6);
+        mp_hip_timing_totals& t = h->times;
+        if (h->spans[i] == MP_TIME_ATTENTION) t.attention_ns += ns, ++t.attention_launches;
+        if (h->spans[i] == MP_TIME_PROJECTION) t.projection_ns += ns, ++t.projection_launches;
+        if (h->spans[i] == MP_TIME_HEAD) t.head_ns += ns, ++t.head_launches;
+    }
     std::memcpy(argmax, results.data(), sizeof(int32_t) * nseq);
     if (nonfinite) std::memcpy(nonfinite, results.data() + nseq, sizeof(int32_t) * nseq);
     ++h->stats.forward_calls;
@@ -542,5 +587,27 @@ int mp_hip_kv_pools(const mp_hip* h, float** keys, float** values, size_t* eleme
 }
 
 void* mp_hip_stream(const mp_hip* h) { return h ? (void*)h->stream : nullptr; }
+
+int mp_hip_set_timing(mp_hip* h, uint32_t classes) {
+    if (!h || (classes & ~7u)) return fail(h, MP_INVALID_ARGUMENT, "invalid timing classes");
+    int status = mp_hip_sync(h);
+    if (status) return status;
+    // One pair per GEMM and attention of every layer plus the head.
+    const size_t need = 2 * (5 * (size_t)h->model.layers + 1);
+    while (h->events.size() < need) {
+        hipEvent_t ev = nullptr;
+        if ((status = check(h, hipEventCreate(&ev), "create timing event"))) return status;
+        h->events.push_back(ev);
+    }
+    h->timing = classes;
+    h->times = mp_hip_timing_totals{};
+    return MP_OK;
+}
+
+int mp_hip_kernel_times(const mp_hip* h, mp_hip_timing_totals* out) {
+    if (!h || !out) return MP_INVALID_ARGUMENT;
+    *out = h->times;
+    return MP_OK;
+}
 
 }  // extern "C"

@@ -53,7 +53,9 @@ hipError_t launch_rope_append(hipStream_t s, float* qkv, int ldqkv, int rows, in
                               int layer);
 
 // Causal GQA attention for every row in the reference two-pass softmax
-// order. q rows at qkv (stride ldq); out rows stride ldo. Scratch holds
+// order. q rows at qkv (stride ldq); out rows stride ldo. Rows are grouped
+// in `blocks` row blocks (first row, row count): consecutive positions of
+// one sequence, at most attention_row_block() rows each. Scratch holds
 // rows*heads score rows of `stride` floats (max length padded to 16) and
 // rows*heads*chunks chunk maxima (chunks = ceil(max length / 256)).
 struct AttentionScratch {
@@ -61,7 +63,10 @@ struct AttentionScratch {
     float* chunk_max;
     int stride;
     int chunks;
+    const int2* row_blocks;
+    int blocks;
 };
+int attention_row_block(int heads, int kv_heads, int dim);
 hipError_t launch_attention(hipStream_t s, const float* qkv, int ldq, int rows, int heads,
                             int kv_heads, int dim, const RowMeta& meta, const PagedKv& kv,
                             int layer, float* out, int ldo, const AttentionScratch& scratch);

@@ -614,76 +614,107 @@ __global__ __launch_bounds__(kAttentionThreads) void attention_single_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Forward attention as three kernels, same arithmetic as attention_row:
-//   scores  : grid (row, kv head, 256-token chunk) -- every K byte of a layer
-//             is requested at once; per-chunk maxima.
-//   softmax : grid (row, head) -- max of chunk maxima, e = expf(s - m),
+// Forward attention as three kernels over ROW BLOCKS. A row block is up to
+// kRowBlock consecutive rows (positions) of one sequence; decode rows are
+// blocks of one. Each block reads every K and V byte of its sequence once,
+// while every (row, head) keeps its own reference-order chains
+// (llama_runner.cpp:86-92):
+//   scores  : grid (block, kv head, 256-token chunk), thread = token;
+//             s = (sum_d q_d k_td, sequential d) / sqrt(dim) for each causal
+//             (row, head), plus per-chunk maxima.
+//   softmax : grid (row, head): max of chunk maxima, e = expf(s - m),
 //             sequential denominator, p = e / den (in place).
-//   pv      : grid (row, kv head) -- V pages streamed through a 2 x 64 KB
-//             LDS double buffer by all waves while the chain lanes
-//             (head, d) sum the previous batch in token order.
-// Score rows are `stride` floats (length padded to 16, padding zero).
+//   pv      : grid (block, kv head): V pages streamed through an LDS double
+//             buffer by all waves while each (row, head, d) chain sums its
+//             causal prefix in token order.
+// Score rows are `stride` floats (max length padded to 16, padding zero).
 constexpr int kScoreChunk = 256;
-constexpr int kPvBufferFloats = 16384;  // one V batch buffer (64 KB)
-constexpr int kPvMaxBatchTokens = 256;  // p values staged per head per batch
+constexpr int kMaxRowHeads = 48;       // rows x query heads of one block
+constexpr int kPvBatchFloats = 8192;   // one V batch buffer (32 KB)
+constexpr int kPvMaxBatchTokens = 128;
+constexpr int kPvMaxChains = 12;       // (row, head, d) chains per thread
+constexpr int kPvThreads = 256;
 
-template <int BT>
+__device__ __forceinline__ float wave_max(float v) {
+    for (int o = kWave / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+
+template <int BT, int DIM>
 __global__ __launch_bounds__(kScoreChunk) void attn_scores_kernel(
     const float* __restrict__ qkv, int ldq, int heads, int kv_heads, int dim, RowMeta meta,
-    PagedKv kv, int layer, float* __restrict__ scores, int stride, float* __restrict__ chunk_max,
-    int chunks) {
-    __shared__ float qs[kMaxGroup * kMaxDim];
-    __shared__ float reduce[kScoreChunk / kWave];
-    const int r = blockIdx.x, kh = blockIdx.y, chunk = blockIdx.z;
-    const int length = meta.row_pos[r] + 1;
-    if (chunk * kScoreChunk >= length) return;
+    PagedKv kv, int layer, const int2* __restrict__ blocks, float* __restrict__ scores, int stride,
+    float* __restrict__ chunk_max, int chunks) {
+    __shared__ float4 qs4[kPvMaxChains * kPvThreads / 4];
+    __shared__ float partial[kScoreChunk / kWave][kMaxRowHeads];
+    const int2 blk = blocks[blockIdx.x];
+    const int r0 = blk.x, nr = blk.y, kh = blockIdx.y, chunk = blockIdx.z;
+    const int pos0 = meta.row_pos[r0];
+    const int last_length = pos0 + nr;
+    if (chunk * kScoreChunk >= last_length) return;
+    if (DIM) dim = DIM;
     const int group = heads / kv_heads, tid = threadIdx.x;
+    const int rh = nr * group;
     const int bt = BT ? BT : kv.block_tokens;
-    const float* q = qkv + (size_t)r * ldq + (size_t)kh * group * dim;
-    const int32_t* table = kv.tables + (size_t)meta.seq_slot[meta.row_seq[r]] * kv.table_stride;
-    for (int i = tid; i < group * dim; i += kScoreChunk) qs[i] = q[i];
+    const int32_t* table = kv.tables + (size_t)meta.seq_slot[meta.row_seq[r0]] * kv.table_stride;
+    // q of the block's (row, head) pairs, row-major: rh x dim.
+    float* qs = reinterpret_cast<float*>(qs4);
+    for (int i = tid; i < rh * dim; i += kScoreChunk) {
+        const int r = i / (group * dim), rest = i - r * group * dim;
+        qs[i] = qkv[(size_t)(r0 + r) * ldq + (size_t)kh * group * dim + rest];
+    }
     __syncthreads();
     const int t = chunk * kScoreChunk + tid;
-    float s[kMaxGroup];
-    for (int h = 0; h < group; ++h) s[h] = -INFINITY;
-    if (t < length) {
-        const int page = t / bt, slot = t - page * bt;
-        const float* k = kv.keys +
-                         (((size_t)table[page] * kv.layers + layer) * bt + slot) * kv.kv_width +
-                         (size_t)kh * dim;
-        for (int h = 0; h < group; ++h) s[h] = 0.0f;
-        // All of a 64-wide block of the key row is requested before the
-        // dot products start.
-        for (int d0 = 0; d0 < dim; d0 += 64) {
-            float4 k4[16];
+    const bool live = t < last_length;
+    const int tc = live ? t : 0;
+    const int page = tc / bt, slot = tc - page * bt;
+    const float4* k4p = reinterpret_cast<const float4*>(
+        kv.keys + (((size_t)table[page] * kv.layers + layer) * bt + slot) * kv.kv_width + (size_t)kh * dim);
+    // Row r (relative to the block) sees token t when t <= pos0 + r.
+    const int ifirst = (t - pos0 > 0 ? t - pos0 : 0) * group;
+    const float root = sqrtf((float)dim);
+    const int wave = tid / kWave, lane = tid % kWave;
+    float4 kreg[DIM ? DIM / 4 : 1];
+    if (DIM) {
 #pragma unroll
-            for (int j = 0; j < 16; ++j)
-                k4[j] = d0 + 4 * j < dim ? *reinterpret_cast<const float4*>(k + d0 + 4 * j)
-                                         : make_float4(0.f, 0.f, 0.f, 0.f);
-            for (int h = 0; h < group; ++h) {
-                const float* qh = qs + h * dim + d0;
-                float acc = s[h];
+        for (int j = 0; j < DIM / 4; ++j) kreg[j] = k4p[j];
+    }
+    for (int i = 0; i < rh; ++i) {
+        const float4* q4 = qs4 + i * (dim / 4);
+        float acc = 0.0f;
+        if (DIM) {
 #pragma unroll
-                for (int j = 0; j < 16; ++j) {
-                    if (d0 + 4 * j >= dim) break;
-                    const float4 q4 = *reinterpret_cast<const float4*>(qh + 4 * j);
-                    acc = acc + q4.x * k4[j].x;
-                    acc = acc + q4.y * k4[j].y;
-                    acc = acc + q4.z * k4[j].z;
-                    acc = acc + q4.w * k4[j].w;
-                }
-                s[h] = acc;
+            for (int j = 0; j < DIM / 4; ++j) {
+                const float4 q = q4[j];
+                acc = acc + q.x * kreg[j].x;
+                acc = acc + q.y * kreg[j].y;
+                acc = acc + q.z * kreg[j].z;
+                acc = acc + q.w * kreg[j].w;
+            }
+        } else {
+            for (int j = 0; j < dim / 4; ++j) {
+                const float4 q = q4[j], k = k4p[j];
+                acc = acc + q.x * k.x;
+                acc = acc + q.y * k.y;
+                acc = acc + q.z * k.z;
+                acc = acc + q.w * k.w;
             }
         }
-        const float root = sqrtf((float)dim);
-        for (int h = 0; h < group; ++h) {
-            s[h] = s[h] / root;
-            scores[((size_t)r * heads + kh * group + h) * stride + t] = s[h];
+        const bool keep = live && i >= ifirst;
+        const float score = acc / root;
+        if (keep) {
+            const int r = i / group, h = i - r * group;
+            scores[((size_t)(r0 + r) * heads + kh * group + h) * stride + t] = score;
         }
+        const float m = wave_max(keep ? score : -INFINITY);
+        if (lane == 0) partial[wave][i] = m;
     }
-    for (int h = 0; h < group; ++h) {
-        const float m = block_max(s[h], reduce);
-        if (tid == 0) chunk_max[((size_t)r * heads + kh * group + h) * chunks + chunk] = m;
+    __syncthreads();
+    if (tid < rh) {
+        float m = partial[0][tid];
+        for (int w = 1; w < kScoreChunk / kWave; ++w) m = fmaxf(m, partial[w][tid]);
+        const int r = tid / group, h = tid - r * group;
+        chunk_max[((size_t)(r0 + r) * heads + kh * group + h) * chunks + chunk] = m;
     }
 }
 
@@ -704,16 +735,17 @@ __global__ __launch_bounds__(kSoftmaxThreads) void attn_softmax_kernel(
     float local = -INFINITY;
     for (int c = tid; c < used; c += kSoftmaxThreads) local = local < cm[c] ? cm[c] : local;
     const float m = block_max(local, reduce);
-    // e = expf(s - m) staged through LDS; the denominator runs in token order
-    // in one lane over each staged block.
+    // The row's own padded length; e = expf(s - m) staged through LDS, the
+    // denominator summed in token order in one lane per staged block.
+    const int row_stride = (length + 15) & ~15;
     float den = 0.0f;
-    for (int c0 = 0; c0 < stride; c0 += kSoftmaxStage) {
-        const int n = min(kSoftmaxStage, stride - c0);
+    for (int c0 = 0; c0 < row_stride; c0 += kSoftmaxStage) {
+        const int n = min(kSoftmaxStage, row_stride - c0);
         for (int i = tid; i < n; i += kSoftmaxThreads) {
             const int t = c0 + i;
             const float e = t < length ? ref_expf(row[t] - m) : 0.0f;
             stage[i] = e;
-            if (stride > kSoftmaxStage) row[t] = e;
+            if (row_stride > kSoftmaxStage) row[t] = e;
         }
         __syncthreads();
         if (tid == 0) den = sequential_sum(stage, n, den);
@@ -722,47 +754,46 @@ __global__ __launch_bounds__(kSoftmaxThreads) void attn_softmax_kernel(
     if (tid == 0) den_shared = den;
     __syncthreads();
     den = den_shared;
-    if (stride <= kSoftmaxStage) {
-        for (int t = tid; t < length; t += kSoftmaxThreads) row[t] = stage[t] / den;
+    if (row_stride <= kSoftmaxStage) {
+        for (int t = tid; t < row_stride; t += kSoftmaxThreads) row[t] = t < length ? stage[t] / den : 0.0f;
     } else {
-        for (int t = tid; t < length; t += kSoftmaxThreads) row[t] = row[t] / den;
+        for (int t = tid; t < row_stride; t += kSoftmaxThreads) row[t] = t < length ? row[t] / den : 0.0f;
     }
 }
-
-constexpr int kPvThreads = 256;
 
 template <int BT, int DIM>
 __global__ __launch_bounds__(kPvThreads) void attn_pv_kernel(
     const float* __restrict__ probs, int stride, int heads, int kv_heads, int dim, RowMeta meta,
-    PagedKv kv, int layer, float* __restrict__ out, int ldo) {
-    __shared__ float4 vbuf4[2][kPvBufferFloats / 4];
-    __shared__ float4 pbuf4[2][kMaxGroup * kPvMaxBatchTokens / 4];
+    PagedKv kv, int layer, const int2* __restrict__ blocks, float* __restrict__ out, int ldo) {
+    __shared__ float4 vbuf4[2][kPvBatchFloats / 4];
+    __shared__ float4 pbuf4[2][kMaxRowHeads * kPvMaxBatchTokens / 4];
     __shared__ int32_t lds_table[kLdsTable];
-    const int r = blockIdx.x, kh = blockIdx.y, tid = threadIdx.x;
-    const int group = heads / kv_heads;
+    __shared__ float totals[kPvMaxChains * kPvThreads];  // chain i of thread tid at i*256+tid
+    if (DIM) dim = DIM;
+    const int2 blk = blocks[blockIdx.x];
+    const int r0 = blk.x, nr = blk.y, kh = blockIdx.y, tid = threadIdx.x;
+    const int group = heads / kv_heads, rh = nr * group;
     const int bt = BT ? BT : kv.block_tokens;
-    const int length = meta.row_pos[r] + 1;
-    const int pages = (length + bt - 1) / bt;
-    const int32_t* table = kv.tables + (size_t)meta.seq_slot[meta.row_seq[r]] * kv.table_stride;
+    const int pos0 = meta.row_pos[r0];
+    const int last_length = pos0 + nr;
+    const int pages = (last_length + bt - 1) / bt;
+    const int32_t* table = kv.tables + (size_t)meta.seq_slot[meta.row_seq[r0]] * kv.table_stride;
     // Page table in LDS (at most kLdsTable pages, checked by the host), so V
     // addresses never wait on a global load.
     for (int i = tid; i < pages; i += kPvThreads) lds_table[i] = table[i];
     __syncthreads();
-    // Pages per batch: bounded by the V buffer and by the staged p rows.
-    int batch_pages = kPvBufferFloats / (bt * dim);
+    int batch_pages = kPvBatchFloats / (bt * dim);
     if (batch_pages * bt > kPvMaxBatchTokens) batch_pages = kPvMaxBatchTokens / bt;
     const int batch_tokens = batch_pages * bt;
     const int batches = (pages + batch_pages - 1) / batch_pages;
     const int vec_per_token = dim / 4;
     const int vec_per_batch = batch_tokens * vec_per_token;
-    const float* prow = probs + ((size_t)r * heads + (size_t)kh * group) * stride;
-    // Loader: each thread carries up to kLoads float4 of V for the next batch.
-    constexpr int kLoads = kPvBufferFloats / 4 / kPvThreads;  // 16
-    float4 vreg[kLoads];
-    float4 preg[(kMaxGroup * kPvMaxBatchTokens / 4 + kPvThreads - 1) / kPvThreads];
-    // Fast layout (16-token pages, head_dim 64): thread element j is token
-    // 16*j + tid/16 of the batch, float4 tid%16 of its row, i.e. page
-    // batch*16 + j at slot tid/16, read from a wave-uniform page base.
+    const int pvec_per_row = batch_tokens / 4;
+    constexpr int kLoads = kPvBatchFloats / 4 / kPvThreads;                        // 8
+    constexpr int kPLoads = kMaxRowHeads * kPvMaxBatchTokens / 4 / kPvThreads;     // 6
+    float4 vreg[kLoads], preg[kPLoads];
+    // Fast layout (16-token pages, head_dim 64): thread element j is page
+    // batch*8 + j, slot tid/16, float4 tid%16, from a wave-uniform page base.
     constexpr bool kFast = BT == 16 && DIM == 64;
     const uint32_t fast_off = (uint32_t)(tid / 16) * (uint32_t)kv.kv_width + 4u * (uint32_t)(tid % 16);
     auto fetch = [&](int batch) {
@@ -782,7 +813,7 @@ __global__ __launch_bounds__(kPvThreads) void attn_pv_kernel(
                 const int e = tid + j * kPvThreads;
                 const int tok = e / vec_per_token, d4 = e - tok * vec_per_token;
                 const int t = t0 + tok;
-                const bool in = e < vec_per_batch && t < length;
+                const bool in = e < vec_per_batch && t < last_length;
                 const int tc = in ? t : 0;
                 const int page = tc / bt, slot = tc - page * bt;
                 vreg[j] = *reinterpret_cast<const float4*>(
@@ -790,20 +821,20 @@ __global__ __launch_bounds__(kPvThreads) void attn_pv_kernel(
                     (size_t)kh * dim + 4 * (in ? d4 : 0));
             }
         }
-        const int pvec = group * batch_tokens / 4;
 #pragma unroll
-        for (int j = 0; j < (int)(sizeof(preg) / sizeof(preg[0])); ++j) {
+        for (int j = 0; j < kPLoads; ++j) {
             const int e = tid + j * kPvThreads;
-            const int h = e / (batch_tokens / 4), i4 = e - h * (batch_tokens / 4);
-            const bool in = e < pvec && t0 + 4 * i4 < stride;
-            preg[j] = *reinterpret_cast<const float4*>(prow + (in ? (size_t)h * stride + t0 + 4 * i4 : 0));
+            const int i = e / pvec_per_row, i4 = e - i * pvec_per_row;  // (row, head), token quad
+            const int r = i / group, h = i - r * group;
+            const bool in = i < rh && t0 + 4 * i4 < stride;
+            preg[j] = *reinterpret_cast<const float4*>(
+                probs + (in ? ((size_t)(r0 + r) * heads + kh * group + h) * stride + t0 + 4 * i4 : 0));
         }
     };
-    // Masks are applied here, after every load of the batch is in flight;
-    // only a batch that runs past the row's length needs them.
+    // Masks are applied here, after every load of the batch is in flight.
     auto stash = [&](int batch, int buffer) {
         const int t0 = batch * batch_tokens;
-        const bool whole = kFast && t0 + batch_tokens <= length;
+        const bool whole = kFast && t0 + batch_tokens <= last_length;
 #pragma unroll
         for (int j = 0; j < kLoads; ++j) {
             const int e = tid + j * kPvThreads;
@@ -811,52 +842,49 @@ __global__ __launch_bounds__(kPvThreads) void attn_pv_kernel(
                 vbuf4[buffer][e] = vreg[j];
             } else {
                 const int tok = e / vec_per_token;
-                vbuf4[buffer][e] = keep_if(vreg[j], mask_of(e < vec_per_batch && t0 + tok < length));
+                vbuf4[buffer][e] = keep_if(vreg[j], mask_of(e < vec_per_batch && t0 + tok < last_length));
             }
         }
-        const int pvec = group * batch_tokens / 4;
 #pragma unroll
-        for (int j = 0; j < (int)(sizeof(preg) / sizeof(preg[0])); ++j) {
+        for (int j = 0; j < kPLoads; ++j) {
             const int e = tid + j * kPvThreads;
-            const int h = e / (batch_tokens / 4), i4 = e - h * (batch_tokens / 4);
-            if (e < kMaxGroup * kPvMaxBatchTokens / 4)
-                pbuf4[buffer][e] = keep_if(preg[j], mask_of(e < pvec && t0 + 4 * i4 < stride));
+            const int i = e / pvec_per_row, i4 = e - i * pvec_per_row;
+            pbuf4[buffer][e] = keep_if(preg[j], mask_of(i < rh && t0 + 4 * i4 < stride));
         }
     };
-    constexpr int kMaxChains = kMaxGroup * kMaxDim / kPvThreads;
-    float total[kMaxChains];
-#pragma unroll
-    for (int i = 0; i < kMaxChains; ++i) total[i] = 0.0f;
+    const int chains = rh * dim;
+    for (int i = 0; i < kPvMaxChains; ++i) totals[i * kPvThreads + tid] = 0.0f;
     fetch(0);
     stash(0, 0);
     __syncthreads();
     for (int b = 0; b < batches; ++b) {
         const int buffer = b & 1;
+        const int t0 = b * batch_tokens;
         if (b + 1 < batches) fetch(b + 1);
-        const int n = min(batch_tokens, length - b * batch_tokens);
         const float* vb = reinterpret_cast<const float*>(vbuf4[buffer]);
         const float* pb = reinterpret_cast<const float*>(pbuf4[buffer]);
-#pragma unroll
-        for (int i = 0; i < kMaxChains; ++i) {
+        for (int i = 0; i < kPvMaxChains; ++i) {
             const int chain = tid + i * kPvThreads;
-            if (chain >= group * dim) break;
-            const int h = chain / dim, d = chain - h * dim;
-            const float* ph = pb + h * batch_tokens;
-            const float* vd = vb + d;
-            float acc = total[i];
-            float dummy = 0.0f;
-            chain_dot<false, 0>(ph, vd, nullptr, n, acc, dummy, dim);
-            total[i] = acc;
+            if (chain >= chains) break;
+            const int rhi = chain / dim, d = chain - rhi * dim;
+            const int r = rhi / group;
+            // Causal: row r attends tokens [0, pos0 + r].
+            const int n = min(batch_tokens, pos0 + r + 1 - t0);
+            if (n <= 0) continue;
+            float acc = totals[i * kPvThreads + tid];
+            float unused = 0.0f;
+            chain_dot<false, DIM>(pb + rhi * batch_tokens, vb + d, nullptr, n, acc, unused, dim);
+            totals[i * kPvThreads + tid] = acc;
         }
         if (b + 1 < batches) stash(b + 1, buffer ^ 1);
         __syncthreads();
     }
-#pragma unroll
-    for (int i = 0; i < kMaxChains; ++i) {
+    for (int i = 0; i < kPvMaxChains; ++i) {
         const int chain = tid + i * kPvThreads;
-        if (chain >= group * dim) break;
-        const int h = chain / dim, d = chain - h * dim;
-        out[(size_t)r * ldo + ((size_t)kh * group + h) * dim + d] = total[i];
+        if (chain >= chains) break;
+        const int rhi = chain / dim, d = chain - rhi * dim;
+        const int r = rhi / group, h = rhi - r * group;
+        out[(size_t)(r0 + r) * ldo + ((size_t)kh * group + h) * dim + d] = totals[i * kPvThreads + tid];
     }
 }
 
@@ -998,25 +1026,32 @@ hipError_t launch_rope_append(hipStream_t s, float* qkv, int ldqkv, int rows, in
     return hipGetLastError();
 }
 
+int attention_row_block(int heads, int kv_heads, int dim) {
+    const int group = heads / kv_heads;
+    int rows = kMaxRowHeads / group;
+    if (rows * group * dim > kPvMaxChains * kPvThreads) rows = kPvMaxChains * kPvThreads / (group * dim);
+    return rows < 16 ? rows : 16;
+}
+
 hipError_t launch_attention(hipStream_t s, const float* qkv, int ldq, int rows, int heads,
                             int kv_heads, int dim, const RowMeta& meta, const PagedKv& kv,
                             int layer, float* out, int ldo, const AttentionScratch& scratch) {
     if (rows <= 0) return hipSuccess;
-    if (heads / kv_heads > kMaxGroup || dim > kMaxDim || dim % 4 || kv.block_tokens * dim > kPvBufferFloats)
+    const int group = heads / kv_heads;
+    if (group > kMaxGroup || dim > kMaxDim || dim % 4 || group * dim > kPvMaxChains * kPvThreads ||
+        kv.block_tokens * dim > kPvBatchFloats)
         return hipErrorInvalidValue;
-    const dim3 sgrid(rows, kv_heads, scratch.chunks);
-    if (kv.block_tokens == 16)
-        attn_scores_kernel<16><<<sgrid, kScoreChunk, 0, s>>>(qkv, ldq, heads, kv_heads, dim, meta, kv, layer, scratch.scores, scratch.stride, scratch.chunk_max, scratch.chunks);
+    const dim3 sgrid(scratch.blocks, kv_heads, scratch.chunks);
+    if (kv.block_tokens == 16 && dim == 64)
+        attn_scores_kernel<16, 64><<<sgrid, kScoreChunk, 0, s>>>(qkv, ldq, heads, kv_heads, dim, meta, kv, layer, scratch.row_blocks, scratch.scores, scratch.stride, scratch.chunk_max, scratch.chunks);
     else
-        attn_scores_kernel<0><<<sgrid, kScoreChunk, 0, s>>>(qkv, ldq, heads, kv_heads, dim, meta, kv, layer, scratch.scores, scratch.stride, scratch.chunk_max, scratch.chunks);
+        attn_scores_kernel<0, 0><<<sgrid, kScoreChunk, 0, s>>>(qkv, ldq, heads, kv_heads, dim, meta, kv, layer, scratch.row_blocks, scratch.scores, scratch.stride, scratch.chunk_max, scratch.chunks);
     attn_softmax_kernel<<<dim3(rows, heads), kSoftmaxThreads, 0, s>>>(scratch.scores, scratch.stride, scratch.chunk_max, scratch.chunks, meta, heads);
-    if (kv.block_tokens == 16)
-        if (dim == 64)
-            attn_pv_kernel<16, 64><<<dim3(rows, kv_heads), kPvThreads, 0, s>>>(scratch.scores, scratch.stride, heads, kv_heads, dim, meta, kv, layer, out, ldo);
-        else
-            attn_pv_kernel<16, 0><<<dim3(rows, kv_heads), kPvThreads, 0, s>>>(scratch.scores, scratch.stride, heads, kv_heads, dim, meta, kv, layer, out, ldo);
+    const dim3 pgrid(scratch.blocks, kv_heads);
+    if (kv.block_tokens == 16 && dim == 64)
+        attn_pv_kernel<16, 64><<<pgrid, kPvThreads, 0, s>>>(scratch.scores, scratch.stride, heads, kv_heads, dim, meta, kv, layer, scratch.row_blocks, out, ldo);
     else
-        attn_pv_kernel<0, 0><<<dim3(rows, kv_heads), kPvThreads, 0, s>>>(scratch.scores, scratch.stride, heads, kv_heads, dim, meta, kv, layer, out, ldo);
+        attn_pv_kernel<0, 0><<<pgrid, kPvThreads, 0, s>>>(scratch.scores, scratch.stride, heads, kv_heads, dim, meta, kv, layer, scratch.row_blocks, out, ldo);
     return hipGetLastError();
 }
 

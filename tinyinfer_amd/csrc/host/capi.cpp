@@ -274,6 +274,12 @@ int mpx_runner_sequence(const void* runner, const char* id, int32_t* blocks, int
     });
 }
 
+void* mpx_runner_device(void* runner) {
+    void* out = nullptr;
+    if (guarded([&] { out = mpx::device_of(runner_of(runner)); })) return nullptr;
+    return out;
+}
+
 void* mpx_engine_create(void* runner, int32_t max_batch_size, int32_t token_budget, int32_t prefill_chunk,
                         int32_t context) {
     EngineBox* out = nullptr;

@@ -5,6 +5,7 @@
 
 namespace miniprefix {
 bool hip_runner_sequence(const ModelRunner& runner, const RequestId& id, const PagedSequence** out);
+void* hip_runner_device(ModelRunner& runner);
 }
 
 namespace mpx {
@@ -49,5 +50,7 @@ bool sequence_of(const miniprefix::ModelRunner& runner, const std::string& id, s
     *used = s->used;
     return true;
 }
+
+void* device_of(miniprefix::ModelRunner& runner) { return miniprefix::hip_runner_device(runner); }
 
 }  // namespace mpx

@@ -22,5 +22,7 @@ std::unique_ptr<miniprefix::ModelRunner> make_runner(int kind, std::shared_ptr<m
 void set_batching(miniprefix::Engine& engine, bool enabled);
 // Committed page table of a sequence, when the runner exposes it.
 bool sequence_of(const miniprefix::ModelRunner& runner, const std::string& id, std::vector<int>* blocks, int* used);
+// The runner's device context, or nullptr.
+void* device_of(miniprefix::ModelRunner& runner);
 
 }  // namespace mpx

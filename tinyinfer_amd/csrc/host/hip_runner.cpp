@@ -183,6 +183,7 @@ public:
 
     // Committed page table of a sequence (tests compare it with the reference's).
     const PagedSequence& sequence(const RequestId& id) const { return kv_.sequence(id); }
+    mp_hip* device() { return device_; }
 
 private:
     static constexpr int kMaxSequences = 1024;
@@ -275,6 +276,12 @@ bool hip_runner_sequence(const ModelRunner& runner, const RequestId& id, const P
     if (!hip) return false;
     *out = &hip->sequence(id);
     return true;
+}
+
+// Device context of a runner built by make_hip_runner.
+void* hip_runner_device(ModelRunner& runner) {
+    auto* hip = dynamic_cast<HipRunner*>(&runner);
+    return hip ? hip->device() : nullptr;
 }
 
 }  // namespace miniprefix

@@ -80,6 +80,7 @@ def bind(lib: ctypes.CDLL) -> ctypes.CDLL:
         "mpx_runner_cost_stats": ([vp, U64P], ctypes.c_int),
         "mpx_runner_set_cost_timing": ([vp, i32], ctypes.c_int),
         "mpx_runner_sequence": ([vp, c, I32P, i32, I32P, I32P], ctypes.c_int),
+        "mpx_runner_device": ([vp], vp),
         "mpx_engine_create": ([vp, i32, i32, i32, i32], vp),
         "mpx_engine_free": ([vp], None),
         "mpx_engine_set_batching": ([vp, i32], ctypes.c_int),
@@ -242,6 +243,10 @@ class Runner:
 
     def set_cost_timing(self, enabled: bool):
         _check(self.lib, self.lib.mpx_runner_set_cost_timing(self.handle, int(enabled)))
+
+    def device(self) -> int | None:
+        """The runner's device context (mp_hip*), or None."""
+        return self.lib.mpx_runner_device(self.handle)
 
     def sequence(self, rid: str) -> tuple[list[int], int]:
         """(page table, used tokens) of a committed sequence."""
