@@ -155,3 +155,30 @@ def test_batched_prefill_and_decode_rows(torch_cuda):
             _logits_match(got[i], want[i])
             assert am[i] == int(np.argmax(want[i]))
             used[i] += counts[i]
+
+
+@pytest.mark.parametrize("shape", ["paged16_dim64", "tiny_generic"])
+def test_long_context_softmax_windows(torch_cuda, shape):
+    """Rows longer than one 2048-token softmax window: the denominators are
+    summed over several staged windows and e_t is formed again per window
+    (prefill row blocks with every head of a group in one task, then decode
+    rows), on the 16-token page / dim-64 path and on the generic path."""
+    if shape == "paged16_dim64":
+        cfg = dict(layers=1, hidden=192, intermediate=256, heads=3, kv_heads=1, vocabulary=512, context=2720,
+                   eos=0, rms_epsilon=1e-5, rope_theta=100000.0, tied=1)
+        bt, chunks = 16, [1100, 1100, 500, 1, 1]
+    else:
+        cfg = tiny_config(context=2600)
+        bt, chunks = 4, [1000, 1100, 300, 1, 1]
+    model = OracleModel(cfg, seed=31)
+    pages = (cfg["context"] + bt - 1) // bt
+    backend = HipBackend(cfg, block_tokens=bt, max_blocks=pages + 8, max_sequences=2)
+    upload_model(backend, model)
+    o = Oracle()
+    table = o.permutation(pages + 8, 31, 8000)[:pages].copy()
+    tokens = [int(t) for t in o.fill_tokens(sum(chunks), 31, 8001, cfg["vocabulary"])]
+    split, at = [], 0
+    for n in chunks:
+        split.append(tokens[at:at + n])
+        at += n
+    _run_sequence(model, backend, bt, split, table)

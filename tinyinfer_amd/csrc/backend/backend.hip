@@ -1,13 +1,16 @@
 // C ABI of the MI355X device backend (include/mp_hip.h).
 //
-// One context owns: the resident weights (Q|K|V concatenated per layer into a
-// [hidden, q+2kv] matrix, everything else as the reference stores it, plus a
-// [hidden, vocab] head), the K and V page pools, the block-table arena, the
-// RoPE cos/sin table, a grow-only workspace and one stream. It corresponds to
+// One context owns: the resident weights, every projection stored transposed
+// ([out][in]; Q|K|V concatenated per layer into one [q+2kv][hidden] matrix;
+// the tied LM head is the embedding itself, which already is [vocab][hidden]),
+// the K and V page pools, the block-table arena, the RoPE cos/sin table, a
+// grow-only workspace (activations in the row-tile quad layout of layout.h)
+// and one stream. It corresponds to
 // the device half of CudaRunner (miniprefix/src/backend/cuda/llama_runner.cu:51-186)
 // and its resources (resources.cpp:13-45).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -17,6 +20,7 @@
 
 #include "../../../include/mp_hip.h"
 #include "kernels.h"
+#include "layout.h"
 
 namespace {
 
@@ -38,7 +42,7 @@ struct mp_hip {
     mp_hip_counters stats{};
     // weights
     float* embedding = nullptr;      // [vocab, hidden]
-    float* head = nullptr;           // [hidden, vocab]
+    float* head = nullptr;           // [vocab, hidden]: the embedding when tied
     float* final_norm = nullptr;     // [hidden]
     std::vector<float*> input_norm, post_norm, qkv, o, gate, up, down;
     std::vector<unsigned char> uploaded;  // per (layer, slot) + model tensors
@@ -56,7 +60,13 @@ struct mp_hip {
     float *x = nullptr, *xn = nullptr, *qkv_out = nullptr, *ctx = nullptr, *ffn = nullptr;
     float *last = nullptr, *logits = nullptr, *scratch = nullptr;
     size_t scratch_floats = 0;
-    int32_t* meta = nullptr;  // tokens | row_seq | row_pos | seq_slot | seq_last_row
+    float* best_value = nullptr;  // LM-head partials [seqs][groups]
+    int32_t* best_index = nullptr;
+    int32_t* best_bad = nullptr;
+    float* staging = nullptr;  // weight upload staging (grow-only)
+    size_t staging_floats = 0;
+    int32_t* meta = nullptr;  // tokens | row_seq | row_pos | seq_slot | seq_last_row | blocks | items
+    size_t meta_capacity = 0;   // int32 entries
     int32_t* results = nullptr;  // argmax[seqs] | nonfinite[seqs]
     std::vector<int32_t> host_meta;
     std::vector<void*> allocations;
@@ -166,15 +176,17 @@ int ensure_workspace(mp_hip* h, int rows, int seqs, int max_length) {
         return MP_OK;
     int status = mp_hip_sync(h);
     if (status) return status;
-    const int R = rows > h->workspace_rows ? rows : h->workspace_rows;
-    const int S = seqs > h->workspace_seqs ? seqs : h->workspace_seqs;
+    // Whole row tiles, so every quad-layout tile a kernel touches exists.
+    const int R = ((rows > h->workspace_rows ? rows : h->workspace_rows) + 63) / 64 * 64;
+    const int S = ((seqs > h->workspace_seqs ? seqs : h->workspace_seqs) + 63) / 64 * 64;
     for (void* p : {(void*)h->x, (void*)h->xn, (void*)h->qkv_out, (void*)h->ctx, (void*)h->ffn,
-                    (void*)h->last, (void*)h->logits, (void*)h->meta, (void*)h->results})
+                    (void*)h->last, (void*)h->logits, (void*)h->results,
+                    (void*)h->best_value, (void*)h->best_index, (void*)h->best_bad})
         device_free(h, p);
-    h->x = h->xn = h->qkv_out = h->ctx = h->ffn = h->last = h->logits = nullptr;
-    h->meta = h->results = nullptr;
+    h->x = h->xn = h->qkv_out = h->ctx = h->ffn = h->last = h->logits = h->best_value = nullptr;
+    h->results = h->best_index = h->best_bad = nullptr;
     h->workspace_rows = h->workspace_seqs = 0;
-    const size_t hd = c.hidden;
+    const size_t hd = c.hidden, groups = mphip::head_groups(c.vocabulary);
     struct Item { void** p; size_t bytes; };
     const Item items[] = {
         {(void**)&h->x, sizeof(float) * R * hd},
@@ -184,14 +196,25 @@ int ensure_workspace(mp_hip* h, int rows, int seqs, int max_length) {
         {(void**)&h->ffn, sizeof(float) * R * (size_t)c.intermediate},
         {(void**)&h->last, sizeof(float) * S * hd},
         {(void**)&h->logits, sizeof(float) * S * (size_t)c.vocabulary},
-        {(void**)&h->meta, sizeof(int32_t) * (5 * (size_t)R + 2 * (size_t)S)},
         {(void**)&h->results, sizeof(int32_t) * 2 * (size_t)S},
+        {(void**)&h->best_value, sizeof(float) * S * groups},
+        {(void**)&h->best_index, sizeof(int32_t) * S * groups},
+        {(void**)&h->best_bad, sizeof(int32_t) * S * groups},
     };
     size_t total = 0;
     for (const auto& it : items) {
         if ((status = device_alloc(h, it.p, it.bytes, "allocate workspace"))) return status;
         total += it.bytes;
     }
+    // Padding rows of the activation tiles are read (never stored) by the
+    // projections: start them finite.
+    for (void* p : {(void*)h->x, (void*)h->xn, (void*)h->qkv_out, (void*)h->ctx, (void*)h->ffn, (void*)h->last})
+        if ((status = check(h, hipMemsetAsync(p, 0, p == h->last ? sizeof(float) * S * hd
+                                                   : p == h->qkv_out ? sizeof(float) * R * (size_t)qkv_width(c)
+                                                   : p == h->ffn ? sizeof(float) * R * (size_t)c.intermediate
+                                                                 : sizeof(float) * R * hd, h->stream),
+                            "clear workspace")))
+            return status;
     if (need_scratch > h->scratch_floats) {
         device_free(h, h->scratch);
         h->scratch = nullptr;
@@ -207,6 +230,21 @@ int ensure_workspace(mp_hip* h, int rows, int seqs, int max_length) {
     return MP_OK;
 }
 
+// Grow-only per-call metadata (int32 entries).
+int ensure_call_buffers(mp_hip* h, size_t meta_entries) {
+    int status = MP_OK;
+    if (meta_entries > h->meta_capacity) {
+        if ((status = mp_hip_sync(h))) return status;
+        device_free(h, h->meta);
+        h->meta = nullptr;
+        h->meta_capacity = 0;
+        const size_t cap = meta_entries + meta_entries / 2;
+        if ((status = device_alloc(h, (void**)&h->meta, sizeof(int32_t) * cap, "allocate call metadata"))) return status;
+        h->meta_capacity = cap;
+    }
+    return status;
+}
+
 }  // namespace
 
 extern "C" {
@@ -220,9 +258,12 @@ int mp_hip_create(const mp_model_desc* model, const mp_kv_desc* kv, mp_hip** out
     h->kv = *kv;
     const mp_model_desc& c = h->model;
     // Pages are streamed as float4 runs of tokens: the device path needs a
-    // page size that is a multiple of 4 tokens and fits one V batch buffer,
-    // head_dim a multiple of 4 and at most 8 query heads per KV head.
-    if (!valid_model(c) || (c.hidden / c.heads) % 4 || c.heads / c.kv_heads > 8 ||
+    // page size that is a multiple of 4 tokens, head_dim a multiple of 4 and
+    // at most 64 (one output lane per d) and at most 8 query heads per KV
+    // head; the quad activation layout needs hidden and intermediate
+    // multiples of 4.
+    if (!valid_model(c) || (c.hidden / c.heads) % 4 || c.hidden / c.heads > 64 || c.hidden % 4 ||
+        c.intermediate % 4 || c.heads / c.kv_heads > 8 ||
         kv->block_tokens < 4 || kv->block_tokens % 4 ||
         kv->block_tokens * (c.hidden / c.heads) > 8192 || kv->max_blocks < 1 ||
         kv->max_sequences < 1 || kv->max_sequence_blocks < 1 || kv->max_sequence_blocks > 2048) {
@@ -247,7 +288,8 @@ int mp_hip_create(const mp_model_desc* model, const mp_kv_desc* kv, mp_hip** out
         if (!status) h->stats.device_weight_bytes += elements * sizeof(float);
     };
     alloc_weights(&h->embedding, (size_t)c.vocabulary * hd);
-    alloc_weights(&h->head, (size_t)c.vocabulary * hd);
+    if (c.tied) h->head = h->embedding;
+    else alloc_weights(&h->head, (size_t)c.vocabulary * hd);
     alloc_weights(&h->final_norm, hd);
     for (int l = 0; l < c.layers; ++l) {
         alloc_weights(&h->input_norm[l], hd);
@@ -313,39 +355,39 @@ int mp_hip_upload_tensor(mp_hip* h, int32_t layer, int32_t slot, const float* da
     for (size_t i = 0; i < count; ++i)
         if (!std::isfinite(data[i])) return fail(h, MP_INVALID_ARGUMENT, "nonfinite weights");
     const size_t bytes = count * sizeof(float);
-    const size_t hd = c.hidden, kvw = kv_width(c), qw = qkv_width(c);
+    const int hd = c.hidden, kvw = kv_width(c), in = c.intermediate;
     hipError_t e = hipSuccess;
     const hipMemcpyKind h2d = hipMemcpyHostToDevice;
-    if (layer < 0) {
-        if (slot == MP_TENSOR_EMBEDDING) {
-            e = hipMemcpyAsync(h->embedding, data, bytes, h2d, h->stream);
-            // Tied head: the [hidden, vocab] transpose of the embedding, read
-            // with the same sequential-k order as the reference's packed
-            // transposed RHS (matmul_kernel.cpp:172-189).
-            if (e == hipSuccess && c.tied)
-                e = mphip::launch_transpose(h->stream, h->embedding, h->head, c.vocabulary, c.hidden);
-        } else if (slot == MP_TENSOR_FINAL_NORM) {
-            e = hipMemcpyAsync(h->final_norm, data, bytes, h2d, h->stream);
-        } else {
-            e = hipMemcpyAsync(h->head, data, bytes, h2d, h->stream);
+    // Projections arrive [in][out] (model.cpp:33-37) and are stored [out][in]
+    // through a staging buffer; norms and the embedding are stored as given.
+    auto transposed = [&](float* dst, int rows, int cols) -> hipError_t {
+        if (h->staging_floats < count) {
+            device_free(h, h->staging);
+            h->staging = nullptr;
+            h->staging_floats = 0;
+            if (device_alloc(h, (void**)&h->staging, bytes, "allocate upload staging")) return hipErrorOutOfMemory;
+            h->staging_floats = count;
         }
+        hipError_t r = hipMemcpyAsync(h->staging, data, bytes, h2d, h->stream);
+        if (r == hipSuccess) r = mphip::launch_transpose(h->stream, h->staging, dst, rows, cols, rows);
+        return r;
+    };
+    if (layer < 0) {
+        if (slot == MP_TENSOR_EMBEDDING) e = hipMemcpyAsync(h->embedding, data, bytes, h2d, h->stream);
+        else if (slot == MP_TENSOR_FINAL_NORM) e = hipMemcpyAsync(h->final_norm, data, bytes, h2d, h->stream);
+        else e = transposed(h->head, hd, c.vocabulary);
     } else {
+        float* qkv = h->qkv[layer];
         switch (slot) {
         case MP_TENSOR_INPUT_NORM: e = hipMemcpyAsync(h->input_norm[layer], data, bytes, h2d, h->stream); break;
         case MP_TENSOR_POST_NORM: e = hipMemcpyAsync(h->post_norm[layer], data, bytes, h2d, h->stream); break;
-        case MP_TENSOR_Q:
-            e = hipMemcpy2DAsync(h->qkv[layer], qw * 4, data, hd * 4, hd * 4, hd, h2d, h->stream);
-            break;
-        case MP_TENSOR_K:
-            e = hipMemcpy2DAsync(h->qkv[layer] + hd, qw * 4, data, kvw * 4, kvw * 4, hd, h2d, h->stream);
-            break;
-        case MP_TENSOR_V:
-            e = hipMemcpy2DAsync(h->qkv[layer] + hd + kvw, qw * 4, data, kvw * 4, kvw * 4, hd, h2d, h->stream);
-            break;
-        case MP_TENSOR_O: e = hipMemcpyAsync(h->o[layer], data, bytes, h2d, h->stream); break;
-        case MP_TENSOR_GATE: e = hipMemcpyAsync(h->gate[layer], data, bytes, h2d, h->stream); break;
-        case MP_TENSOR_UP: e = hipMemcpyAsync(h->up[layer], data, bytes, h2d, h->stream); break;
-        case MP_TENSOR_DOWN: e = hipMemcpyAsync(h->down[layer], data, bytes, h2d, h->stream); break;
+        case MP_TENSOR_Q: e = transposed(qkv, hd, hd); break;
+        case MP_TENSOR_K: e = transposed(qkv + (size_t)hd * hd, hd, kvw); break;
+        case MP_TENSOR_V: e = transposed(qkv + (size_t)(hd + kvw) * hd, hd, kvw); break;
+        case MP_TENSOR_O: e = transposed(h->o[layer], hd, hd); break;
+        case MP_TENSOR_GATE: e = transposed(h->gate[layer], hd, in); break;
+        case MP_TENSOR_UP: e = transposed(h->up[layer], hd, in); break;
+        case MP_TENSOR_DOWN: e = transposed(h->down[layer], in, hd); break;
         }
     }
     int status = check(h, e, "upload weights");
@@ -353,6 +395,13 @@ int mp_hip_upload_tensor(mp_hip* h, int32_t layer, int32_t slot, const float* da
     if (status) return status;
     h->uploaded[uploaded_index(c, layer, slot)] = 1;
     h->stats.weight_uploaded_bytes += bytes;
+    int32_t ready = 0;
+    mp_hip_ready(h, &ready);
+    if (ready && h->staging) {
+        device_free(h, h->staging);
+        h->staging = nullptr;
+        h->staging_floats = 0;
+    }
     return MP_OK;
 }
 
@@ -384,13 +433,20 @@ int mp_hip_table_write(mp_hip* h, int32_t slot, int32_t first, const int32_t* bl
 int mp_hip_copy_tail(mp_hip* h, const mp_tail_region* r) {
     if (!h || !r) return MP_INVALID_ARGUMENT;
     if (!r->rows || !r->width) return MP_OK;
-    const uint64_t span = (r->rows - 1) * r->pitch + r->width;
+    // A page region (pitch = one page of one layer) carries the valid tail
+    // tokens somewhere inside each page-layer span in the device layout, so
+    // whole spans are copied; slots beyond the valid tail are rewritten by
+    // later appends before any attention reads them. Other regions are
+    // plain strided copies of `width` floats per row.
+    const uint64_t page = (uint64_t)h->kv.block_tokens * kv_width(h->model);
+    const uint64_t width = r->pitch == page ? page : r->width;
+    const uint64_t span = (r->rows - 1) * r->pitch + width;
     if (r->width > r->pitch || r->destination + span > h->pool_elements ||
         r->source + span > h->pool_elements)
         return fail(h, MP_INVALID_ARGUMENT, "tail copy region out of range");
     const int status = check(h, mphip::launch_copy_region(h->stream, h->keys, h->values,
                                                           r->destination, r->source, r->pitch,
-                                                          r->width, r->rows),
+                                                          width, r->rows),
                              "COW copy");
     if (!status) {
         ++h->stats.cow_copies;
@@ -443,14 +499,34 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
     int status = ensure_workspace(h, R, nseq, max_length);
     if (status) return status;
     // Row metadata: tokens | row_seq | row_pos | seq_slot | seq_last_row |
-    // attention row blocks (first row, rows).
+    // attention row blocks (first row, rows) by decreasing attended length |
+    // scores work items (block, chunk).
+    const int block_rows = mphip::attention_row_block(c.heads, c.kv_heads, c.hidden / c.heads);
+    struct Block { int first, rows, length; };
+    std::vector<Block> blocks;
+    bool decode = true;
+    for (int s = 0, first = 0; s < nseq; first += steps[s].count, ++s) {
+        if (steps[s].count != 1) decode = false;
+        for (int i = 0; i < steps[s].count; i += block_rows) {
+            const int rows_b = std::min(block_rows, steps[s].count - i);
+            blocks.push_back({first + i, rows_b, steps[s].used + i + rows_b});
+        }
+    }
+    std::stable_sort(blocks.begin(), blocks.end(), [](const Block& a, const Block& b) { return a.length > b.length; });
+    size_t items = 0;
+    for (const Block& b : blocks) items += (size_t)(b.length + 255) / 256;
+    const size_t nblocks = blocks.size();
+    const size_t entries = 3 * (size_t)R + 2 * (size_t)nseq + 2 * nblocks + 2 * items;
+    if ((status = ensure_call_buffers(h, entries))) return status;
     auto& m = h->host_meta;
-    m.resize(5 * (size_t)R + 2 * (size_t)nseq + 1);
+    m.resize(entries);
     int32_t* m_tokens = m.data();
     int32_t* m_seq = m_tokens + R;
     int32_t* m_pos = m_seq + R;
     int32_t* m_slot = m_pos + R;
     int32_t* m_last = m_slot + nseq;
+    int32_t* m_blocks = m_last + nseq;
+    int32_t* m_items = m_blocks + 2 * nblocks;
     int r = 0;
     for (int s = 0; s < nseq; ++s) {
         for (int i = 0; i < steps[s].count; ++i, ++r) {
@@ -461,16 +537,17 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
         m_slot[s] = steps[s].table_slot;
         m_last[s] = r - 1;
     }
-    const int block_rows = mphip::attention_row_block(c.heads, c.kv_heads, c.hidden / c.heads);
-    int32_t* m_blocks = m_last + nseq;
-    int nblocks = 0;
-    for (int s = 0, first = 0; s < nseq; first += steps[s].count, ++s)
-        for (int i = 0; i < steps[s].count; i += block_rows, ++nblocks) {
-            m_blocks[2 * nblocks] = first + i;
-            m_blocks[2 * nblocks + 1] = std::min(block_rows, steps[s].count - i);
+    size_t it = 0;
+    for (size_t b = 0; b < nblocks; ++b) {
+        m_blocks[2 * b] = blocks[b].first;
+        m_blocks[2 * b + 1] = blocks[b].rows;
+        for (int ch = 0; ch < (blocks[b].length + 255) / 256; ++ch, ++it) {
+            m_items[2 * it] = (int32_t)b;
+            m_items[2 * it + 1] = ch;
         }
-    status = check(h, hipMemcpyAsync(h->meta, m.data(), sizeof(int32_t) * (3 * (size_t)R + 2 * (size_t)nseq + 2 * (size_t)nblocks),
-                                     hipMemcpyHostToDevice, h->stream), "upload input tokens");
+    }
+    status = check(h, hipMemcpyAsync(h->meta, m.data(), sizeof(int32_t) * entries, hipMemcpyHostToDevice, h->stream),
+                   "upload input tokens");
     if (status) return status;
     h->stats.token_uploaded_bytes += sizeof(int32_t) * R;
     mphip::RowMeta meta{h->meta, h->meta + R, h->meta + 2 * (size_t)R, h->meta + 3 * (size_t)R,
@@ -478,10 +555,15 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
     const int dim = c.hidden / c.heads, kvw = kv_width(c), qw = qkv_width(c);
     mphip::PagedKv kv{h->keys, h->values, h->tables, h->kv.max_sequence_blocks,
                       c.layers, h->kv.block_tokens, kvw};
-    const mphip::AttentionScratch scratch{h->scratch, h->scratch + (size_t)R * c.heads * score_stride(max_length),
-                                          score_stride(max_length), score_chunks(max_length),
-                                          reinterpret_cast<const int2*>(h->meta + 3 * (size_t)R + 2 * (size_t)nseq),
-                                          nblocks};
+    mphip::AttentionWork work{};
+    work.blocks = reinterpret_cast<const int2*>(m_blocks - m.data() + h->meta);
+    work.items = reinterpret_cast<const int2*>(m_items - m.data() + h->meta);
+    work.blocks_count = (int)nblocks;
+    work.items_count = (int)items;
+    work.scores = h->scratch;
+    work.stride = score_stride(max_length);
+    work.chunks = score_chunks(max_length);
+    work.chunk_max = h->scratch + (size_t)R * c.heads * work.stride;
     hipStream_t s = h->stream;
     // Launches of an enabled timing class are bracketed by a pair of events
     // from the pool that mp_hip_set_timing sized for one forward call.
@@ -496,21 +578,49 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
         return r;
     };
     const uint32_t P = MP_TIME_PROJECTION, A = MP_TIME_ATTENTION;
-    hipError_t e = mphip::launch_embed(s, h->embedding, meta.tokens, h->x, R, c.hidden);
+    auto gemm = [&](mphip::Epilogue epi, const float* x, int rows, int inner, const float* w, const float* w2,
+                    int columns, float* out) {
+        mphip::GemmArgs a{};
+        a.x = x;
+        a.w = w;
+        a.w2 = w2;
+        a.out = out;
+        a.rows = rows;
+        a.inner = inner;
+        a.columns = columns;
+        return mphip::launch_gemm(s, epi, a);
+    };
+    const int hd = c.hidden, in = c.intermediate;
+    const float eps = c.rms_epsilon;
+    hipError_t e = mphip::launch_embed(s, h->embedding, meta.tokens, h->x, R, hd);
     for (int l = 0; l < c.layers && e == hipSuccess; ++l) {
-        e = mphip::launch_rms(s, h->x, c.hidden, nullptr, h->input_norm[l], h->xn, c.hidden, R, c.hidden, c.rms_epsilon);
-        if (e == hipSuccess) e = timed(P, [&] { return mphip::launch_gemm(s, mphip::kStore, h->xn, c.hidden, R, c.hidden, h->qkv[l], nullptr, qw, qw, h->qkv_out, qw); });
+        e = mphip::launch_rms(s, h->x, nullptr, h->input_norm[l], h->xn, R, hd, eps);
+        if (e == hipSuccess) e = timed(P, [&] { return gemm(mphip::kStore, h->xn, R, hd, h->qkv[l], nullptr, qw, h->qkv_out); });
         if (e == hipSuccess) e = mphip::launch_rope_append(s, h->qkv_out, qw, R, c.heads, c.kv_heads, dim, h->cos_table, h->sin_table, meta, kv, l);
-        if (e == hipSuccess) e = timed(A, [&] { return mphip::launch_attention(s, h->qkv_out, qw, R, c.heads, c.kv_heads, dim, meta, kv, l, h->ctx, c.hidden, scratch); });
-        if (e == hipSuccess) e = timed(P, [&] { return mphip::launch_gemm(s, mphip::kResidual, h->ctx, c.hidden, R, c.hidden, h->o[l], nullptr, c.hidden, c.hidden, h->x, c.hidden); });
-        if (e == hipSuccess) e = mphip::launch_rms(s, h->x, c.hidden, nullptr, h->post_norm[l], h->xn, c.hidden, R, c.hidden, c.rms_epsilon);
-        if (e == hipSuccess) e = timed(P, [&] { return mphip::launch_gemm(s, mphip::kSwiglu, h->xn, c.hidden, R, c.hidden, h->gate[l], h->up[l], c.intermediate, c.intermediate, h->ffn, c.intermediate); });
-        if (e == hipSuccess) e = timed(P, [&] { return mphip::launch_gemm(s, mphip::kResidual, h->ffn, c.intermediate, R, c.intermediate, h->down[l], nullptr, c.hidden, c.hidden, h->x, c.hidden); });
+        if (e == hipSuccess) e = timed(A, [&] { return mphip::launch_attention(s, h->qkv_out, qw, R, c.heads, c.kv_heads, dim, meta, kv, l, h->ctx, hd, work, decode); });
+        if (e == hipSuccess) e = timed(P, [&] { return gemm(mphip::kResidual, h->ctx, R, hd, h->o[l], nullptr, hd, h->x); });
+        if (e == hipSuccess) e = mphip::launch_rms(s, h->x, nullptr, h->post_norm[l], h->xn, R, hd, eps);
+        if (e == hipSuccess) e = timed(P, [&] { return gemm(mphip::kSwiglu, h->xn, R, hd, h->gate[l], h->up[l], in, h->ffn); });
+        if (e == hipSuccess) e = timed(P, [&] { return gemm(mphip::kResidual, h->ffn, R, in, h->down[l], nullptr, hd, h->x); });
     }
     if (e == hipSuccess) e = timed(MP_TIME_HEAD, [&] {
-        hipError_t r = mphip::launch_rms(s, h->x, c.hidden, meta.seq_last_row, h->final_norm, h->last, c.hidden, nseq, c.hidden, c.rms_epsilon);
-        if (r == hipSuccess) r = mphip::launch_gemm(s, mphip::kStore, h->last, c.hidden, nseq, c.hidden, h->head, nullptr, c.vocabulary, c.vocabulary, h->logits, c.vocabulary);
-        if (r == hipSuccess) r = mphip::launch_argmax(s, h->logits, nseq, c.vocabulary, h->results, h->results + nseq);
+        // Final norm of each sequence's last row, then the LM head with the
+        // greedy argmax folded into its epilogue (logits are written only
+        // when the caller asks for them).
+        hipError_t r = mphip::launch_rms(s, h->x, meta.seq_last_row, h->final_norm, h->last, nseq, hd, eps);
+        mphip::GemmArgs a{};
+        a.x = h->last;
+        a.w = h->head;
+        a.out = logits ? h->logits : nullptr;
+        a.rows = nseq;
+        a.inner = hd;
+        a.columns = c.vocabulary;
+        a.best_value = h->best_value;
+        a.best_index = h->best_index;
+        a.bad = h->best_bad;
+        a.groups = mphip::head_groups(c.vocabulary);
+        if (r == hipSuccess) r = mphip::launch_gemm(s, mphip::kHead, a);
+        if (r == hipSuccess) r = mphip::launch_head_argmax(s, a, h->results, h->results + nseq);
         return r;
     });
     if ((status = check(h, e, "model kernel launch"))) return status;

@@ -1,0 +1,369 @@
+// Projections of the MiniPrefix forward with the reference CPU path's
+// arithmetic: out[r][n] = sum_k x[r][k] * w[k][n] with k in increasing order
+// from 0.0f, multiply and add rounded separately (src/backend/cpu/
+// matmul_kernel.cpp:101-109 and :289-354; this file is compiled with
+// -ffp-contract=off).
+//
+// Every output is one lane's serial chain, so the parallelism is the number
+// of outputs. Lane = row: a wavefront's 64 lanes are the 64 rows of one row
+// tile and the wavefront owns C output columns, giving C chains per lane.
+// The activation tile reaches each lane as one float4 (4 consecutive k) per
+// LDS read; the column's weights (stored transposed, [n][k]) are read as an
+// LDS broadcast. A work-group of NW wavefronts covers NW*C consecutive
+// columns; k advances in 64-wide chunks that the wavefronts copy straight
+// from global memory into an NS-stage LDS ring (global_load_lds, no register
+// staging), NS-2 chunks ahead of the arithmetic. Each stage is a separate LDS
+// object so that the compiler's own LDS-DMA wait tracking tells stages
+// apart; the cross-wavefront hand-off is an explicit vmcnt wait plus a bare
+// s_barrier. Decode (64 rows) uses C = 1 so that the outputs spread over as
+// many SIMDs as exist; prefill and the LM head use larger C.
+#include "exact_math.h"
+#include "kernels.h"
+#include "layout.h"
+
+namespace mphip {
+namespace {
+
+constexpr int kChunk = 64;            // k per stage
+constexpr int kQuads = kChunk / 4;    // float4 quads of k per stage
+
+template <int C, int NW, int EPI>
+struct Shape {
+    static constexpr int kThreads = NW * 64;
+    static constexpr int kMats = EPI == kSwiglu ? 2 : 1;
+    static constexpr int kCols = NW * C;                    // columns per work-group
+    static constexpr int kX4 = 64 * kQuads;                 // x float4 per stage (16 KB)
+    static constexpr int kWaveW4 = C * kMats * kQuads;      // one wavefront's weights per stage
+    static constexpr int kW4 = NW * kWaveW4;
+    static constexpr int kXDma = 16 / NW;                   // 1 KB copies per wavefront per stage
+    static constexpr int kWDma = (kWaveW4 + 63) / 64;
+    static constexpr int kDma = kXDma + kWDma;
+    static_assert(16 % NW == 0, "x stage split");
+};
+
+template <int X4, int W4>
+struct Stage {
+    float4 x[X4];  // [q][row]
+    float4 w[W4];  // [wave][column][matrix][q]
+};
+
+typedef __attribute__((address_space(3))) void* LdsPtr;
+
+// Each lane copies 16 bytes from `src` to lds_base + 16*lane.
+__device__ __forceinline__ void dma16(const float4* src, float4* lds_base) {
+    __builtin_amdgcn_global_load_lds((const void*)src, (LdsPtr)lds_base, 16, 0, 0);
+}
+
+// s_waitcnt vmcnt(N) with every other counter left alone (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (0x7 << 4) | (0xf << 8) | ((N >> 4) << 14));
+}
+
+// Barrier without a memory fence: LDS-DMA completion is established by the
+// explicit vmcnt waits, and LDS reads complete before their values are used.
+__device__ __forceinline__ void bare_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// FULL: inner % 64 == 0 and columns % kCols == 0 (no clamping anywhere).
+template <int C, int NW, int EPI, int NS, bool FULL>
+__global__ __launch_bounds__(NW * 64) void gemm_rows_kernel(GemmArgs a) {
+    using S = Shape<C, NW, EPI>;
+    constexpr int M = S::kMats;
+    constexpr int D = S::kDma;
+    static_assert(NS >= 3 && NS <= 6, "stage count");
+    static_assert((NS - 2) * D < 64, "vmcnt range");
+    using St = Stage<S::kX4, S::kW4>;
+    __shared__ St st0, st1, st2, st3, st4, st5;
+    auto stage = [&](int s) -> St& {
+        switch (s) {
+        case 0: return st0;
+        case 1: return st1;
+        case 2: return st2;
+        case 3: return st3;
+        case 4: return st4;
+        default: return st5;
+        }
+    };
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int tile = blockIdx.y;
+    const int n0 = blockIdx.x * S::kCols;
+    const int col0 = n0 + wave * C;
+    const int K = a.inner, N = a.columns;
+    const int kq_total = K >> 2;
+    const float4* xsrc = reinterpret_cast<const float4*>(a.x) + (size_t)tile * kq_total * 64;
+    const float4* w4 = reinterpret_cast<const float4*>(a.w);
+    const float4* u4 = reinterpret_cast<const float4*>(a.w2);
+    const int chunks = (K + kChunk - 1) / kChunk;
+
+    // Copies chunk c into stage `st`: this wavefront's share of the x tile
+    // and its own columns' weights.
+    auto issue = [&](int c, St& st) {
+        const int q0 = c * kQuads;
+#pragma unroll
+        for (int j = 0; j < S::kXDma; ++j) {
+            const int q = wave * S::kXDma + j;
+            const bool in = FULL || q0 + q < kq_total;
+            dma16(xsrc + (in ? (size_t)(q0 + q) * 64 + lane : 0), st.x + q * 64);
+        }
+#pragma unroll
+        for (int j = 0; j < S::kWDma; ++j) {
+            const int e = j * 64 + lane;  // (column, matrix, q) within the wavefront
+            if (S::kWaveW4 % 64 == 0 || e < S::kWaveW4) {
+                const int cm = e / kQuads, q = e % kQuads;
+                const int c_ = cm / M, m = cm % M;
+                const int n = col0 + c_;
+                const bool in = FULL || (n < N && q0 + q < kq_total);
+                const float4* src = (M == 2 && m) ? u4 : w4;
+                dma16(src + (in ? (size_t)n * kq_total + q0 + q : 0), st.w + wave * S::kWaveW4 + j * 64);
+            }
+        }
+    };
+    // Waits until at most `later` chunks' copies of this wavefront are in flight.
+    auto wait_chunks = [&](int later) {
+        switch (later) {
+        case 0: wait_vm<0>(); break;
+        case 1: wait_vm<D>(); break;
+        case 2: wait_vm<(2 * D < 64 ? 2 * D : 63)>(); break;
+        case 3: wait_vm<(3 * D < 64 ? 3 * D : 63)>(); break;
+        default: wait_vm<((NS - 2) * D)>(); break;
+        }
+    };
+
+    float acc[M][C];
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+        for (int c = 0; c < C; ++c) acc[m][c] = 0.0f;
+
+    // One quad: 4 steps of every chain of this lane, k in order.
+    auto step4 = [&](const float4& xv, const float4 (&wv)[M][C]) {
+#pragma unroll
+        for (int c = 0; c < C; ++c)
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                float t = acc[m][c];
+                t = t + xv.x * wv[m][c].x;
+                t = t + xv.y * wv[m][c].y;
+                t = t + xv.z * wv[m][c].z;
+                t = t + xv.w * wv[m][c].w;
+                acc[m][c] = t;
+            }
+    };
+    auto read_quad = [&](const St& st, int q, float4& xv, float4 (&wv)[M][C]) {
+        xv = st.x[q * 64 + lane];
+#pragma unroll
+        for (int c = 0; c < C; ++c)
+#pragma unroll
+            for (int m = 0; m < M; ++m) wv[m][c] = st.w[wave * S::kWaveW4 + (c * M + m) * kQuads + q];
+    };
+    // With one chain per lane (decode) a wavefront has no other work to hide
+    // LDS latency behind, so a chunk's reads run kDepth quads ahead of its
+    // arithmetic; with C chains per lane a quad's own reads are enough.
+    constexpr int kDepth = 4;
+    auto compute = [&](const St& st, int nq) {
+        if (C == 1 && (FULL || nq == kQuads)) {
+            float4 xv[kDepth];
+            float4 wv[kDepth][M][C];
+#pragma unroll
+            for (int q = 0; q < kDepth; ++q) read_quad(st, q, xv[q], wv[q]);
+#pragma unroll
+            for (int q = 0; q < kQuads; ++q) {
+                const int d = q % kDepth;
+                const float4 x = xv[d];
+                float4 w[M][C];
+#pragma unroll
+                for (int m = 0; m < M; ++m)
+#pragma unroll
+                    for (int c = 0; c < C; ++c) w[m][c] = wv[d][m][c];
+                if (q + kDepth < kQuads) read_quad(st, q + kDepth, xv[d], wv[d]);
+                step4(x, w);
+            }
+        } else {
+#pragma unroll 2
+            for (int q = 0; q < nq; ++q) {
+                float4 x;
+                float4 w[M][C];
+                read_quad(st, q, x, w);
+                step4(x, w);
+            }
+        }
+    };
+
+    // Prologue: chunks 0..NS-2 in flight, then chunk 0 complete everywhere.
+#pragma unroll
+    for (int s = 0; s < NS - 1; ++s)
+        if (s < chunks) issue(s, stage(s));
+    wait_chunks(min(NS - 2, chunks - 1));
+    bare_barrier();
+    for (int c0 = 0; c0 < chunks; c0 += NS) {
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            const int c = c0 + s;
+            if (c >= chunks) break;
+            compute(stage(s), min(kQuads, kq_total - c * kQuads));
+            if (c + 1 < chunks) {
+                // Chunk c+1 complete in every wavefront; then stage (s-1)
+                // (last read by chunk c-1) takes chunk c+NS-1.
+                wait_chunks(min(c + NS - 2, chunks - 1) - (c + 1));
+                bare_barrier();
+                if (c + NS - 1 < chunks) issue(c + NS - 1, stage((s + NS - 1) % NS));
+            }
+        }
+    }
+
+    // Epilogue: lane = row of the tile, columns n0 + wave*C + c.
+    const int row = tile * 64 + lane;
+    const bool row_ok = row < a.rows;
+    if (EPI == kHead) {
+        // First maximum over this lane's columns (std::max_element keeps the
+        // earliest of equal values), then over the work-group's wavefronts
+        // in column order; one partial per (row, work-group).
+        __shared__ float red_v[NW][64];
+        __shared__ int32_t red_i[NW][64];
+        __shared__ int32_t red_bad[NW][64];
+        float best = 0.0f;
+        int32_t best_i = -1, bad = 0;
+#pragma unroll
+        for (int c = 0; c < C; ++c) {
+            const int n = n0 + wave * C + c;
+            if (!FULL && n >= N) break;
+            const float v = acc[0][c];
+            if (!isfinite(v)) bad = 1;
+            if (best_i < 0 || best < v) {
+                best = v;
+                best_i = n;
+            }
+            if (a.out && row_ok) a.out[(size_t)row * N + n] = v;
+        }
+        red_v[wave][lane] = best;
+        red_i[wave][lane] = best_i;
+        red_bad[wave][lane] = bad;
+        __syncthreads();
+        if (wave == 0 && row_ok) {
+            for (int w = 1; w < NW; ++w) {
+                const int32_t i = red_i[w][lane];
+                if (i >= 0 && (best_i < 0 || best < red_v[w][lane])) {
+                    best = red_v[w][lane];
+                    best_i = i;
+                }
+                bad |= red_bad[w][lane];
+            }
+            const size_t p = (size_t)row * a.groups + blockIdx.x;
+            a.best_value[p] = best;
+            a.best_index[p] = best_i;
+            a.bad[p] = bad;
+        }
+        return;
+    }
+    if (!row_ok) return;
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+        const int n = n0 + wave * C + c;
+        if (!FULL && n >= N) break;
+        float* o = a.out + quad_index(row, n, N);
+        if (EPI == kStore) {
+            *o = acc[0][c];
+        } else if (EPI == kResidual) {
+            *o = *o + acc[0][c];
+        } else if (EPI == kSwiglu) {
+            const float g = acc[0][c];
+            *o = (g / (1.0f + ref_expf(-g))) * acc[S::kMats - 1][c];
+        }
+    }
+}
+
+// Combines the per-work-group partials of each row in work-group (= column)
+// order: largest value, earliest index among equal values.
+__global__ __launch_bounds__(256) void head_argmax_kernel(const float* __restrict__ best_value,
+                                                          const int32_t* __restrict__ best_index,
+                                                          const int32_t* __restrict__ bad, int groups,
+                                                          int32_t* __restrict__ argmax,
+                                                          int32_t* __restrict__ nonfinite) {
+    __shared__ float sv[256];
+    __shared__ int32_t si[256];
+    __shared__ int32_t sb[256];
+    const int row = blockIdx.x, tid = threadIdx.x;
+    const float* v = best_value + (size_t)row * groups;
+    const int32_t* ix = best_index + (size_t)row * groups;
+    const int32_t* bd = bad + (size_t)row * groups;
+    float best = 0.0f;
+    int32_t best_i = -1, any_bad = 0;
+    for (int g = tid; g < groups; g += 256) {
+        const int32_t i = ix[g];
+        any_bad |= bd[g];
+        if (i >= 0 && (best_i < 0 || best < v[g])) {  // g ascending within the thread
+            best = v[g];
+            best_i = i;
+        }
+    }
+    sv[tid] = best;
+    si[tid] = best_i;
+    sb[tid] = any_bad;
+    __syncthreads();
+    for (int s = 128; s > 0; s >>= 1) {
+        if (tid < s) {
+            const float ov = sv[tid + s];
+            const int32_t oi = si[tid + s];
+            const int32_t ci = si[tid];
+            if (oi >= 0 && (ci < 0 || sv[tid] < ov || (sv[tid] == ov && oi < ci))) {
+                sv[tid] = ov;
+                si[tid] = oi;
+            }
+            sb[tid] |= sb[tid + s];
+        }
+        __syncthreads();
+    }
+    if (tid == 0) {
+        argmax[row] = si[0];
+        nonfinite[row] = sb[0];
+    }
+}
+
+template <int C, int NW, int EPI, int NS>
+hipError_t launch_shape(hipStream_t s, const GemmArgs& a) {
+    using S = Shape<C, NW, EPI>;
+    const dim3 grid((a.columns + S::kCols - 1) / S::kCols, (a.rows + 63) / 64);
+    const bool full = a.inner % kChunk == 0 && a.columns % S::kCols == 0;
+    if (full)
+        gemm_rows_kernel<C, NW, EPI, NS, true><<<grid, S::kThreads, 0, s>>>(a);
+    else
+        gemm_rows_kernel<C, NW, EPI, NS, false><<<grid, S::kThreads, 0, s>>>(a);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+int head_groups(int columns) { return (columns + kHeadColumns - 1) / kHeadColumns; }
+
+hipError_t launch_gemm(hipStream_t s, Epilogue epilogue, const GemmArgs& a) {
+    if (a.rows <= 0 || a.columns <= 0) return hipSuccess;
+    if (a.inner <= 0 || a.inner % 4 || a.columns % 4) return hipErrorInvalidValue;
+    // Enough chains for every SIMD at one output per lane when the row count
+    // is small (decode); more columns per wavefront when rows are plentiful.
+    const bool many = a.rows > 64;
+    switch (epilogue) {
+    case kStore: return many ? launch_shape<4, 4, kStore, 5>(s, a) : launch_shape<1, 4, kStore, 6>(s, a);
+    case kResidual: return many ? launch_shape<4, 4, kResidual, 5>(s, a) : launch_shape<1, 4, kResidual, 6>(s, a);
+    case kSwiglu: return many ? launch_shape<4, 4, kSwiglu, 5>(s, a) : launch_shape<1, 4, kSwiglu, 6>(s, a);
+    case kHead: {
+        using S = Shape<kHeadColumns / 8, 8, kHead>;
+        static_assert(S::kCols == kHeadColumns, "head work-group width");
+        return launch_shape<kHeadColumns / 8, 8, kHead, 4>(s, a);
+    }
+    }
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_head_argmax(hipStream_t s, const GemmArgs& a, int32_t* argmax, int32_t* nonfinite) {
+    if (a.rows <= 0) return hipSuccess;
+    head_argmax_kernel<<<a.rows, 256, 0, s>>>(a.best_value, a.best_index, a.bad, a.groups, argmax, nonfinite);
+    return hipGetLastError();
+}
+
+}  // namespace mphip

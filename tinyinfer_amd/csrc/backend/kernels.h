@@ -1,5 +1,7 @@
 // Launchers for the gfx950 kernels of the MiniPrefix device forward.
 // All launchers enqueue on `stream` and return hipGetLastError().
+// Activations use the row-tile quad layout of layout.h; projection weights
+// are stored transposed ([out][in]).
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stddef.h>
@@ -27,67 +29,81 @@ struct PagedKv {
     int32_t layers, block_tokens, kv_width;
 };
 
-enum Epilogue { kStore = 0, kResidual = 1, kSwiglu = 2 };
+enum Epilogue { kStore = 0, kResidual = 1, kSwiglu = 2, kHead = 3 };
 
-hipError_t launch_embed(hipStream_t s, const float* embedding, const int32_t* tokens, float* x,
-                        int rows, int hidden);
+// out[r][n] = epilogue(sum_k x[r][k] * w[n][k]) with k accumulated in order
+// from 0, multiply and add rounded separately. x is `rows` x `inner` (quad
+// layout), w is [columns][inner]. kStore writes out (quad layout, `columns`
+// wide); kResidual adds into out; kSwiglu computes (g/(1+exp(-g)))*u from the
+// chains of w (g) and w2 (u); kHead writes, per row and per group of
+// kHeadColumns columns, the first maximum and a non-finite flag into the
+// partial arrays, and the logits row-major into `out` when it is non-null.
+struct GemmArgs {
+    const float* x;
+    const float* w;
+    const float* w2;
+    float* out;
+    int rows, inner, columns;
+    float* best_value;
+    int32_t* best_index;
+    int32_t* bad;
+    int groups;
+};
+constexpr int kHeadColumns = 64;
+int head_groups(int columns);
+hipError_t launch_gemm(hipStream_t s, Epilogue epilogue, const GemmArgs& args);
+// argmax[r] = first index of the row maximum, nonfinite[r] = any non-finite
+// logit, from the kHead partials of `args`.
+hipError_t launch_head_argmax(hipStream_t s, const GemmArgs& args, int32_t* argmax, int32_t* nonfinite);
 
-// out[r] = (x[r]*scale_r)*w with scale_r = 1/sqrt(sequential sum of squares/width + eps);
-// row r reads x row row_map[r] when row_map is non-null.
-hipError_t launch_rms(hipStream_t s, const float* x, int ldx, const int32_t* row_map,
-                      const float* weight, float* out, int ldo, int rows, int width, float eps);
+hipError_t launch_embed(hipStream_t s, const float* embedding, const int32_t* tokens, float* x, int rows,
+                        int hidden);
 
-// out[r][n] = epilogue(sum_k x[r][k]*w[k][n]) with k accumulated in order,
-// multiply and add rounded separately. kResidual adds into out; kSwiglu
-// combines the chains of w and w2 as (g/(1+exp(-g)))*u.
-hipError_t launch_gemm(hipStream_t s, Epilogue epilogue, const float* x, int ldx, int rows,
-                       int inner, const float* w, const float* w2, int columns, int ldw,
-                       float* out, int ldo);
+// out[r] = (x[r']*scale_r')*w with scale = 1/sqrt(sequential sum of squares/width + eps);
+// r' = row_map[r] when row_map is non-null, else r.
+hipError_t launch_rms(hipStream_t s, const float* x, const int32_t* row_map, const float* weight, float* out,
+                      int rows, int width, float eps);
 
 // Split-half RoPE of q and k (from host-computed cos/sin tables) for every
 // row, in place for q, and the row's rotated K and its V written into the
-// pools through the page table.
-hipError_t launch_rope_append(hipStream_t s, float* qkv, int ldqkv, int rows, int heads,
-                              int kv_heads, int dim, const float* cos_table,
-                              const float* sin_table, const RowMeta& meta, const PagedKv& kv,
-                              int layer);
+// pools through the page table. qkv is `width` = heads*dim + 2*kv_width wide.
+hipError_t launch_rope_append(hipStream_t s, float* qkv, int width, int rows, int heads, int kv_heads, int dim,
+                              const float* cos_table, const float* sin_table, const RowMeta& meta,
+                              const PagedKv& kv, int layer);
 
 // Causal GQA attention for every row in the reference two-pass softmax
-// order. q rows at qkv (stride ldq); out rows stride ldo. Rows are grouped
-// in `blocks` row blocks (first row, row count): consecutive positions of
-// one sequence, at most attention_row_block() rows each. Scratch holds
-// rows*heads score rows of `stride` floats (max length padded to 16) and
-// rows*heads*chunks chunk maxima (chunks = ceil(max length / 256)).
-struct AttentionScratch {
+// order. q rows at qkv (quad layout, ldq wide); out is quad layout, ldo
+// wide. Rows are grouped in row blocks (first row, row count): consecutive
+// positions of one sequence, at most attention_row_block() rows each,
+// ordered by decreasing attended length. `items` lists (block, 256-token
+// chunk) for every chunk each block reaches. Scratch: scores
+// [rows][heads][stride] (stride >= max length, multiple of 16) and chunk
+// maxima [rows][heads][chunks]. `decode` = every block has one row. Head
+// dim at most 64 (lane = d), at most 2048 pages per sequence.
+struct AttentionWork {
+    const int2* blocks;
+    const int2* items;
+    int blocks_count, items_count;
     float* scores;
     float* chunk_max;
-    int stride;
-    int chunks;
-    const int2* row_blocks;
-    int blocks;
+    int stride, chunks;
 };
 int attention_row_block(int heads, int kv_heads, int dim);
-hipError_t launch_attention(hipStream_t s, const float* qkv, int ldq, int rows, int heads,
-                            int kv_heads, int dim, const RowMeta& meta, const PagedKv& kv,
-                            int layer, float* out, int ldo, const AttentionScratch& scratch);
-// Stand-alone single-row variant over a caller page table.
-hipError_t launch_attention_single(hipStream_t s, const float* q, const float* keys,
-                                   const float* values, const int32_t* table, int length,
-                                   int layer, int layers, int block_tokens, int heads,
-                                   int kv_heads, int dim, float* out, float* scratch);
+hipError_t launch_attention(hipStream_t s, const float* qkv, int ldq, int rows, int heads, int kv_heads, int dim,
+                            const RowMeta& meta, const PagedKv& kv, int layer, float* out, int ldo,
+                            const AttentionWork& work, bool decode);
+// Stand-alone single-row variant over a caller page table (plain layouts).
+hipError_t launch_attention_single(hipStream_t s, const float* q, const float* keys, const float* values,
+                                   const int32_t* table, int length, int layer, int layers, int block_tokens,
+                                   int heads, int kv_heads, int dim, float* out, float* scratch);
 // Score floats per row that fit in LDS.
 constexpr int kAttentionLdsScores = 10240;
 
-// First index of the maximum of each row of logits (std::max_element), and
-// per row a flag: 1 when any value of the row is not finite, else 0.
-hipError_t launch_argmax(hipStream_t s, const float* logits, int rows, int vocabulary,
-                         int32_t* argmax, int32_t* nonfinite);
-
 // Copies a strided region inside both pools (rows x width floats, pitch apart).
-hipError_t launch_copy_region(hipStream_t s, float* keys, float* values, uint64_t destination,
-                              uint64_t source, uint64_t pitch, uint64_t width, uint64_t rows);
+hipError_t launch_copy_region(hipStream_t s, float* keys, float* values, uint64_t destination, uint64_t source,
+                              uint64_t pitch, uint64_t width, uint64_t rows);
 
-// dst[c][r] = src[r][c] for a rows x cols matrix.
-hipError_t launch_transpose(hipStream_t s, const float* src, float* dst, int rows, int cols);
+// dst[c*ld_dst + r] = src[r*cols + c] for a rows x cols matrix.
+hipError_t launch_transpose(hipStream_t s, const float* src, float* dst, int rows, int cols, int ld_dst);
 
 }  // namespace mphip

@@ -1,0 +1,218 @@
+// Row-wise kernels of the MiniPrefix forward on the row-tile quad layout:
+// embedding gather, RMSNorm, RoPE + paged K/V append, the copy-on-write tail
+// copy and the weight transpose used at upload. Reference order:
+// miniprefix/src/backend/cpu/llama_runner.cpp:10-22 (rms, rope), :71-73
+// (embedding) and :81-83 (K/V write).
+#include <algorithm>
+
+#include "kernels.h"
+#include "layout.h"
+
+namespace mphip {
+namespace {
+
+// x[r][:] = E[tokens[r]][:] for rows < rows; padding rows of the last tile
+// are zeroed so that later kernels only ever see finite values there.
+__global__ __launch_bounds__(256) void embed_kernel(const float* __restrict__ embedding,
+                                                    const int32_t* __restrict__ tokens,
+                                                    float* __restrict__ x, int rows, int hidden) {
+    const int quads = hidden >> 2;
+    const size_t total = (size_t)((rows + 63) >> 6) * quads * 64;
+    float4* x4 = reinterpret_cast<float4*>(x);
+    const float4* e4 = reinterpret_cast<const float4*>(embedding);
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total;
+         i += (size_t)gridDim.x * blockDim.x) {
+        const int r_in = (int)(i & 63);
+        const size_t tq = i >> 6;  // tile * quads + q
+        const int q = (int)(tq % quads);
+        const int row = (int)(tq / quads) * 64 + r_in;
+        x4[i] = row < rows ? e4[(size_t)tokens[row] * quads + q] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+}
+
+// out[r] = (x[src(r)] * scale) * weight with scale = 1/sqrt(sum/width + eps),
+// sum = sequential float sum of squares (llama_runner.cpp:10-16). One
+// work-group per output row tile; lane l of every wavefront handles row l.
+// The tile (up to kRmsQuads quads at a time) is copied into LDS with every
+// copy in flight at once (global_load_lds); wavefront 0 runs the 64 row
+// chains over it in column order; the normalized tile is written from LDS
+// (the whole tile when it fits, else re-read from global memory).
+constexpr int kRmsQuads = 144;  // 144 KB of LDS: a whole 576-wide tile
+
+typedef __attribute__((address_space(3))) void* LdsPtr;
+
+__global__ __launch_bounds__(256) void rms_kernel(const float* __restrict__ x, const int32_t* __restrict__ row_map,
+                                                  const float* __restrict__ weight, float* __restrict__ out,
+                                                  int rows, int width, float eps) {
+    __shared__ float4 tile_s[kRmsQuads * 64];
+    __shared__ float scale_s[64];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int tile = blockIdx.x;
+    const int quads = width >> 2;
+    const float4* x4 = reinterpret_cast<const float4*>(x);
+    const int row = tile * 64 + lane;
+    const int src = row < rows ? (row_map ? row_map[row] : row) : -1;
+    const int src_c = src < 0 ? 0 : src;
+    // Quad q of this lane's source row.
+    const float4* xrow = x4 + (size_t)(src_c >> 6) * quads * 64 + (src_c & 63);
+    float sum = 0.0f;
+    for (int q0 = 0; q0 < quads; q0 += kRmsQuads) {
+        const int nq = min(kRmsQuads, quads - q0);
+        if (q0) __syncthreads();  // previous chunk fully read
+        for (int q = wave; q < nq; q += 4)
+            __builtin_amdgcn_global_load_lds((const void*)(xrow + (size_t)(q0 + q) * 64), (LdsPtr)(tile_s + q * 64),
+                                             16, 0, 0);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (wave == 0) {
+            const float4* t4 = tile_s + lane;
+            int q = 0;
+            for (; q + 8 <= nq; q += 8) {
+                float4 v[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) v[j] = t4[(q + j) * 64];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    sum = sum + v[j].x * v[j].x;
+                    sum = sum + v[j].y * v[j].y;
+                    sum = sum + v[j].z * v[j].z;
+                    sum = sum + v[j].w * v[j].w;
+                }
+            }
+            for (; q < nq; ++q) {
+                const float4 v = t4[q * 64];
+                sum = sum + v.x * v.x;
+                sum = sum + v.y * v.y;
+                sum = sum + v.z * v.z;
+                sum = sum + v.w * v.w;
+            }
+        }
+    }
+    if (wave == 0) scale_s[lane] = 1.0f / sqrtf(sum / (float)width + eps);
+    __syncthreads();
+    if (src < 0) return;
+    const float s = scale_s[lane];
+    const float4* w4 = reinterpret_cast<const float4*>(weight);
+    float4* o4 = reinterpret_cast<float4*>(out) + (size_t)tile * quads * 64 + lane;
+    const bool resident = quads <= kRmsQuads;
+#pragma unroll 4
+    for (int q = wave; q < quads; q += 4) {
+        const float4 v = resident ? tile_s[q * 64 + lane] : xrow[(size_t)q * 64];
+        const float4 w = w4[q];
+        o4[(size_t)q * 64] = make_float4(v.x * s * w.x, v.y * s * w.y, v.z * s * w.z, v.w * s * w.w);
+    }
+}
+
+// llama_runner.cpp:17-22 and :81-83: split-half rotation of every q and k
+// head at the row's position (cos/sin from the host table of
+// float(pos)/powf(theta, 2d/dim), so the rotation is bit-identical); q is
+// rotated in place, the rotated k and the v row go to the pools (device page
+// layout of layout.h).
+__global__ void rope_append_kernel(float* __restrict__ qkv, int width, int heads, int kv_heads, int dim,
+                                   const float* __restrict__ cos_table, const float* __restrict__ sin_table,
+                                   RowMeta meta, PagedKv kv, int layer) {
+    const int r = blockIdx.x;
+    const int pos = meta.row_pos[r];
+    const int32_t* table = kv.tables + (size_t)meta.seq_slot[meta.row_seq[r]] * kv.table_stride;
+    const int half = dim / 2;
+    const float* cs_row = cos_table + (size_t)pos * half;
+    const float* sn_row = sin_table + (size_t)pos * half;
+    const int bt = kv.block_tokens, slot = pos % bt;
+    const size_t base = kv_page_base(table[pos / bt], layer, kv.layers, bt, kv.kv_width);
+    const int hidden = heads * dim;
+    for (int p = threadIdx.x; p < heads * half; p += blockDim.x) {
+        const int h = p / half, d = p % half;
+        const int i = h * dim + d, j = i + half;
+        float* qi = qkv + quad_index(r, i, width);
+        float* qj = qkv + quad_index(r, j, width);
+        const float a = *qi, b = *qj, cs = cs_row[d], sn = sn_row[d];
+        *qi = a * cs - b * sn;
+        *qj = b * cs + a * sn;
+    }
+    for (int p = threadIdx.x; p < kv_heads * half; p += blockDim.x) {
+        const int h = p / half, d = p % half;
+        const int i = h * dim + d, j = i + half;
+        const float a = qkv[quad_index(r, hidden + i, width)], b = qkv[quad_index(r, hidden + j, width)];
+        const float cs = cs_row[d], sn = sn_row[d];
+        kv.keys[base + key_offset(slot, h, d, bt, dim)] = a * cs - b * sn;
+        kv.keys[base + key_offset(slot, h, d + half, bt, dim)] = b * cs + a * sn;
+    }
+    for (int i = threadIdx.x; i < kv.kv_width; i += blockDim.x)
+        kv.values[base + value_offset(slot, i / dim, i % dim, bt, dim)] =
+            qkv[quad_index(r, hidden + kv.kv_width + i, width)];
+}
+
+// Copies `rows` consecutive spans of `width` floats, `pitch` apart, in both
+// pools; float4 when everything is 16-byte aligned.
+__global__ void copy_region_kernel(float* keys, float* values, uint64_t destination, uint64_t source,
+                                   uint64_t pitch, uint64_t width) {
+    float* pool = blockIdx.y == 0 ? keys : values;
+    const uint64_t row = blockIdx.x;
+    float* dst = pool + destination + row * pitch;
+    const float* src = pool + source + row * pitch;
+    if (((destination | source | pitch | width) & 3) == 0) {
+        float4* d4 = reinterpret_cast<float4*>(dst);
+        const float4* s4 = reinterpret_cast<const float4*>(src);
+        for (uint64_t i = threadIdx.x; i < width / 4; i += blockDim.x) d4[i] = s4[i];
+    } else {
+        for (uint64_t i = threadIdx.x; i < width; i += blockDim.x) dst[i] = src[i];
+    }
+}
+
+__global__ void transpose_kernel(const float* __restrict__ src, float* __restrict__ dst, int rows, int cols,
+                                 int ld_dst) {
+    __shared__ float tile[32][33];
+    const int c0 = blockIdx.x * 32, r0 = blockIdx.y * 32;
+    for (int i = threadIdx.y; i < 32; i += blockDim.y) {
+        const int r = r0 + i, c = c0 + threadIdx.x;
+        if (r < rows && c < cols) tile[i][threadIdx.x] = src[(size_t)r * cols + c];
+    }
+    __syncthreads();
+    for (int i = threadIdx.y; i < 32; i += blockDim.y) {
+        const int c = c0 + i, r = r0 + threadIdx.x;
+        if (r < rows && c < cols) dst[(size_t)c * ld_dst + r] = tile[threadIdx.x][i];
+    }
+}
+
+}  // namespace
+
+hipError_t launch_embed(hipStream_t s, const float* embedding, const int32_t* tokens, float* x, int rows,
+                        int hidden) {
+    if (rows <= 0) return hipSuccess;
+    const size_t total = quad_floats(rows, hidden) / 4;
+    const int blocks = (int)std::min<size_t>((total + 255) / 256, 4096);
+    embed_kernel<<<blocks, 256, 0, s>>>(embedding, tokens, x, rows, hidden);
+    return hipGetLastError();
+}
+
+hipError_t launch_rms(hipStream_t s, const float* x, const int32_t* row_map, const float* weight, float* out,
+                      int rows, int width, float eps) {
+    if (rows <= 0) return hipSuccess;
+    rms_kernel<<<(rows + 63) / 64, 256, 0, s>>>(x, row_map, weight, out, rows, width, eps);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope_append(hipStream_t s, float* qkv, int width, int rows, int heads, int kv_heads, int dim,
+                              const float* cos_table, const float* sin_table, const RowMeta& meta,
+                              const PagedKv& kv, int layer) {
+    if (rows <= 0) return hipSuccess;
+    rope_append_kernel<<<rows, 256, 0, s>>>(qkv, width, heads, kv_heads, dim, cos_table, sin_table, meta, kv,
+                                            layer);
+    return hipGetLastError();
+}
+
+hipError_t launch_copy_region(hipStream_t s, float* keys, float* values, uint64_t destination, uint64_t source,
+                              uint64_t pitch, uint64_t width, uint64_t rows) {
+    if (!rows || !width) return hipSuccess;
+    copy_region_kernel<<<dim3((unsigned)rows, 2), 256, 0, s>>>(keys, values, destination, source, pitch, width);
+    return hipGetLastError();
+}
+
+hipError_t launch_transpose(hipStream_t s, const float* src, float* dst, int rows, int cols, int ld_dst) {
+    transpose_kernel<<<dim3((cols + 31) / 32, (rows + 31) / 32), dim3(32, 8), 0, s>>>(src, dst, rows, cols,
+                                                                                     ld_dst);
+    return hipGetLastError();
+}
+
+}  // namespace mphip
