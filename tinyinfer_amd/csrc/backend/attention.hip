@@ -30,29 +30,6 @@ constexpr int kMaxRowHeads = 48;
 constexpr int kMaxTable = 2048;  // pages of one sequence (the host enforces it)
 constexpr int kMaxDim = 64;  // lane = d in the output chains
 
-typedef __attribute__((address_space(3))) void* LdsPtr;
-
-// 16 bytes per lane from `src` to LDS base + 16*lane, issued from inline
-// assembly so that the compiler adds no waits of its own for it (its
-// LDS-DMA tracking falls back to draining every load before any other LDS
-// read): the caller waits with vm_wait<N>() itself. The kernels that use it
-// keep nothing of their own in M0.
-__device__ __forceinline__ void lds_copy16(const void* src, uint32_t lds_base) {
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
-                 :: "v"(src), "s"(lds_base) : "memory", "m0");
-}
-__device__ __forceinline__ uint32_t lds_address(const void* p) {
-    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
-}
-// s_waitcnt vmcnt(N) with a compiler barrier on each side.
-template <int N>
-__device__ __forceinline__ void vm_wait() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_waitcnt((N & 15) | (0x7 << 4) | (0xf << 8) | ((N >> 4) << 14));
-    asm volatile("" ::: "memory");
-}
-
 // Wavefront maximum with DPP row shifts and row broadcasts (the maximum is
 // order-free); lane 63 ends up with the result, which is then broadcast.
 __device__ __forceinline__ float wave_max(float v) {
@@ -152,14 +129,13 @@ __global__ __launch_bounds__(kScoreChunk) void attn_scores_kernel(const float* _
 //   den = sum_t e_t in token order (lane h of the wavefront, one chain per
 //         head); p_t = e_t / den;
 //   out_d = sum_t p_t v_td in token order.
-// V pages stream through kStages LDS stages filled by direct-to-LDS copies
-// (issued from inline assembly with exact hand-placed waits); the first
-// pages are already in flight while the denominators are summed. grid =
+// V pages stream through a ring of registers; the first pages are already
+// in flight while the denominators are summed. grid =
 // (blocks, kv heads, tasks per block): for decode the 3 heads of a
 // (sequence, kv head) are 192 work-groups apart in dispatch order, which
 // keeps them on one XCD (shared L2) but on different CUs.
 constexpr int kPWindow = 2048;
-constexpr int kStages = 8;  // V pages of the LDS ring (4 KB each)
+constexpr int kRingPages = 8;  // V pages in flight per wavefront (16 VGPRs each)
 
 template <int BT, int DIM, int P>
 __global__ __launch_bounds__(64) void attn_pv_kernel(int heads, int kv_heads, int dim_rt, RowMeta meta, PagedKv kv,
@@ -167,19 +143,6 @@ __global__ __launch_bounds__(64) void attn_pv_kernel(int heads, int kv_heads, in
     __shared__ int32_t table_s[kMaxTable];
     __shared__ float4 p_s[P][kPWindow / 4];
     __shared__ float den_s[P];
-    __shared__ float4 v0[256], v1[256], v2[256], v3[256], v4[256], v5[256], v6[256], v7[256];
-    auto vstage = [&](int i) -> float4* {
-        switch (i) {
-        case 0: return v0;
-        case 1: return v1;
-        case 2: return v2;
-        case 3: return v3;
-        case 4: return v4;
-        case 5: return v5;
-        case 6: return v6;
-        default: return v7;
-        }
-    };
     const int dim = DIM ? DIM : dim_rt;
     const int bt = BT ? BT : kv.block_tokens;
     const int2 blk = w.blocks[blockIdx.x];
@@ -299,43 +262,49 @@ __global__ __launch_bounds__(64) void attn_pv_kernel(int heads, int kv_heads, in
         }
     };
     const int d = lane < dim ? lane : 0;
-    const size_t lane_off = value_offset(0, kvh, d, bt, dim);
-    auto issue = [&](int pg, float4* stage) {
+    // Ring of kRingPages V pages in registers (16-token pages, dim 64):
+    // lane d holds the page's 16 values of d as 4 float4 (tokens 4j..4j+3),
+    // each float4 load one contiguous 1 KB run across the wavefront.
+    float4 ring[kRingPages][4];
+    auto load_page = [&](int pg, float4 (&v)[4]) {
         const int block = __builtin_amdgcn_readfirstlane(table_s[pg]);
         const float4* src = reinterpret_cast<const float4*>(
             kv.values + kv_page_base(block, layer, kv.layers, 16, kv.kv_width) + value_offset(0, kvh, 0, 16, 64));
-        const uint32_t base = __builtin_amdgcn_readfirstlane(lds_address(stage));
 #pragma unroll
-        for (int j = 0; j < 4; ++j) lds_copy16(src + 4 * lane + j, base + 1024 * j);
+        for (int j = 0; j < 4; ++j) v[j] = src[64 * j + lane];
+    };
+    // Ring invariant at a group boundary pg: ring[s] holds page
+    // min(pg + s, last).
+    auto prologue = [&](int pg_first, int pg_end) {
+#pragma unroll
+        for (int s = 0; s < kRingPages; ++s) load_page(min(pg_first + s, pg_end - 1), ring[s]);
     };
     constexpr bool kRing = BT == 16 && DIM == 64;
-    // Denominators. One window: e stays staged for the outputs; the first
-    // V pages are copied meanwhile. Several windows: a first pass sums the
-    // denominators, a second recomputes e per window.
+    // Denominators. One window: e is staged once, the first V pages are
+    // requested, and the chain runs while they arrive. Several windows: a
+    // first pass sums the denominators; the window loop forms e again.
+    // (The ring is first filled at a single place in the window loop so that
+    // every path reaches the page loop with the same loads in flight.)
     const bool one_window = len <= kPWindow;
     float den = 0.0f;
-    if (one_window) {
-        stage_e(0, len);
-        if (kRing) {
-            __builtin_amdgcn_s_waitcnt(0);  // staging loads done before the copies' accounting starts
-#pragma unroll
-            for (int s = 0; s < kStages - 1; ++s)
-                if (s < pages) issue(s, vstage(s));
-        }
-        chain(len, den);
-    } else {
+    if (!one_window) {
         for (int u0 = 0; u0 < len; u0 += kPWindow) {
             stage_e(u0, min(kPWindow, len - u0));
             chain(min(kPWindow, len - u0), den);
         }
+        if (lane < P) den_s[lane] = den;
     }
-    if (lane < P) den_s[lane] = den;
     float acc[P];
 #pragma unroll
     for (int h = 0; h < P; ++h) acc[h] = 0.0f;
     for (int u0 = 0; u0 < len; u0 += kPWindow) {
         const int n_win = min(kPWindow, len - u0);
-        if (!one_window) stage_e(u0, n_win);
+        stage_e(u0, n_win);
+        if (kRing) prologue(u0 >> 4, (u0 + n_win + 15) >> 4);
+        if (one_window) {
+            chain(len, den);
+            if (lane < P) den_s[lane] = den;
+        }
         // p_t = e_t / den in place.
 #pragma unroll
         for (int h = 0; h < P; ++h) {
@@ -346,16 +315,10 @@ __global__ __launch_bounds__(64) void attn_pv_kernel(int heads, int kv_heads, in
             }
         }
         if (kRing) {
-            // Page pg uses stage (pg - pg_first) % kStages; each page is 4
-            // copies; before page pg is read, the (up to kStages-2) pages
-            // issued after it may still be in flight.
             const int pg_first = u0 >> 4;
             const int pg_end = (u0 + n_win + 15) >> 4;
             const int full_end = (u0 + n_win) >> 4;
-            auto page_sum = [&](const float4* stage, int pg, int n) {
-                float4 v[4];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) v[j] = stage[64 * j + lane];
+            auto page_sum = [&](const float4 (&v)[4], int pg, int n) {
                 const int q0 = (pg - pg_first) * 4;
 #pragma unroll
                 for (int h = 0; h < P; ++h) {
@@ -378,30 +341,31 @@ __global__ __launch_bounds__(64) void attn_pv_kernel(int heads, int kv_heads, in
                     acc[h] = a;
                 }
             };
-            if (!one_window) {
-                __builtin_amdgcn_s_waitcnt(0);
+            const int last = pg_end - 1;
+            int pg = pg_first;
+            for (; pg + kRingPages <= full_end; pg += kRingPages) {
 #pragma unroll
-                for (int s = 0; s < kStages - 1; ++s)
-                    if (pg_first + s < pg_end) issue(pg_first + s, vstage(s));
-            }
-            for (int pg0 = pg_first; pg0 < pg_end; pg0 += kStages) {
-#pragma unroll
-                for (int s = 0; s < kStages; ++s) {
-                    const int pg = pg0 + s;
-                    if (pg >= pg_end) break;
-                    if (pg + kStages - 1 < pg_end) {
-                        issue(pg + kStages - 1, vstage((s + kStages - 1) % kStages));
-                        vm_wait<4 * (kStages - 1)>();
-                    } else {
-                        vm_wait<0>();
-                    }
-                    page_sum(vstage(s), pg, pg < full_end ? 16 : u0 + n_win - (pg << 4));
+                for (int s = 0; s < kRingPages; ++s) {
+                    page_sum(ring[s], pg + s, 16);
+                    load_page(min(pg + s + kRingPages, last), ring[s]);
+                    // Keep each page's LDS reads next to its use (no
+                    // hoisting across pages: register pressure).
+                    __builtin_amdgcn_sched_barrier(0);
                 }
             }
+            // Fewer than kRingPages full pages and the partial page remain.
+#pragma unroll
+            for (int s = 0; s < kRingPages; ++s)
+                if (pg + s < pg_end) page_sum(ring[s], pg + s, pg + s < full_end ? 16 : u0 + n_win - ((pg + s) << 4));
+            // Drain the clamped refills past the window so that the next
+            // window starts with no ring load in flight (the compiler then
+            // keeps exact per-page waits in the loop above).
+            if (!one_window) __builtin_amdgcn_s_waitcnt(0);
         } else {
             for (int u = 0; u < n_win; ++u) {
                 const int tt = u0 + u, pg = tt / bt, slot = tt - pg * bt;
-                const float v = kv.values[kv_page_base(table_s[pg], layer, kv.layers, bt, kv.kv_width) + lane_off + slot];
+                const float v = kv.values[kv_page_base(table_s[pg], layer, kv.layers, bt, kv.kv_width) +
+                                          value_offset(slot, kvh, d, bt, dim)];
 #pragma unroll
                 for (int h = 0; h < P; ++h) acc[h] = acc[h] + reinterpret_cast<const float*>(p_s[h])[u] * v;
             }

@@ -706,7 +706,8 @@ int mp_hip_set_timing(mp_hip* h, uint32_t classes) {
     const size_t need = 2 * (5 * (size_t)h->model.layers + 1);
     while (h->events.size() < need) {
         hipEvent_t ev = nullptr;
-        if ((status = check(h, hipEventCreate(&ev), "create timing event"))) return status;
+        if ((status = check(h, hipEventCreateWithFlags(&ev, hipEventDisableSystemFence), "create timing event")))
+            return status;
         h->events.push_back(ev);
     }
     h->timing = classes;

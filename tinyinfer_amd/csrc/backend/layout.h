@@ -17,8 +17,8 @@
 // (block, layer) the order differs: kv head major, then for keys
 // [d/4][slot][4] (a wavefront whose lanes are consecutive tokens reads one
 // float4 of d per lane as contiguous 256-byte runs) and for values
-// [d][slot] (a lane that owns one d reads a page's 16 tokens as 64
-// contiguous bytes).
+// [slot/4][d][4] (a wavefront whose lanes are the d of one head reads 4
+// consecutive tokens per lane as one contiguous run of dim*16 bytes).
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stddef.h>
@@ -45,7 +45,7 @@ __host__ __device__ __forceinline__ size_t key_offset(int slot, int kv_head, int
     return (size_t)kv_head * bt * dim + (size_t)(d >> 2) * bt * 4 + (size_t)slot * 4 + (d & 3);
 }
 __host__ __device__ __forceinline__ size_t value_offset(int slot, int kv_head, int d, int bt, int dim) {
-    return (size_t)kv_head * bt * dim + (size_t)d * bt + slot;
+    return (size_t)kv_head * bt * dim + (size_t)(slot >> 2) * dim * 4 + (size_t)d * 4 + (slot & 3);
 }
 
 }  // namespace mphip
