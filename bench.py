@@ -18,7 +18,10 @@ roofline: the dominant kernel is paged attention (score, softmax and value
 kernels of one layer = one launch), timed live with HIP events on the
 runner's stream over the timed steps. Algorithmic bytes per launch =
 sum over sequences of T*kv_width*4*2 (K and V of every attended token, read
-once) + rows*hidden*4*2 (q in, context out).
+once) + rows*hidden*4*2 (q in, context out). `traffic` is this run's
+algorithmic bytes times the measured/algorithmic ratio recorded in
+profiles/attention_b64_decode_traffic.json (two rocprofv3 --pmc passes,
+FETCH_SIZE and WRITE_SIZE, calibrated with a copy of known size).
 
 cpu_baseline: the oracle (a C restatement of the reference CPU path,
 bit-identical to it) on one host core, decoding single tokens at contexts
@@ -207,11 +210,15 @@ def main():
         raise SystemExit("--steps must be >= 1 and --warmup >= 0")
     g = gpu_leg(args)
     cpu = None if args.no_cpu_baseline else cpu_leg(args)
-    traffic = None
+    # HBM bytes per attention launch: the counter-measured bytes / algorithmic
+    # bytes ratio of the committed two-pass FETCH_SIZE/WRITE_SIZE record (same
+    # workload and seed, fewer steps), applied to this run's algorithmic bytes.
+    traffic, traffic_ratio = None, None
     if TRAFFIC_FILE.exists():
         rec = json.loads(TRAFFIC_FILE.read_text())
-        if rec.get("seed") == args.seed:
-            traffic = rec.get("attention_bytes_per_launch")
+        if rec.get("seed") == args.seed and rec.get("traffic_ratio"):
+            traffic_ratio = rec["traffic_ratio"]
+            traffic = int(round(traffic_ratio * g["attention_bytes_per_launch"]))
     frac = g["achieved"] / HBM_PEAK_GBS
     line = {
         "metric": METRIC, "value": round(g["value"], 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
@@ -225,7 +232,7 @@ def main():
                    "seed": args.seed, "mean_context": round(g["mean_context"], 1)},
         "roofline": {"bound": "hbm", "kernel": "paged attention (score+softmax+value kernels, one layer)",
                      "achieved": round(g["achieved"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(frac, 4), "traffic": traffic,
+                     "frac": round(frac, 4), "traffic": traffic, "traffic_ratio": traffic_ratio,
                      "algorithmic_bytes_per_launch": int(g["attention_bytes_per_launch"]),
                      "us_per_launch": round(g["attention_us_per_launch"], 2)},
         "cpu_baseline": cpu,
