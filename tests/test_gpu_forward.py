@@ -157,16 +157,20 @@ def test_batched_prefill_and_decode_rows(torch_cuda):
             used[i] += counts[i]
 
 
-@pytest.mark.parametrize("shape", ["paged16_dim64", "tiny_generic"])
+@pytest.mark.parametrize("shape", ["paged16_dim64", "paged16_dim64_beyond_fused", "tiny_generic"])
 def test_long_context_softmax_windows(torch_cuda, shape):
     """Rows longer than one 2048-token softmax window: the denominators are
     summed over several staged windows and e_t is formed again per window
-    (prefill row blocks with every head of a group in one task, then decode
-    rows), on the 16-token page / dim-64 path and on the generic path."""
-    if shape == "paged16_dim64":
-        cfg = dict(layers=1, hidden=192, intermediate=256, heads=3, kv_heads=1, vocabulary=512, context=2720,
+    (prefill row blocks with every head of a group in one task), then decode
+    rows: on the 16-token page / dim-64 path (decode through the fused
+    kernel up to 4096 tokens, through the two-kernel path beyond) and on the
+    generic path."""
+    if shape.startswith("paged16_dim64"):
+        context = 2720 if shape == "paged16_dim64" else 4400
+        cfg = dict(layers=1, hidden=192, intermediate=256, heads=3, kv_heads=1, vocabulary=512, context=context,
                    eos=0, rms_epsilon=1e-5, rope_theta=100000.0, tied=1)
-        bt, chunks = 16, [1100, 1100, 500, 1, 1]
+        bt = 16
+        chunks = [1100, 1100, 500, 1, 1] if context == 2720 else [2048, 2048, 200, 1, 1]
     else:
         cfg = tiny_config(context=2600)
         bt, chunks = 4, [1000, 1100, 300, 1, 1]

@@ -266,13 +266,14 @@ __global__ __launch_bounds__(64) void attn_pv_kernel(int heads, int kv_heads, in
     // lane d holds the page's 16 values of d as 4 float4 (tokens 4j..4j+3),
     // each float4 load one contiguous 1 KB run across the wavefront.
     float4 ring[kRingPages][4];
-    auto load_page = [&](int pg, float4 (&v)[4]) {
-        const int block = __builtin_amdgcn_readfirstlane(table_s[pg]);
+    auto load_block = [&](int block_id, float4 (&v)[4]) {
+        const int block = __builtin_amdgcn_readfirstlane(block_id);
         const float4* src = reinterpret_cast<const float4*>(
             kv.values + kv_page_base(block, layer, kv.layers, 16, kv.kv_width) + value_offset(0, kvh, 0, 16, 64));
 #pragma unroll
         for (int j = 0; j < 4; ++j) v[j] = src[64 * j + lane];
     };
+    auto load_page = [&](int pg, float4 (&v)[4]) { load_block(table_s[pg], v); };
     // Ring invariant at a group boundary pg: ring[s] holds page
     // min(pg + s, last).
     auto prologue = [&](int pg_first, int pg_end) {
@@ -318,45 +319,93 @@ __global__ __launch_bounds__(64) void attn_pv_kernel(int heads, int kv_heads, in
             const int pg_first = u0 >> 4;
             const int pg_end = (u0 + n_win + 15) >> 4;
             const int full_end = (u0 + n_win) >> 4;
-            auto page_sum = [&](const float4 (&v)[4], int pg, int n) {
+            // Products p_t * v_td (rounded as the reference rounds them) are
+            // formed one page ahead of their additions and interleaved with
+            // them in program order (each dependent add is followed by
+            // independent multiplies), so the add chain is the only latency.
+            auto read_p = [&](int pg, float4 (&o)[P][4]) {
                 const int q0 = (pg - pg_first) * 4;
 #pragma unroll
-                for (int h = 0; h < P; ++h) {
-                    float a = acc[h];
+                for (int h = 0; h < P; ++h)
 #pragma unroll
-                    for (int s4 = 0; s4 < 4; ++s4) {
-                        const float4 p = p_s[h][q0 + s4];
-                        if (n == 16) {
-                            a = a + p.x * v[s4].x;
-                            a = a + p.y * v[s4].y;
-                            a = a + p.z * v[s4].z;
-                            a = a + p.w * v[s4].w;
-                        } else {
-                            if (4 * s4 + 0 < n) a = a + p.x * v[s4].x;
-                            if (4 * s4 + 1 < n) a = a + p.y * v[s4].y;
-                            if (4 * s4 + 2 < n) a = a + p.z * v[s4].z;
-                            if (4 * s4 + 3 < n) a = a + p.w * v[s4].w;
-                        }
+                    for (int s4 = 0; s4 < 4; ++s4) o[h][s4] = p_s[h][q0 + s4];
+            };
+            auto lane4 = [](const float4& v, int c) { return c == 0 ? v.x : c == 1 ? v.y : c == 2 ? v.z : v.w; };
+            auto products = [&](const float4 (&v)[4], const float4 (&pp)[P][4], float (&o)[P][16]) {
+#pragma unroll
+                for (int h = 0; h < P; ++h)
+#pragma unroll
+                    for (int t = 0; t < 16; ++t) o[h][t] = lane4(pp[h][t >> 2], t & 3) * lane4(v[t >> 2], t & 3);
+            };
+            // acc += products of the first n tokens of a page, in order.
+            auto add_page = [&](const float (&o)[P][16], int n) {
+#pragma unroll
+                for (int t = 0; t < 16; ++t)
+                    if (n == 16 || t < n) {
+#pragma unroll
+                        for (int h = 0; h < P; ++h) acc[h] = acc[h] + o[h][t];
                     }
-                    acc[h] = a;
-                }
             };
             const int last = pg_end - 1;
             int pg = pg_first;
+            float pr[P][16];  // products of page pg
+            {
+                float4 pp[P][4];
+                read_p(pg, pp);
+                products(ring[0], pp, pr);
+            }
             for (; pg + kRingPages <= full_end; pg += kRingPages) {
+                // Block ids of this group's refills, read together.
+                int32_t refill[kRingPages];
+#pragma unroll
+                for (int s = 0; s < kRingPages; ++s) refill[s] = table_s[min(pg + kRingPages + s, last)];
 #pragma unroll
                 for (int s = 0; s < kRingPages; ++s) {
-                    page_sum(ring[s], pg + s, 16);
-                    load_page(min(pg + s + kRingPages, last), ring[s]);
-                    // Keep each page's LDS reads next to its use (no
-                    // hoisting across pages: register pressure).
-                    __builtin_amdgcn_sched_barrier(0);
+                    // ring[s] (page pg+s) is consumed: refill it; add page
+                    // pg+s while forming the products of page pg+s+1
+                    // (ring[s+1], or the refilled ring[0] at the end of the
+                    // group).
+                    load_block(refill[s], ring[s]);
+                    float4 pp[P][4];
+                    read_p(min(pg + s + 1, last), pp);
+                    const float4 (&vn)[4] = ring[(s + 1) % kRingPages];
+                    float nx[P][16];
+#pragma unroll
+                    for (int t = 0; t < 16; ++t) {
+#pragma unroll
+                        for (int h = 0; h < P; ++h) acc[h] = acc[h] + pr[h][t];
+                        // The first adds run while the next page's p and V
+                        // arrive; from the 4th on, each add is followed by
+                        // the multiplies of the next page.
+                        if (t >= 3) {
+                            const int t0 = (t - 3) * 16 / 13, t1 = (t - 2) * 16 / 13;
+#pragma unroll
+                            for (int u = t0; u < t1; ++u)
+#pragma unroll
+                                for (int h = 0; h < P; ++h)
+                                    nx[h][u] = lane4(pp[h][u >> 2], u & 3) * lane4(vn[u >> 2], u & 3);
+                        }
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+#pragma unroll
+                    for (int h = 0; h < P; ++h)
+#pragma unroll
+                        for (int t = 0; t < 16; ++t) pr[h][t] = nx[h][t];
                 }
             }
-            // Fewer than kRingPages full pages and the partial page remain.
+            // Fewer than kRingPages full pages and the partial page remain;
+            // ring[s] holds page pg+s and pr the products of page pg.
 #pragma unroll
-            for (int s = 0; s < kRingPages; ++s)
-                if (pg + s < pg_end) page_sum(ring[s], pg + s, pg + s < full_end ? 16 : u0 + n_win - ((pg + s) << 4));
+            for (int s = 0; s < kRingPages; ++s) {
+                if (pg + s < pg_end) {
+                    if (s) {
+                        float4 pp[P][4];
+                        read_p(pg + s, pp);
+                        products(ring[s], pp, pr);
+                    }
+                    add_page(pr, pg + s < full_end ? 16 : u0 + n_win - ((pg + s) << 4));
+                }
+            }
             // Drain the clamped refills past the window so that the next
             // window starts with no ring load in flight (the compiler then
             // keeps exact per-page waits in the loop above).
@@ -375,6 +424,207 @@ __global__ __launch_bounds__(64) void attn_pv_kernel(int heads, int kv_heads, in
 #pragma unroll
         for (int j = 0; j < P; ++j) out[quad_index(row, (h0 + j) * dim + lane, ldo)] = acc[j];
     }
+}
+
+// Decode rows with 16-token pages and head dim 64, contexts up to
+// kFusedMaxT, after the scores kernel: one work-group of 8 wavefronts per
+// (sequence row, KV head) forms the softmax and the output of its G query
+// heads.
+//   1. the row's scores of the G heads go to LDS; maximum (order-free);
+//   2. e_t = expf(s_t - m), all threads;
+//   3. den: wavefront h, lane 0, sums head h's e_t in token order;
+//   4. p_t = e_t / den, all threads;
+//   5. output: wavefront h adds p_t * v_td (product rounded as the reference
+//      rounds it; each dependent add is followed by the next multiply) in
+//      token order, lane = d, with V pages streamed through a ring of
+//      registers kRingPages ahead. The G wavefronts read the same pages, so
+//      two of three reads hit the work-group's L1; LDS only serves p_t.
+constexpr int kFusedMaxT = 4096;
+constexpr int kFusedThreads = 512;
+
+// Work-group barrier that orders LDS only: this wavefront's LDS accesses
+// complete (lgkmcnt(0)) before the barrier; global loads stay in flight.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // vmcnt 63, expcnt 7, lgkmcnt 0
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+template <int G>
+__global__ __launch_bounds__(kFusedThreads) void attn_decode_kernel(int heads, RowMeta meta, PagedKv kv, int layer,
+                                                                    AttentionWork w, float* __restrict__ out,
+                                                                    int ldo) {
+    static_assert(G >= 1 && G < kFusedThreads / 64, "waves per head");
+    __shared__ float4 sc4[G][kFusedMaxT / 4];  // s_t, then e_t, then p_t
+    __shared__ float red_s[kFusedThreads / 64][G];
+    __shared__ float den_s[G];
+    __shared__ uint32_t voff_s[kFusedMaxT / 16];  // page pg's V of this KV head, in float4 from kv.values
+    float* const sc = reinterpret_cast<float*>(&sc4[0][0]);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int kvh = blockIdx.y;
+    const int row = w.blocks[blockIdx.x].x;
+    const int len = meta.row_pos[row] + 1;
+    const int pages = (len + 15) >> 4;
+    const int last_page = pages - 1;
+    const int32_t* table_g = kv.tables + (size_t)meta.seq_slot[meta.row_seq[row]] * kv.table_stride;
+    // Float4 offsets of the pages' V for this KV head (the pool holds fewer
+    // than 2^32 float4: checked at creation).
+    const uint32_t page_f4 = (uint32_t)(16 * kv.kv_width / 4);
+    for (int i = tid; i < pages; i += kFusedThreads)
+        voff_s[i] = ((uint32_t)table_g[i] * (uint32_t)kv.layers + (uint32_t)layer) * page_f4 + (uint32_t)kvh * 256u;
+
+    // ---- 1. scores of the row's G heads and their maxima
+    float mx[G];
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+        const float4* src = reinterpret_cast<const float4*>(w.scores + ((size_t)row * heads + kvh * G + h) * w.stride);
+        float m = -INFINITY;
+        const int n4 = (len + 3) >> 2;  // the stride is a multiple of 16: whole float4 stay in the row
+        for (int e = tid; e < n4; e += kFusedThreads) {
+            const float4 v = src[e];
+            sc4[h][e] = v;
+            const int t = 4 * e;
+            m = fmaxf(m, v.x);
+            if (t + 1 < len) m = fmaxf(m, v.y);
+            if (t + 2 < len) m = fmaxf(m, v.z);
+            if (t + 3 < len) m = fmaxf(m, v.w);
+        }
+        m = wave_max(m);
+        if (lane == 0) red_s[wave][h] = m;
+    }
+    __syncthreads();
+    // ---- 2. maximum and e_t
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+        float m = red_s[0][h];
+#pragma unroll
+        for (int v = 1; v < kFusedThreads / 64; ++v) m = fmaxf(m, red_s[v][h]);
+        mx[h] = m;
+    }
+    for (int t = tid; t < len; t += kFusedThreads) {
+#pragma unroll
+        for (int h = 0; h < G; ++h) sc[h * kFusedMaxT + t] = ref_expf(sc[h * kFusedMaxT + t] - mx[h]);
+    }
+    lds_barrier();
+    // ---- 3. denominators
+    if (wave < G && lane == 0) {
+        const float4* e4 = sc4[wave];
+        const int full = len >> 2;
+        float den = 0.0f;
+        int q = 0;
+        for (; q + 8 <= full; q += 8) {
+            float4 v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = e4[q + j];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                den = den + v[j].x;
+                den = den + v[j].y;
+                den = den + v[j].z;
+                den = den + v[j].w;
+            }
+        }
+        for (; q < full; ++q) {
+            const float4 v = e4[q];
+            den = den + v.x;
+            den = den + v.y;
+            den = den + v.z;
+            den = den + v.w;
+        }
+        const float* e = reinterpret_cast<const float*>(e4);
+        for (int u = full * 4; u < len; ++u) den = den + e[u];
+        den_s[wave] = den;
+    }
+    lds_barrier();
+    // ---- 4. p_t = e_t / den
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+        const float dn = den_s[h];
+        for (int t = tid; t < len; t += kFusedThreads) sc[h * kFusedMaxT + t] = sc[h * kFusedMaxT + t] / dn;
+    }
+    lds_barrier();
+
+    // ---- 5. output chains (no barrier from here on)
+    if (wave >= G) return;
+    const float4* p4 = sc4[wave];
+    const float4* vbase = reinterpret_cast<const float4*>(kv.values);
+    auto lane4 = [](const float4& v, int c) { return c == 0 ? v.x : c == 1 ? v.y : c == 2 ? v.z : v.w; };
+    float4 ring[kRingPages][4];
+    auto load_page = [&](uint32_t off, float4 (&v)[4]) {
+        const float4* src = vbase + __builtin_amdgcn_readfirstlane(off);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = src[64 * j + lane];
+    };
+    float acc = 0.0f;
+    // acc += p_t * v_td over a full page: each dependent add is followed by
+    // the next token's multiply.
+    auto add_page = [&](const float4 (&v)[4], const float4 (&pp)[4]) {
+        float prod = pp[0].x * v[0].x;
+#pragma unroll
+        for (int t = 0; t < 16; ++t) {
+            const float cur = prod;
+            if (t < 15) prod = lane4(pp[(t + 1) >> 2], (t + 1) & 3) * lane4(v[(t + 1) >> 2], (t + 1) & 3);
+            acc = acc + cur;
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    auto read_p = [&](int pg, float4 (&pp)[4]) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) pp[j] = p4[pg * 4 + j];
+    };
+    // Ring invariant at a group boundary pg: ring[r] holds page
+    // min(pg + r, last_page).
+#pragma unroll
+    for (int r = 0; r < kRingPages; ++r) load_page(voff_s[min(r, last_page)], ring[r]);
+    const int full_pages = len >> 4;
+    int pg = 0;
+    for (; pg + kRingPages <= full_pages; pg += kRingPages) {
+        uint32_t refill[kRingPages];
+#pragma unroll
+        for (int r = 0; r < kRingPages; ++r) refill[r] = voff_s[min(pg + kRingPages + r, last_page)];
+#pragma unroll
+        for (int r = 0; r < kRingPages; ++r) {
+            float4 pp[4];
+            read_p(pg + r, pp);
+            add_page(ring[r], pp);
+            load_page(refill[r], ring[r]);
+        }
+    }
+    // Fewer than kRingPages full pages and the partial page remain.
+#pragma unroll
+    for (int r = 0; r < kRingPages; ++r) {
+        const int q = pg + r;
+        if (q < pages) {
+            float4 pp[4];
+            read_p(q, pp);
+            if (q < full_pages) {
+                add_page(ring[r], pp);
+            } else {
+                const int n = len - 16 * q;
+#pragma unroll
+                for (int t = 0; t < 16; ++t)
+                    if (t < n) acc = acc + lane4(pp[t >> 2], t & 3) * lane4(ring[r][t >> 2], t & 3);
+            }
+        }
+    }
+    out[quad_index(row, (kvh * G + wave) * 64 + lane, ldo)] = acc;
+}
+
+hipError_t launch_fused_decode(hipStream_t s, const float* qkv, int ldq, int heads, int kv_heads,
+                               const RowMeta& meta, const PagedKv& kv, int layer, float* out, int ldo,
+                               const AttentionWork& w) {
+    attn_scores_kernel<16, 64><<<dim3(w.items_count, kv_heads), kScoreChunk, 0, s>>>(qkv, ldq, heads, kv_heads, 64,
+                                                                                    meta, kv, layer, w);
+    const dim3 grid(w.blocks_count, kv_heads);
+    switch (heads / kv_heads) {
+    case 1: attn_decode_kernel<1><<<grid, kFusedThreads, 0, s>>>(heads, meta, kv, layer, w, out, ldo); break;
+    case 2: attn_decode_kernel<2><<<grid, kFusedThreads, 0, s>>>(heads, meta, kv, layer, w, out, ldo); break;
+    case 3: attn_decode_kernel<3><<<grid, kFusedThreads, 0, s>>>(heads, meta, kv, layer, w, out, ldo); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
 }
 
 template <int BT, int DIM>
@@ -420,6 +670,11 @@ hipError_t launch_attention(hipStream_t s, const float* qkv, int ldq, int rows, 
     if (group > kMaxRowHeads || dim % 4 || dim > kMaxDim || kv.block_tokens % 4 ||
         kv.table_stride > kMaxTable)
         return hipErrorInvalidValue;
+    // Decode rows of 16-token pages, head dim 64, at most 3 query heads per
+    // KV head and contexts up to kFusedMaxT (stride = longest context
+    // rounded up to 16): one fused kernel.
+    if (decode && kv.block_tokens == 16 && dim == 64 && group <= 3 && w.stride <= kFusedMaxT)
+        return launch_fused_decode(s, qkv, ldq, heads, kv_heads, meta, kv, layer, out, ldo, w);
     if (kv.block_tokens == 16 && dim == 64)
         return launch_pair<16, 64>(s, qkv, ldq, heads, kv_heads, dim, meta, kv, layer, out, ldo, w, decode);
     return launch_pair<0, 0>(s, qkv, ldq, heads, kv_heads, dim, meta, kv, layer, out, ldo, w, decode);

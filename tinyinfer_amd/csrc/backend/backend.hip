@@ -16,6 +16,7 @@
 #include <cstring>
 #include <new>
 #include <string>
+#include <unordered_map>
 #include <vector>
 
 #include "../../../include/mp_hip.h"
@@ -68,7 +69,17 @@ struct mp_hip {
     int32_t* meta = nullptr;  // tokens | row_seq | row_pos | seq_slot | seq_last_row | blocks | items
     size_t meta_capacity = 0;   // int32 entries
     int32_t* results = nullptr;  // argmax[seqs] | nonfinite[seqs]
-    std::vector<int32_t> host_meta;
+    // Block-table entries written since the last flush (table index ->
+    // block id): applied on the device at the start of the next forward
+    // (or sync), uploaded with that call's metadata.
+    std::unordered_map<int32_t, int32_t> pending_tables;
+    // Pinned host staging of the metadata upload and of the results, reused
+    // across calls; `staged` marks the last upload out of the meta staging.
+    int32_t* host_meta = nullptr;
+    size_t host_meta_capacity = 0;  // int32 entries
+    int32_t* host_results = nullptr;
+    size_t host_results_capacity = 0;
+    hipEvent_t staged = nullptr;
     std::vector<void*> allocations;
     // kernel timing (mp_hip_set_timing): event pairs of one forward call
     uint32_t timing = 0;
@@ -89,6 +100,9 @@ int check(mp_hip* h, hipError_t e, const char* what) {
     return fail(h, e == hipErrorOutOfMemory ? MP_OUT_OF_MEMORY : MP_DEVICE_ERROR,
                 std::string(what) + ": " + hipGetErrorString(e));
 }
+
+// Waits for the context's stream (internal: buffers about to be replaced).
+int stream_sync(mp_hip* h) { return check(h, hipStreamSynchronize(h->stream), "model completion"); }
 
 int device_alloc(mp_hip* h, void** out, size_t bytes, const char* what) {
     void* p = nullptr;
@@ -174,7 +188,7 @@ int ensure_workspace(mp_hip* h, int rows, int seqs, int max_length) {
     const size_t need_scratch = attention_scratch_floats(c, rows, max_length);
     if (rows <= h->workspace_rows && seqs <= h->workspace_seqs && need_scratch <= h->scratch_floats)
         return MP_OK;
-    int status = mp_hip_sync(h);
+    int status = stream_sync(h);
     if (status) return status;
     // Whole row tiles, so every quad-layout tile a kernel touches exists.
     const int R = ((rows > h->workspace_rows ? rows : h->workspace_rows) + 63) / 64 * 64;
@@ -230,11 +244,30 @@ int ensure_workspace(mp_hip* h, int rows, int seqs, int max_length) {
     return MP_OK;
 }
 
-// Grow-only per-call metadata (int32 entries).
+// Grow-only pinned host buffer of `entries` int32 (contents not kept).
+int ensure_pinned(mp_hip* h, int32_t** buffer, size_t* capacity, size_t entries, const char* what) {
+    if (entries <= *capacity) return MP_OK;
+    int status = stream_sync(h);
+    if (status) return status;
+    if (*buffer) (void)hipHostFree(*buffer);
+    *buffer = nullptr;
+    *capacity = 0;
+    const size_t cap = entries + entries / 2;
+    if ((status = check(h, hipHostMalloc((void**)buffer, sizeof(int32_t) * cap, hipHostMallocDefault), what)))
+        return status;
+    *capacity = cap;
+    return MP_OK;
+}
+
+// Grow-only per-call metadata (int32 entries), device and pinned host.
 int ensure_call_buffers(mp_hip* h, size_t meta_entries) {
     int status = MP_OK;
+    // The previous upload out of the host staging must have been read.
+    if (h->staged && (status = check(h, hipEventSynchronize(h->staged), "metadata upload"))) return status;
+    if ((status = ensure_pinned(h, &h->host_meta, &h->host_meta_capacity, meta_entries, "allocate pinned metadata")))
+        return status;
     if (meta_entries > h->meta_capacity) {
-        if ((status = mp_hip_sync(h))) return status;
+        if ((status = stream_sync(h))) return status;
         device_free(h, h->meta);
         h->meta = nullptr;
         h->meta_capacity = 0;
@@ -242,6 +275,35 @@ int ensure_call_buffers(mp_hip* h, size_t meta_entries) {
         if ((status = device_alloc(h, (void**)&h->meta, sizeof(int32_t) * cap, "allocate call metadata"))) return status;
         h->meta_capacity = cap;
     }
+    return status;
+}
+
+// Appends the pending block-table entries to `dst` as (index, block) pairs
+// and clears them; returns the number of pairs.
+size_t take_pending_tables(mp_hip* h, int32_t* dst) {
+    size_t n = 0;
+    for (const auto& kv : h->pending_tables) {
+        dst[2 * n] = kv.first;
+        dst[2 * n + 1] = kv.second;
+        ++n;
+    }
+    h->pending_tables.clear();
+    return n;
+}
+
+// Uploads and applies pending block-table entries on the context's stream.
+int flush_tables(mp_hip* h) {
+    if (h->pending_tables.empty()) return MP_OK;
+    const size_t n = h->pending_tables.size();
+    int status = ensure_call_buffers(h, 2 * n);
+    if (status) return status;
+    take_pending_tables(h, h->host_meta);
+    status = check(h, hipMemcpyAsync(h->meta, h->host_meta, sizeof(int32_t) * 2 * n, hipMemcpyHostToDevice,
+                                      h->stream), "upload block table entries");
+    if (!status) status = check(h, hipEventRecord(h->staged, h->stream), "metadata upload event");
+    if (!status)
+        status = check(h, mphip::launch_table_update(h->stream, h->tables, reinterpret_cast<const int2*>(h->meta),
+                                                     (int)n), "apply block table entries");
     return status;
 }
 
@@ -266,12 +328,16 @@ int mp_hip_create(const mp_model_desc* model, const mp_kv_desc* kv, mp_hip** out
         c.intermediate % 4 || c.heads / c.kv_heads > 8 ||
         kv->block_tokens < 4 || kv->block_tokens % 4 ||
         kv->block_tokens * (c.hidden / c.heads) > 8192 || kv->max_blocks < 1 ||
-        kv->max_sequences < 1 || kv->max_sequence_blocks < 1 || kv->max_sequence_blocks > 2048) {
+        kv->max_sequences < 1 || kv->max_sequence_blocks < 1 || kv->max_sequence_blocks > 2048 ||
+        // page offsets are 32-bit float4 indices in the decode attention
+        (uint64_t)kv->max_blocks * (uint64_t)c.layers * (uint64_t)kv->block_tokens *
+                (uint64_t)(c.kv_heads * (c.hidden / c.heads)) / 4 > 0xFFFFFFFFull) {
         delete h;
         return MP_INVALID_ARGUMENT;
     }
     int status = check(h, hipGetDevice(&h->device), "get device");
     if (!status) status = check(h, hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking), "create model stream");
+    if (!status) status = check(h, hipEventCreateWithFlags(&h->staged, hipEventDisableTiming), "create upload event");
     const size_t hd = c.hidden;
     h->input_norm.assign(c.layers, nullptr);
     h->post_norm.assign(c.layers, nullptr);
@@ -334,6 +400,9 @@ int mp_hip_destroy(mp_hip* h) {
     if (!h) return MP_OK;
     if (h->stream) (void)hipStreamSynchronize(h->stream);
     for (hipEvent_t ev : h->events) (void)hipEventDestroy(ev);
+    if (h->staged) (void)hipEventDestroy(h->staged);
+    if (h->host_meta) (void)hipHostFree(h->host_meta);
+    if (h->host_results) (void)hipHostFree(h->host_results);
     for (void* p : h->allocations)
         if (p) (void)hipFree(p);
     if (h->stream) (void)hipStreamDestroy(h->stream);
@@ -422,12 +491,12 @@ int mp_hip_table_write(mp_hip* h, int32_t slot, int32_t first, const int32_t* bl
         if (blocks[i] < 0 || blocks[i] >= h->kv.max_blocks)
             return fail(h, MP_INVALID_ARGUMENT, "block id out of range");
     if (!count) return MP_OK;
-    int32_t* dst = h->tables + (size_t)slot * h->kv.max_sequence_blocks + first;
-    const int status = check(h, hipMemcpyAsync(dst, blocks, sizeof(int32_t) * count,
-                                               hipMemcpyHostToDevice, h->stream),
-                             "upload block table entries");
-    if (!status) h->stats.block_table_uploaded_bytes += sizeof(int32_t) * count;
-    return status;
+    // Queued; the next forward (or sync) uploads the entries with its own
+    // metadata and applies them before any kernel reads a table.
+    const int32_t base = slot * h->kv.max_sequence_blocks + first;
+    for (int32_t i = 0; i < count; ++i) h->pending_tables[base + i] = blocks[i];
+    h->stats.block_table_uploaded_bytes += sizeof(int32_t) * count;
+    return MP_OK;
 }
 
 int mp_hip_copy_tail(mp_hip* h, const mp_tail_region* r) {
@@ -516,17 +585,19 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
     size_t items = 0;
     for (const Block& b : blocks) items += (size_t)(b.length + 255) / 256;
     const size_t nblocks = blocks.size();
-    const size_t entries = 3 * (size_t)R + 2 * (size_t)nseq + 2 * nblocks + 2 * items;
+    const size_t table_pairs = h->pending_tables.size();
+    const size_t entries = 3 * (size_t)R + 2 * (size_t)nseq + 2 * nblocks + 2 * items + 2 * table_pairs;
     if ((status = ensure_call_buffers(h, entries))) return status;
-    auto& m = h->host_meta;
-    m.resize(entries);
-    int32_t* m_tokens = m.data();
+    int32_t* const m0 = h->host_meta;
+    int32_t* m_tokens = m0;
     int32_t* m_seq = m_tokens + R;
     int32_t* m_pos = m_seq + R;
     int32_t* m_slot = m_pos + R;
     int32_t* m_last = m_slot + nseq;
     int32_t* m_blocks = m_last + nseq;
     int32_t* m_items = m_blocks + 2 * nblocks;
+    int32_t* m_tables = m_items + 2 * items;
+    take_pending_tables(h, m_tables);
     int r = 0;
     for (int s = 0; s < nseq; ++s) {
         for (int i = 0; i < steps[s].count; ++i, ++r) {
@@ -546,8 +617,13 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
             m_items[2 * it + 1] = ch;
         }
     }
-    status = check(h, hipMemcpyAsync(h->meta, m.data(), sizeof(int32_t) * entries, hipMemcpyHostToDevice, h->stream),
+    status = check(h, hipMemcpyAsync(h->meta, m0, sizeof(int32_t) * entries, hipMemcpyHostToDevice, h->stream),
                    "upload input tokens");
+    if (!status) status = check(h, hipEventRecord(h->staged, h->stream), "metadata upload event");
+    if (!status && table_pairs)
+        status = check(h, mphip::launch_table_update(h->stream, h->tables,
+                                                     reinterpret_cast<const int2*>(h->meta + (m_tables - m0)),
+                                                     (int)table_pairs), "apply block table entries");
     if (status) return status;
     h->stats.token_uploaded_bytes += sizeof(int32_t) * R;
     mphip::RowMeta meta{h->meta, h->meta + R, h->meta + 2 * (size_t)R, h->meta + 3 * (size_t)R,
@@ -556,8 +632,8 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
     mphip::PagedKv kv{h->keys, h->values, h->tables, h->kv.max_sequence_blocks,
                       c.layers, h->kv.block_tokens, kvw};
     mphip::AttentionWork work{};
-    work.blocks = reinterpret_cast<const int2*>(m_blocks - m.data() + h->meta);
-    work.items = reinterpret_cast<const int2*>(m_items - m.data() + h->meta);
+    work.blocks = reinterpret_cast<const int2*>(m_blocks - m0 + h->meta);
+    work.items = reinterpret_cast<const int2*>(m_items - m0 + h->meta);
     work.blocks_count = (int)nblocks;
     work.items_count = (int)items;
     work.scores = h->scratch;
@@ -624,8 +700,11 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
         return r;
     });
     if ((status = check(h, e, "model kernel launch"))) return status;
-    std::vector<int32_t> results(2 * (size_t)nseq);
-    status = check(h, hipMemcpyAsync(results.data(), h->results, sizeof(int32_t) * 2 * nseq, hipMemcpyDeviceToHost, s), "download argmax");
+    if ((status = ensure_pinned(h, &h->host_results, &h->host_results_capacity, 2 * (size_t)nseq,
+                                "allocate pinned results")))
+        return status;
+    int32_t* const results = h->host_results;
+    status = check(h, hipMemcpyAsync(results, h->results, sizeof(int32_t) * 2 * nseq, hipMemcpyDeviceToHost, s), "download argmax");
     if (!status && logits) {
         status = check(h, hipMemcpyAsync(logits, h->logits, sizeof(float) * (size_t)nseq * c.vocabulary, hipMemcpyDeviceToHost, s), "download logits");
         if (!status) h->stats.logits_downloaded_bytes += sizeof(float) * (size_t)nseq * c.vocabulary;
@@ -642,8 +721,8 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
         if (h->spans[i] == MP_TIME_PROJECTION) t.projection_ns += ns, ++t.projection_launches;
         if (h->spans[i] == MP_TIME_HEAD) t.head_ns += ns, ++t.head_launches;
     }
-    std::memcpy(argmax, results.data(), sizeof(int32_t) * nseq);
-    if (nonfinite) std::memcpy(nonfinite, results.data() + nseq, sizeof(int32_t) * nseq);
+    std::memcpy(argmax, results, sizeof(int32_t) * nseq);
+    if (nonfinite) std::memcpy(nonfinite, results + nseq, sizeof(int32_t) * nseq);
     ++h->stats.forward_calls;
     h->stats.forward_rows += R;
     for (int i = 0; i < nseq; ++i)
@@ -679,6 +758,8 @@ int mp_hip_paged_attention_decode(const float* q, const float* keys, const float
 
 int mp_hip_sync(mp_hip* h) {
     if (!h) return MP_INVALID_ARGUMENT;
+    const int status = flush_tables(h);
+    if (status) return status;
     return check(h, hipStreamSynchronize(h->stream), "model completion");
 }
 

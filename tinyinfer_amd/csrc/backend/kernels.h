@@ -103,6 +103,10 @@ constexpr int kAttentionLdsScores = 10240;
 hipError_t launch_copy_region(hipStream_t s, float* keys, float* values, uint64_t destination, uint64_t source,
                               uint64_t pitch, uint64_t width, uint64_t rows);
 
+// tables[updates[i].x] = updates[i].y for i < count (queued block-table
+// entries; the indices are distinct).
+hipError_t launch_table_update(hipStream_t s, int32_t* tables, const int2* updates, int count);
+
 // dst[c*ld_dst + r] = src[r*cols + c] for a rows x cols matrix.
 hipError_t launch_transpose(hipStream_t s, const float* src, float* dst, int rows, int cols, int ld_dst);
 

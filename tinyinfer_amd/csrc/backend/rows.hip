@@ -160,6 +160,12 @@ __global__ void copy_region_kernel(float* keys, float* values, uint64_t destinat
     }
 }
 
+// tables[updates[i].x] = updates[i].y; the indices are distinct.
+__global__ void table_update_kernel(int32_t* __restrict__ tables, const int2* __restrict__ updates, int count) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < count; i += gridDim.x * blockDim.x)
+        tables[updates[i].x] = updates[i].y;
+}
+
 __global__ void transpose_kernel(const float* __restrict__ src, float* __restrict__ dst, int rows, int cols,
                                  int ld_dst) {
     __shared__ float tile[32][33];
@@ -206,6 +212,12 @@ hipError_t launch_copy_region(hipStream_t s, float* keys, float* values, uint64_
                               uint64_t pitch, uint64_t width, uint64_t rows) {
     if (!rows || !width) return hipSuccess;
     copy_region_kernel<<<dim3((unsigned)rows, 2), 256, 0, s>>>(keys, values, destination, source, pitch, width);
+    return hipGetLastError();
+}
+
+hipError_t launch_table_update(hipStream_t s, int32_t* tables, const int2* updates, int count) {
+    if (count <= 0) return hipSuccess;
+    table_update_kernel<<<std::min((count + 255) / 256, 64), 256, 0, s>>>(tables, updates, count);
     return hipGetLastError();
 }
 
