@@ -31,76 +31,81 @@ __global__ __launch_bounds__(256) void embed_kernel(const float* __restrict__ em
 }
 
 // out[r] = (x[src(r)] * scale) * weight with scale = 1/sqrt(sum/width + eps),
-// sum = sequential float sum of squares (llama_runner.cpp:10-16). One
-// work-group per output row tile; lane l of every wavefront handles row l.
-// The tile (up to kRmsQuads quads at a time) is copied into LDS with every
-// copy in flight at once (global_load_lds); wavefront 0 runs the 64 row
-// chains over it in column order; the normalized tile is written from LDS
-// (the whole tile when it fits, else re-read from global memory).
-constexpr int kRmsQuads = 144;  // 144 KB of LDS: a whole 576-wide tile
+// sum = sequential float sum of squares (llama_runner.cpp:10-16).
+// A work-group of kRmsWaves wavefronts per (64-row tile, column slice),
+// lane = row. The row tile is taken kRmsWaves*kRmsPer quads (4 columns) at
+// a time, all loads in flight together: wavefront 0 sums its own first
+// kRmsPer quads straight from registers while the other wavefronts land
+// theirs in LDS, then continues over the LDS copy. Every work-group of a
+// tile computes the same scales and writes only its slice of columns.
+constexpr int kRmsWaves = 4;
+constexpr int kRmsPer = 36;    // quads per wavefront per pass (144 VGPRs)
+constexpr int kRmsSlices = 8;  // work-groups per row tile
 
-typedef __attribute__((address_space(3))) void* LdsPtr;
-
-__global__ __launch_bounds__(256) void rms_kernel(const float* __restrict__ x, const int32_t* __restrict__ row_map,
-                                                  const float* __restrict__ weight, float* __restrict__ out,
-                                                  int rows, int width, float eps) {
-    __shared__ float4 tile_s[kRmsQuads * 64];
+__global__ __launch_bounds__(kRmsWaves * 64) void rms_kernel(const float* __restrict__ x,
+                                                             const int32_t* __restrict__ row_map,
+                                                             const float* __restrict__ weight,
+                                                             float* __restrict__ out, int rows, int width,
+                                                             float eps) {
+    __shared__ float4 tile_s[(kRmsWaves - 1) * kRmsPer * 64];
     __shared__ float scale_s[64];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int tile = blockIdx.x;
+    const int tile = blockIdx.x, slice = blockIdx.y;
     const int quads = width >> 2;
-    const float4* x4 = reinterpret_cast<const float4*>(x);
     const int row = tile * 64 + lane;
     const int src = row < rows ? (row_map ? row_map[row] : row) : -1;
     const int src_c = src < 0 ? 0 : src;
     // Quad q of this lane's source row.
-    const float4* xrow = x4 + (size_t)(src_c >> 6) * quads * 64 + (src_c & 63);
+    const float4* xrow = reinterpret_cast<const float4*>(x) + (size_t)(src_c >> 6) * quads * 64 + (src_c & 63);
     float sum = 0.0f;
-    for (int q0 = 0; q0 < quads; q0 += kRmsQuads) {
-        const int nq = min(kRmsQuads, quads - q0);
-        if (q0) __syncthreads();  // previous chunk fully read
-        for (int q = wave; q < nq; q += 4)
-            __builtin_amdgcn_global_load_lds((const void*)(xrow + (size_t)(q0 + q) * 64), (LdsPtr)(tile_s + q * 64),
-                                             16, 0, 0);
-        __builtin_amdgcn_s_waitcnt(0);
+    auto add4 = [&](const float4& v) {
+        sum = sum + v.x * v.x;
+        sum = sum + v.y * v.y;
+        sum = sum + v.z * v.z;
+        sum = sum + v.w * v.w;
+    };
+    for (int p0 = 0; p0 < quads; p0 += kRmsWaves * kRmsPer) {
+        const int q0 = p0 + wave * kRmsPer;  // this wavefront's quads
+        float4 v[kRmsPer];
+#pragma unroll
+        for (int i = 0; i < kRmsPer; ++i) v[i] = xrow[(size_t)min(q0 + i, quads - 1) * 64];
+        if (wave == 0) {
+#pragma unroll
+            for (int i = 0; i < kRmsPer; ++i)
+                if (q0 + i < quads) add4(v[i]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < kRmsPer; ++i) tile_s[((wave - 1) * kRmsPer + i) * 64 + lane] = v[i];
+        }
         __syncthreads();
         if (wave == 0) {
+            const int n = min(quads - (p0 + kRmsPer), (kRmsWaves - 1) * kRmsPer);
             const float4* t4 = tile_s + lane;
             int q = 0;
-            for (; q + 8 <= nq; q += 8) {
-                float4 v[8];
+            for (; q + 8 <= n; q += 8) {
+                float4 u[8];
 #pragma unroll
-                for (int j = 0; j < 8; ++j) v[j] = t4[(q + j) * 64];
+                for (int j = 0; j < 8; ++j) u[j] = t4[(q + j) * 64];
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    sum = sum + v[j].x * v[j].x;
-                    sum = sum + v[j].y * v[j].y;
-                    sum = sum + v[j].z * v[j].z;
-                    sum = sum + v[j].w * v[j].w;
-                }
+                for (int j = 0; j < 8; ++j) add4(u[j]);
             }
-            for (; q < nq; ++q) {
-                const float4 v = t4[q * 64];
-                sum = sum + v.x * v.x;
-                sum = sum + v.y * v.y;
-                sum = sum + v.z * v.z;
-                sum = sum + v.w * v.w;
-            }
+            for (; q < n; ++q) add4(t4[q * 64]);
         }
+        __syncthreads();
     }
     if (wave == 0) scale_s[lane] = 1.0f / sqrtf(sum / (float)width + eps);
     __syncthreads();
     if (src < 0) return;
-    const float s = scale_s[lane];
+    const float scale = scale_s[lane];
     const float4* w4 = reinterpret_cast<const float4*>(weight);
     float4* o4 = reinterpret_cast<float4*>(out) + (size_t)tile * quads * 64 + lane;
-    const bool resident = quads <= kRmsQuads;
-#pragma unroll 4
-    for (int q = wave; q < quads; q += 4) {
-        const float4 v = resident ? tile_s[q * 64 + lane] : xrow[(size_t)q * 64];
+    const int per = (quads + kRmsSlices - 1) / kRmsSlices;
+    const int qe = min(quads, (slice + 1) * per);
+    for (int q = slice * per + wave; q < qe; q += kRmsWaves) {
+        const float4 v = xrow[(size_t)q * 64];
         const float4 w = w4[q];
-        o4[(size_t)q * 64] = make_float4(v.x * s * w.x, v.y * s * w.y, v.z * s * w.z, v.w * s * w.w);
+        o4[(size_t)q * 64] = make_float4(v.x * scale * w.x, v.y * scale * w.y, v.z * scale * w.z, v.w * scale * w.w);
     }
 }
 
@@ -195,7 +200,8 @@ hipError_t launch_embed(hipStream_t s, const float* embedding, const int32_t* to
 hipError_t launch_rms(hipStream_t s, const float* x, const int32_t* row_map, const float* weight, float* out,
                       int rows, int width, float eps) {
     if (rows <= 0) return hipSuccess;
-    rms_kernel<<<(rows + 63) / 64, 256, 0, s>>>(x, row_map, weight, out, rows, width, eps);
+    rms_kernel<<<dim3((rows + 63) / 64, kRmsSlices), kRmsWaves * 64, 0, s>>>(x, row_map, weight, out, rows, width,
+                                                                             eps);
     return hipGetLastError();
 }
 
