@@ -15,8 +15,15 @@
 // staging), NS-2 chunks ahead of the arithmetic. Each stage is a separate LDS
 // object so that the compiler's own LDS-DMA wait tracking tells stages
 // apart; the cross-wavefront hand-off is an explicit vmcnt wait plus a bare
-// s_barrier. Decode (64 rows) uses C = 1 so that the outputs spread over as
-// many SIMDs as exist; prefill and the LM head use larger C.
+// s_barrier. Prefill and the LM head use this kernel with C > 1.
+//
+// Decode (one row tile) has too few outputs for C > 1, and with C = 1 the
+// LDS copy of the weights costs as much LDS bandwidth as x. There
+// gemm_column_kernel runs instead: one column per wavefront, the column's
+// weights held in VGPRs (each 16-lane row of the wavefront holds the same
+// 16 floats per register) and handed to all 64 lanes by a DPP row broadcast
+// folded into v_mul_f32, while x streams from global memory through a
+// register ring.
 #include "exact_math.h"
 #include "kernels.h"
 #include "layout.h"
@@ -337,6 +344,161 @@ hipError_t launch_shape(hipStream_t s, const GemmArgs& a) {
     return hipGetLastError();
 }
 
+
+// ---------------------------------------------------------------------------
+// Decode projections: one output column per wavefront.
+
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+constexpr int kColRing = 8;    // x quads in flight per wavefront
+constexpr int kColBlocks = 8;  // 64-k weight blocks held per wavefront
+
+// w * x with w taken from lane I of this lane's 16-lane row (DPP
+// row_newbcast, which the compiler folds into the multiply).
+template <int I>
+__device__ __forceinline__ float mul_bcast(float w, float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(w), 0x150 + I, 0xf, 0xf, false)) * x;
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// out[r][n] for the 64 rows r of tile blockIdx.y (lane = row) and column
+// n = blockIdx.x*NW + wave; M = 2 runs the gate (w) and up (w2) chains side
+// by side for the SwiGLU epilogue. k advances in quads (4 k) and 64-k blocks
+// of 16 quads: lane l holds w[n][64J + 4(l%16) .. +3] of block J in one f4v,
+// so quad i of block J multiplies by lane i's four floats. The products of
+// quad q+1 are formed between the four dependent adds of quad q. Requires
+// inner % 64 == 0; rows past a.rows read the tile's padding and are not
+// stored.
+//
+// The weights sit in a ring of D blocks. With RELOAD the slot of block J
+// takes block J + D once J is spent; without it the host guarantees
+// inner <= 64*D, so the whole column is fetched before the first product.
+// That is the faster form where it fits: s_waitcnt retires loads in issue
+// order, so a weight block fetched from HBM during the loop stalls every x
+// ring wait behind it, while fetched up front it costs one round trip per
+// launch.
+template <int M, int NW, int EPI, int D = kColBlocks, bool RELOAD = true>
+__global__ __launch_bounds__(NW * 64) void gemm_column_kernel(GemmArgs a) {
+    constexpr int RX = kColRing;
+    static_assert((D * 16) % RX == 0, "ring slots repeat every D blocks");
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int tile = blockIdx.y;
+    const int N = a.columns;
+    const int col = blockIdx.x * NW + wave;
+    const int n = min(col, N - 1);
+    const int kq = a.inner >> 2, KB = a.inner >> 6;
+    const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(a.x + (size_t)tile * kq * 256, (uint32_t)kq * 1024u);
+    const int xoff = lane * 16;
+    const f4v* ws[2];
+    ws[0] = reinterpret_cast<const f4v*>(a.w) + (size_t)n * kq + (lane & 15);
+    ws[1] = reinterpret_cast<const f4v*>(M == 2 ? a.w2 : a.w) + (size_t)n * kq + (lane & 15);
+    auto load_x = [&](int q) {
+        return __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(xrs, xoff, min(q, kq - 1) * 1024, 0));
+    };
+
+    float acc[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) acc[m] = 0.0f;
+    f4v wr[D][M];
+    f4v xr[RX];
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+#pragma unroll
+        for (int m = 0; m < M; ++m) wr[d][m] = ws[m][min(d, KB - 1) * 16];
+#pragma unroll
+    for (int i = 0; i < RX; ++i) xr[i] = load_x(i);
+    float pn[M][4];  // products of the next quad
+    {
+        const f4v xv = xr[0];
+        xr[0] = load_x(RX);
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            pn[m][0] = mul_bcast<0>(wr[0][m].x, xv.x);
+            pn[m][1] = mul_bcast<0>(wr[0][m].y, xv.y);
+            pn[m][2] = mul_bcast<0>(wr[0][m].z, xv.z);
+            pn[m][3] = mul_bcast<0>(wr[0][m].w, xv.w);
+        }
+    }
+    for (int J0 = 0; J0 < KB; J0 += D) {
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            const int J = J0 + d;
+            if (J >= KB) break;
+            // Quad i of block J: add its products in k order while forming
+            // those of the next quad (lane i+1 of this block, or lane 0 of
+            // the next block held in wr[(d+1)%D]).
+#define MP_COLUMN_QUAD(i)                                                               \
+    {                                                                                   \
+        const int slot = (d * 16 + (i) + 1) % RX;                                       \
+        const int dn = (i) == 15 ? (d + 1) % D : d;                                     \
+        const f4v xv = xr[slot];                                                        \
+        xr[slot] = load_x(J * 16 + (i) + 1 + RX);                                       \
+        for (int m = 0; m < M; ++m) {                                                   \
+            float t = acc[m];                                                           \
+            t = t + pn[m][0];                                                           \
+            pn[m][0] = mul_bcast<((i) + 1) & 15>(wr[dn][m].x, xv.x);                    \
+            __builtin_amdgcn_sched_barrier(0);                                          \
+            t = t + pn[m][1];                                                           \
+            pn[m][1] = mul_bcast<((i) + 1) & 15>(wr[dn][m].y, xv.y);                    \
+            __builtin_amdgcn_sched_barrier(0);                                          \
+            t = t + pn[m][2];                                                           \
+            pn[m][2] = mul_bcast<((i) + 1) & 15>(wr[dn][m].z, xv.z);                    \
+            __builtin_amdgcn_sched_barrier(0);                                          \
+            t = t + pn[m][3];                                                           \
+            pn[m][3] = mul_bcast<((i) + 1) & 15>(wr[dn][m].w, xv.w);                    \
+            __builtin_amdgcn_sched_barrier(0);                                          \
+            acc[m] = t;                                                                 \
+        }                                                                               \
+    }
+            MP_COLUMN_QUAD(0) MP_COLUMN_QUAD(1) MP_COLUMN_QUAD(2) MP_COLUMN_QUAD(3)
+            MP_COLUMN_QUAD(4) MP_COLUMN_QUAD(5) MP_COLUMN_QUAD(6) MP_COLUMN_QUAD(7)
+            MP_COLUMN_QUAD(8) MP_COLUMN_QUAD(9) MP_COLUMN_QUAD(10) MP_COLUMN_QUAD(11)
+            MP_COLUMN_QUAD(12) MP_COLUMN_QUAD(13) MP_COLUMN_QUAD(14)
+            // Block J's weights are spent; the slot takes block J + D.
+            if (RELOAD) {
+#pragma unroll
+                for (int m = 0; m < M; ++m) wr[d][m] = ws[m][min(J + D, KB - 1) * 16];
+            }
+            MP_COLUMN_QUAD(15)
+#undef MP_COLUMN_QUAD
+        }
+    }
+
+    const int row = tile * 64 + lane;
+    if (row >= a.rows || col >= N) return;
+    float* o = a.out + quad_index(row, n, N);
+    if (EPI == kStore) {
+        *o = acc[0];
+    } else if (EPI == kResidual) {
+        *o = *o + acc[0];
+    } else if (EPI == kSwiglu) {
+        const float g = acc[0];
+        *o = (g / (1.0f + ref_expf(-g))) * acc[M - 1];
+    }
+}
+
+
+template <int M, int NW, int EPI, int D, bool RELOAD>
+hipError_t launch_column(hipStream_t s, const GemmArgs& a) {
+    const dim3 grid((a.columns + NW - 1) / NW, (a.rows + 63) / 64);
+    gemm_column_kernel<M, NW, EPI, D, RELOAD><<<grid, NW * 64, 0, s>>>(a);
+    return hipGetLastError();
+}
+
+// A weight column of up to 24 64-k blocks (inner <= 1536) is held whole;
+// longer ones stream through a kColBlocks ring.
+template <int EPI>
+hipError_t launch_column_one(hipStream_t s, const GemmArgs& a) {
+    const int blocks = a.inner / 64;
+    if (blocks <= 9) return launch_column<1, 4, EPI, 9, false>(s, a);
+    if (blocks <= 24) return launch_column<1, 4, EPI, 24, false>(s, a);
+    return launch_column<1, 4, EPI, kColBlocks, true>(s, a);
+}
+
 }  // namespace
 
 int head_groups(int columns) { return (columns + kHeadColumns - 1) / kHeadColumns; }
@@ -344,9 +506,19 @@ int head_groups(int columns) { return (columns + kHeadColumns - 1) / kHeadColumn
 hipError_t launch_gemm(hipStream_t s, Epilogue epilogue, const GemmArgs& a) {
     if (a.rows <= 0 || a.columns <= 0) return hipSuccess;
     if (a.inner <= 0 || a.inner % 4 || a.columns % 4) return hipErrorInvalidValue;
-    // Enough chains for every SIMD at one output per lane when the row count
-    // is small (decode); more columns per wavefront when rows are plentiful.
+    // One row tile (decode): one column per wavefront with register-held
+    // weights. More rows: C = 4 columns per wavefront through LDS.
     const bool many = a.rows > 64;
+    if (!many && a.inner % 64 == 0) {
+        switch (epilogue) {
+        case kStore: return launch_column_one<kStore>(s, a);
+        case kResidual: return launch_column_one<kResidual>(s, a);
+        case kSwiglu:
+            return a.inner <= 9 * 64 ? launch_column<2, 2, kSwiglu, 9, false>(s, a)
+                                     : launch_column<2, 2, kSwiglu, kColBlocks, true>(s, a);
+        default: break;
+        }
+    }
     switch (epilogue) {
     case kStore: return many ? launch_shape<4, 4, kStore, 5>(s, a) : launch_shape<1, 4, kStore, 6>(s, a);
     case kResidual: return many ? launch_shape<4, 4, kResidual, 5>(s, a) : launch_shape<1, 4, kResidual, 6>(s, a);
