@@ -18,6 +18,9 @@
 //           output chains, lane = d.
 // Blocks arrive sorted by decreasing length so the longest chains start
 // first.
+#include <type_traits>
+
+#include "dpp.h"
 #include "exact_math.h"
 #include "kernels.h"
 #include "layout.h"
@@ -430,17 +433,27 @@ __global__ __launch_bounds__(64) void attn_pv_kernel(int heads, int kv_heads, in
 // kFusedMaxT, after the scores kernel: one work-group of 8 wavefronts per
 // (sequence row, KV head) forms the softmax and the output of its G query
 // heads.
-//   1. the row's scores of the G heads go to LDS; maximum (order-free);
-//   2. e_t = expf(s_t - m), all threads;
-//   3. den: wavefront h, lane 0, sums head h's e_t in token order;
+//   1-3. wavefronts G..7 (producers): m = maximum of each head's chunk
+//      maxima (order-free); e_t = expf(s_t - m) for 64-token batches, lane
+//      = token, into LDS, then a per-batch ready flag;
+//      wavefront h < G (consumer): den of head h, adding e_t in token order
+//      batch by batch as the flags come up (every lane runs the same chain
+//      from LDS broadcast reads);
 //   4. p_t = e_t / den, all threads;
 //   5. output: wavefront h adds p_t * v_td (product rounded as the reference
 //      rounds it; each dependent add is followed by the next multiply) in
 //      token order, lane = d, with V pages streamed through a ring of
-//      registers kRingPages ahead. The G wavefronts read the same pages, so
-//      two of three reads hit the work-group's L1; LDS only serves p_t.
+//      registers kRingPages ahead (the producers touched the first pages
+//      after their e_t). The G wavefronts read the same pages, so two of three
+//      reads hit the work-group's L1. p_t reaches the lanes by DPP row
+//      broadcast from one f4 per lane per 64 tokens.
 constexpr int kFusedMaxT = 4096;
 constexpr int kFusedThreads = 512;
+// Producer wavefronts touch up to this many V pages each after their e_t
+// (more floods HBM while the softmax still needs it).
+constexpr int kTouchPages = 16;
+
+typedef __attribute__((address_space(3))) uint32_t LdsU32;
 
 // Work-group barrier that orders LDS only: this wavefront's LDS accesses
 // complete (lgkmcnt(0)) before the barrier; global loads stay in flight.
@@ -457,8 +470,9 @@ __global__ __launch_bounds__(kFusedThreads) void attn_decode_kernel(int heads, R
                                                                     int ldo) {
     static_assert(G >= 1 && G < kFusedThreads / 64, "waves per head");
     __shared__ float4 sc4[G][kFusedMaxT / 4];  // s_t, then e_t, then p_t
-    __shared__ float red_s[kFusedThreads / 64][G];
     __shared__ float den_s[G];
+    __shared__ uint64_t exp_tab[32];
+    __shared__ uint32_t ready_s[G][kFusedMaxT / 64];  // e of batch b of head h is in LDS
     __shared__ uint32_t voff_s[kFusedMaxT / 16];  // page pg's V of this KV head, in float4 from kv.values
     float* const sc = reinterpret_cast<float*>(&sc4[0][0]);
     const int tid = threadIdx.x, lane = tid & 63;
@@ -474,68 +488,127 @@ __global__ __launch_bounds__(kFusedThreads) void attn_decode_kernel(int heads, R
     const uint32_t page_f4 = (uint32_t)(16 * kv.kv_width / 4);
     for (int i = tid; i < pages; i += kFusedThreads)
         voff_s[i] = ((uint32_t)table_g[i] * (uint32_t)kv.layers + (uint32_t)layer) * page_f4 + (uint32_t)kvh * 256u;
-
-    // ---- 1. scores of the row's G heads and their maxima
-    float mx[G];
+    // Producers (wavefronts G..7) start their first loads before the
+    // barrier: head h's scores of their first batch and its chunk maxima.
+    constexpr int kProducers = kFusedThreads / 64 - G;
+    const int batches = (len + 63) >> 6;  // 64-token batches, 64 * batches <= kFusedMaxT
+    const int nch = (len + 255) >> 8;     // at most 16 chunk maxima
+    // Every batch a producer will handle (b = wave - G + i * kProducers) has
+    // its scores requested here, so the producers wait on one round trip.
+    constexpr int kProducerBatches = (kFusedMaxT / 64 + kProducers - 1) / kProducers;
+    float sall[kProducerBatches][G], cmax[G];
+    if (wave >= G) {
 #pragma unroll
-    for (int h = 0; h < G; ++h) {
-        const float4* src = reinterpret_cast<const float4*>(w.scores + ((size_t)row * heads + kvh * G + h) * w.stride);
-        float m = -INFINITY;
-        const int n4 = (len + 3) >> 2;  // the stride is a multiple of 16: whole float4 stay in the row
-        for (int e = tid; e < n4; e += kFusedThreads) {
-            const float4 v = src[e];
-            sc4[h][e] = v;
-            const int t = 4 * e;
-            m = fmaxf(m, v.x);
-            if (t + 1 < len) m = fmaxf(m, v.y);
-            if (t + 2 < len) m = fmaxf(m, v.z);
-            if (t + 3 < len) m = fmaxf(m, v.w);
+        for (int h = 0; h < G; ++h) {
+            const size_t rh = (size_t)row * heads + kvh * G + h;
+            cmax[h] = w.chunk_max[rh * w.chunks + min(lane, nch - 1)];
         }
-        m = wave_max(m);
-        if (lane == 0) red_s[wave][h] = m;
+#pragma unroll
+        for (int i = 0; i < kProducerBatches; ++i)
+#pragma unroll
+            for (int h = 0; h < G; ++h) {
+                const float* srow = w.scores + ((size_t)row * heads + kvh * G + h) * w.stride;
+                sall[i][h] = srow[min(64 * (wave - G + i * kProducers) + lane, len - 1)];
+            }
     }
+    for (int i = tid; i < G * (kFusedMaxT / 64); i += kFusedThreads) (&ready_s[0][0])[i] = 0u;
+    if (tid < 32) exp_tab[tid] = kExp2Table[tid];
     __syncthreads();
-    // ---- 2. maximum and e_t
+
+    // ---- 1-3. e_t into LDS by the producer wavefronts, den by wavefront h
+    if (wave >= G) {
+        // Producers: batch b goes to wavefront G + b % kProducers; lane =
+        // token. m of each head is the maximum of its chunk maxima.
+        float m[G];
 #pragma unroll
-    for (int h = 0; h < G; ++h) {
-        float m = red_s[0][h];
+        for (int h = 0; h < G; ++h) m[h] = wave_max(cmax[h]);
 #pragma unroll
-        for (int v = 1; v < kFusedThreads / 64; ++v) m = fmaxf(m, red_s[v][h]);
-        mx[h] = m;
-    }
-    for (int t = tid; t < len; t += kFusedThreads) {
+        for (int i = 0; i < kProducerBatches; ++i) {
+            const int b = wave - G + i * kProducers;
+            if (b >= batches) break;
 #pragma unroll
-        for (int h = 0; h < G; ++h) sc[h * kFusedMaxT + t] = ref_expf(sc[h * kFusedMaxT + t] - mx[h]);
-    }
-    lds_barrier();
-    // ---- 3. denominators
-    if (wave < G && lane == 0) {
-        const float4* e4 = sc4[wave];
-        const int full = len >> 2;
-        float den = 0.0f;
-        int q = 0;
-        for (; q + 8 <= full; q += 8) {
-            float4 v[8];
+            for (int h = 0; h < G; ++h)
+                sc[h * kFusedMaxT + 64 * b + lane] = ref_expf_select(sall[i][h] - m[h], exp_tab);
+            // The e writes above precede the flags in this wavefront's LDS order.
+            if (lane == 0) {
 #pragma unroll
-            for (int j = 0; j < 8; ++j) v[j] = e4[q + j];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                den = den + v[j].x;
-                den = den + v[j].y;
-                den = den + v[j].z;
-                den = den + v[j].w;
+                for (int h = 0; h < G; ++h) ((volatile LdsU32*)ready_s[h])[b] = 1u;
             }
         }
-        for (; q < full; ++q) {
-            const float4 v = e4[q];
-            den = den + v.x;
-            den = den + v.y;
-            den = den + v.z;
-            den = den + v.w;
+        // Then touch this KV head's V pages (one dword per 64 bytes, a page
+        // per instruction; this wavefront's share of the first
+        // kTouchPages * kProducers pages, all in flight together) so that the
+        // output chains find them in cache rather than in HBM.
+        const float* vf = kv.values;
+        float touch[kTouchPages];
+#pragma unroll
+        for (int i = 0; i < kTouchPages; ++i)
+            touch[i] = vf[(size_t)voff_s[min(wave - G + i * kProducers, last_page)] * 4 + lane * 16];
+        float sink = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kTouchPages; ++i) sink += touch[i];
+        asm volatile("" ::"v"(sink));
+    } else {
+        // Consumer: head h = wave sums its e_t in token order, every lane the
+        // same chain, a batch as soon as its flag is up. The wait is bounded;
+        // every flag below `batches` is set by a producer.
+        const float4* es4 = sc4[wave];
+        const float* es = sc + wave * kFusedMaxT;
+        // Flags are checked four batches at a time (one 16-byte read); a flag
+        // at or past `batches` counts as set.
+        typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+        typedef __attribute__((address_space(3))) u4v LdsU4;
+        volatile LdsU4* const flags4 = (volatile LdsU4*)ready_s[wave];
+        auto wait_group = [&](int g) {
+            for (int spin = 0; spin < (1 << 16); ++spin) {
+                const u4v f = flags4[g];
+                const int b = 4 * g;
+                const bool ok = (f.x | (b >= batches)) && (f.y | (b + 1 >= batches)) &&
+                                (f.z | (b + 2 >= batches)) && (f.w | (b + 3 >= batches));
+                if (__builtin_amdgcn_readfirstlane(ok ? 1 : 0)) break;
+                __builtin_amdgcn_s_sleep(1);
+            }
+            asm volatile("" ::: "memory");
+        };
+        auto read_batch = [&](int b, float4 (&ev)[16]) {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) ev[j] = es4[16 * b + j];
+        };
+        float den = 0.0f;
+        auto add_batch = [&](const float4 (&ev)[16]) {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                den = den + ev[j].x;
+                den = den + ev[j].y;
+                den = den + ev[j].z;
+                den = den + ev[j].w;
+            }
+        };
+        // Full batches in groups of four; within a group batch b+1 is read
+        // while batch b is added.
+        const int full = len >> 6;
+        float4 e0[16], e1[16];
+        for (int g = 0; 4 * g < full; ++g) {
+            const int b = 4 * g;
+            wait_group(g);
+            read_batch(b, e0);
+            if (b + 1 < full) read_batch(b + 1, e1);
+            add_batch(e0);
+            if (b + 1 < full) {
+                if (b + 2 < full) read_batch(b + 2, e0);
+                add_batch(e1);
+                if (b + 2 < full) {
+                    if (b + 3 < full) read_batch(b + 3, e1);
+                    add_batch(e0);
+                    if (b + 3 < full) add_batch(e1);
+                }
+            }
         }
-        const float* e = reinterpret_cast<const float*>(e4);
-        for (int u = full * 4; u < len; ++u) den = den + e[u];
-        den_s[wave] = den;
+        if (full < batches) {
+            wait_group(full >> 2);
+            for (int t = 64 * full; t < len; ++t) den = den + es[t];
+        }
+        if (lane == 0) den_s[wave] = den;
     }
     lds_barrier();
     // ---- 4. p_t = e_t / den
@@ -548,9 +621,14 @@ __global__ __launch_bounds__(kFusedThreads) void attn_decode_kernel(int heads, R
 
     // ---- 5. output chains (no barrier from here on)
     if (wave >= G) return;
-    const float4* p4 = sc4[wave];
+    // p of 64-token group g: lane l holds p[64g + 4(l%16) .. +3], so the p of
+    // token 64g + 4i + c is component c of lane i of every 16-lane row and
+    // reaches all lanes through a DPP row broadcast folded into the multiply.
+    const f4v* pg4 = reinterpret_cast<const f4v*>(sc4[wave]) + (lane & 15);
+    auto read_group = [&](int g) { return pg4[16 * min(g, kFusedMaxT / 64 - 1)]; };
     const float4* vbase = reinterpret_cast<const float4*>(kv.values);
     auto lane4 = [](const float4& v, int c) { return c == 0 ? v.x : c == 1 ? v.y : c == 2 ? v.z : v.w; };
+    auto lane4v = [](const f4v& v, int c) { return c == 0 ? v.x : c == 1 ? v.y : c == 2 ? v.z : v.w; };
     float4 ring[kRingPages][4];
     auto load_page = [&](uint32_t off, float4 (&v)[4]) {
         const float4* src = vbase + __builtin_amdgcn_readfirstlane(off);
@@ -558,54 +636,66 @@ __global__ __launch_bounds__(kFusedThreads) void attn_decode_kernel(int heads, R
         for (int j = 0; j < 4; ++j) v[j] = src[64 * j + lane];
     };
     float acc = 0.0f;
-    // acc += p_t * v_td over a full page: each dependent add is followed by
-    // the next token's multiply.
-    auto add_page = [&](const float4 (&v)[4], const float4 (&pp)[4]) {
-        float prod = pp[0].x * v[0].x;
+    // acc += p_t * v_td over full page K (0..3) of a group: each dependent
+    // add is followed by the next token's multiply.
+    auto add_page = [&](auto kpage, const float4 (&v)[4], const f4v& pv) {
+        constexpr int K = decltype(kpage)::value;
+        float prod = mul_bcast<4 * K>(pv.x, v[0].x);
 #pragma unroll
         for (int t = 0; t < 16; ++t) {
             const float cur = prod;
-            if (t < 15) prod = lane4(pp[(t + 1) >> 2], (t + 1) & 3) * lane4(v[(t + 1) >> 2], (t + 1) & 3);
+            if (t < 15) {
+                const int u = t + 1;
+                prod = mul_bcast_at(4 * K + (u >> 2), lane4v(pv, u & 3), lane4(v[u >> 2], u & 3));
+            }
             acc = acc + cur;
             __builtin_amdgcn_sched_barrier(0);
         }
     };
-    auto read_p = [&](int pg, float4 (&pp)[4]) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) pp[j] = p4[pg * 4 + j];
-    };
-    // Ring invariant at a group boundary pg: ring[r] holds page
-    // min(pg + r, last_page).
+    static_assert(kRingPages == 8, "two p groups per ring turn");
+    // Ring invariant at a turn boundary pg (a multiple of 8): ring[r] holds
+    // page min(pg + r, last_page) and pgrp holds the p groups of pages
+    // pg..pg+7.
 #pragma unroll
     for (int r = 0; r < kRingPages; ++r) load_page(voff_s[min(r, last_page)], ring[r]);
+    f4v pgrp[2] = {read_group(0), read_group(1)};
     const int full_pages = len >> 4;
     int pg = 0;
     for (; pg + kRingPages <= full_pages; pg += kRingPages) {
         uint32_t refill[kRingPages];
 #pragma unroll
         for (int r = 0; r < kRingPages; ++r) refill[r] = voff_s[min(pg + kRingPages + r, last_page)];
-#pragma unroll
-        for (int r = 0; r < kRingPages; ++r) {
-            float4 pp[4];
-            read_p(pg + r, pp);
-            add_page(ring[r], pp);
-            load_page(refill[r], ring[r]);
-        }
+        const f4v next[2] = {read_group((pg >> 2) + 2), read_group((pg >> 2) + 3)};
+        add_page(std::integral_constant<int, 0>(), ring[0], pgrp[0]); load_page(refill[0], ring[0]);
+        add_page(std::integral_constant<int, 1>(), ring[1], pgrp[0]); load_page(refill[1], ring[1]);
+        add_page(std::integral_constant<int, 2>(), ring[2], pgrp[0]); load_page(refill[2], ring[2]);
+        add_page(std::integral_constant<int, 3>(), ring[3], pgrp[0]); load_page(refill[3], ring[3]);
+        add_page(std::integral_constant<int, 0>(), ring[4], pgrp[1]); load_page(refill[4], ring[4]);
+        add_page(std::integral_constant<int, 1>(), ring[5], pgrp[1]); load_page(refill[5], ring[5]);
+        add_page(std::integral_constant<int, 2>(), ring[6], pgrp[1]); load_page(refill[6], ring[6]);
+        add_page(std::integral_constant<int, 3>(), ring[7], pgrp[1]); load_page(refill[7], ring[7]);
+        pgrp[0] = next[0];
+        pgrp[1] = next[1];
     }
     // Fewer than kRingPages full pages and the partial page remain.
 #pragma unroll
     for (int r = 0; r < kRingPages; ++r) {
         const int q = pg + r;
         if (q < pages) {
-            float4 pp[4];
-            read_p(q, pp);
+            const f4v& pv = pgrp[r >> 2];
             if (q < full_pages) {
-                add_page(ring[r], pp);
+                switch (r & 3) {
+                case 0: add_page(std::integral_constant<int, 0>(), ring[r], pv); break;
+                case 1: add_page(std::integral_constant<int, 1>(), ring[r], pv); break;
+                case 2: add_page(std::integral_constant<int, 2>(), ring[r], pv); break;
+                default: add_page(std::integral_constant<int, 3>(), ring[r], pv); break;
+                }
             } else {
                 const int n = len - 16 * q;
 #pragma unroll
                 for (int t = 0; t < 16; ++t)
-                    if (t < n) acc = acc + lane4(pp[t >> 2], t & 3) * lane4(ring[r][t >> 2], t & 3);
+                    if (t < n)
+                        acc = acc + mul_bcast_at(4 * (r & 3) + (t >> 2), lane4v(pv, t & 3), lane4(ring[r][t >> 2], t & 3));
             }
         }
     }

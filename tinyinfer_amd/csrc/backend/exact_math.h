@@ -57,4 +57,37 @@ __device__ __forceinline__ float ref_expf(float x) {
     return (float)y;
 }
 
+// ref_expf without branches: the main path runs for every input (its table
+// index stays in range for any x) and the special cases are selected after,
+// so a wavefront never splits. Same results as ref_expf for every x. `tab`
+// is a copy of kExp2Table (in LDS where the caller keeps global loads for
+// other work in flight: a global table read would wait for all of them).
+__device__ __forceinline__ float ref_expf_select(float x, const uint64_t* tab) {
+    const uint32_t bits = __float_as_uint(x);
+    const uint32_t abstop = (bits >> 20) & 0x7ffu;
+    const double inv_ln2_n = 0x1.71547652b82fep+5;
+    const double shift = 0x1.8p+52;
+    const double xd = (double)x;
+    double kd = __builtin_fma(inv_ln2_n, xd, shift);
+    const uint64_t ki = (uint64_t)__double_as_longlong(kd);
+    kd -= shift;
+    const double r = __builtin_fma(inv_ln2_n, xd, -kd);
+    uint64_t t = tab[ki % 32];
+    t += ki << 47;
+    const double s = __longlong_as_double((long long)t);
+    const double z = __builtin_fma(0x1.c6af84b912394p-20, r, 0x1.ebfce50fac4f3p-13);
+    const double r2 = r * r;
+    double y = __builtin_fma(0x1.62e42ff0c52d6p-6, r, 1.0);
+    y = __builtin_fma(z, r2, y);
+    y = y * s;
+    float res = (float)y;
+    if (abstop >= 0x42bu) {
+        res = x < -0x1.9fe368p6f ? 0.0f : res;
+        res = x > 0x1.62e42ep6f ? __uint_as_float(0x7f800000u) : res;
+        res = abstop >= 0x7f8u ? x + x : res;
+        res = bits == 0xff800000u ? 0.0f : res;
+    }
+    return res;
+}
+
 }  // namespace mphip

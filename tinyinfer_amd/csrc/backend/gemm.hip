@@ -24,6 +24,7 @@
 // 16 floats per register) and handed to all 64 lanes by a DPP row broadcast
 // folded into v_mul_f32, while x streams from global memory through a
 // register ring.
+#include "dpp.h"
 #include "exact_math.h"
 #include "kernels.h"
 #include "layout.h"
@@ -348,17 +349,8 @@ hipError_t launch_shape(hipStream_t s, const GemmArgs& a) {
 // ---------------------------------------------------------------------------
 // Decode projections: one output column per wavefront.
 
-typedef float f4v __attribute__((ext_vector_type(4)));
-
 constexpr int kColRing = 8;    // x quads in flight per wavefront
 constexpr int kColBlocks = 8;  // 64-k weight blocks held per wavefront
-
-// w * x with w taken from lane I of this lane's 16-lane row (DPP
-// row_newbcast, which the compiler folds into the multiply).
-template <int I>
-__device__ __forceinline__ float mul_bcast(float w, float x) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(w), 0x150 + I, 0xf, 0xf, false)) * x;
-}
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
