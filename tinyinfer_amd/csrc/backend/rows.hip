@@ -34,10 +34,13 @@ __global__ __launch_bounds__(256) void embed_kernel(const float* __restrict__ em
 // sum = sequential float sum of squares (llama_runner.cpp:10-16).
 // A work-group of kRmsWaves wavefronts per (64-row tile, column slice),
 // lane = row. The row tile is taken kRmsWaves*kRmsPer quads (4 columns) at
-// a time, all loads in flight together: wavefront 0 sums its own first
-// kRmsPer quads straight from registers while the other wavefronts land
-// theirs in LDS, then continues over the LDS copy. Every work-group of a
-// tile computes the same scales and writes only its slice of columns.
+// a time, all loads in flight together. Wavefront 0 sums its own quads
+// (squares formed between the adds) while wavefronts 1.. write the squares
+// of theirs to LDS; wavefront 0 then continues with adds only over the LDS
+// squares (the next 8 quads read while 8 are added). Every work-group of a
+// tile computes the same scales and writes only its slice of columns: from
+// the wavefronts' registers when the row fits one pass
+// (width <= 4*kRmsWaves*kRmsPer), else from global memory.
 constexpr int kRmsWaves = 4;
 constexpr int kRmsPer = 36;    // quads per wavefront per pass (144 VGPRs)
 constexpr int kRmsSlices = 8;  // work-groups per row tile
@@ -47,50 +50,94 @@ __global__ __launch_bounds__(kRmsWaves * 64) void rms_kernel(const float* __rest
                                                              const float* __restrict__ weight,
                                                              float* __restrict__ out, int rows, int width,
                                                              float eps) {
-    __shared__ float4 tile_s[(kRmsWaves - 1) * kRmsPer * 64];
+    __shared__ float4 sq_s[(kRmsWaves - 1) * kRmsPer * 64];
+    __shared__ float4 w_s[kRmsWaves * kRmsPer];
     __shared__ float scale_s[64];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int tile = blockIdx.x, slice = blockIdx.y;
     const int quads = width >> 2;
+    const bool one_pass = quads <= kRmsWaves * kRmsPer;
     const int row = tile * 64 + lane;
     const int src = row < rows ? (row_map ? row_map[row] : row) : -1;
     const int src_c = src < 0 ? 0 : src;
     // Quad q of this lane's source row.
     const float4* xrow = reinterpret_cast<const float4*>(x) + (size_t)(src_c >> 6) * quads * 64 + (src_c & 63);
+    const float4* w4 = reinterpret_cast<const float4*>(weight);
+    if (one_pass && tid < quads) w_s[tid] = w4[tid];
+    // Wavefront 0's chain; the squares of the next quad are formed between
+    // the four dependent adds of the pending one. pp starts as four zero
+    // squares, whose adds leave sum at +0.0f as the reference starts it.
     float sum = 0.0f;
-    auto add4 = [&](const float4& v) {
-        sum = sum + v.x * v.x;
-        sum = sum + v.y * v.y;
-        sum = sum + v.z * v.z;
-        sum = sum + v.w * v.w;
+    float pp[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    auto step = [&](const float4& n) {
+        sum = sum + pp[0];
+        pp[0] = n.x * n.x;
+        __builtin_amdgcn_sched_barrier(0);
+        sum = sum + pp[1];
+        pp[1] = n.y * n.y;
+        __builtin_amdgcn_sched_barrier(0);
+        sum = sum + pp[2];
+        pp[2] = n.z * n.z;
+        __builtin_amdgcn_sched_barrier(0);
+        sum = sum + pp[3];
+        pp[3] = n.w * n.w;
+        __builtin_amdgcn_sched_barrier(0);
     };
+    auto add_sq = [&](const float4& q) {
+        sum = sum + q.x;
+        sum = sum + q.y;
+        sum = sum + q.z;
+        sum = sum + q.w;
+    };
+    float4 v[kRmsPer];
+    int q0 = 0;
     for (int p0 = 0; p0 < quads; p0 += kRmsWaves * kRmsPer) {
-        const int q0 = p0 + wave * kRmsPer;  // this wavefront's quads
-        float4 v[kRmsPer];
+        q0 = p0 + wave * kRmsPer;  // this wavefront's quads
 #pragma unroll
         for (int i = 0; i < kRmsPer; ++i) v[i] = xrow[(size_t)min(q0 + i, quads - 1) * 64];
         if (wave == 0) {
 #pragma unroll
             for (int i = 0; i < kRmsPer; ++i)
-                if (q0 + i < quads) add4(v[i]);
+                if (q0 + i < quads) step(v[i]);
+            sum = sum + pp[0];
+            sum = sum + pp[1];
+            sum = sum + pp[2];
+            sum = sum + pp[3];
+            pp[0] = pp[1] = pp[2] = pp[3] = 0.0f;
         } else {
 #pragma unroll
-            for (int i = 0; i < kRmsPer; ++i) tile_s[((wave - 1) * kRmsPer + i) * 64 + lane] = v[i];
+            for (int i = 0; i < kRmsPer; ++i)
+                sq_s[((wave - 1) * kRmsPer + i) * 64 + lane] =
+                    make_float4(v[i].x * v[i].x, v[i].y * v[i].y, v[i].z * v[i].z, v[i].w * v[i].w);
         }
         __syncthreads();
         if (wave == 0) {
             const int n = min(quads - (p0 + kRmsPer), (kRmsWaves - 1) * kRmsPer);
-            const float4* t4 = tile_s + lane;
+            const float4* t4 = sq_s + lane;
+            auto read8 = [&](int q, float4 (&u)[8]) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) u[j] = t4[min(q + j, n - 1) * 64];
+            };
             int q = 0;
-            for (; q + 8 <= n; q += 8) {
-                float4 u[8];
+            if (n >= 8) {
+                float4 u0[8], u1[8];
+                read8(0, u0);
+                for (; q + 16 <= n; q += 16) {
+                    read8(q + 8, u1);
 #pragma unroll
-                for (int j = 0; j < 8; ++j) u[j] = t4[(q + j) * 64];
+                    for (int j = 0; j < 8; ++j) add_sq(u0[j]);
+                    read8(q + 16, u0);
 #pragma unroll
-                for (int j = 0; j < 8; ++j) add4(u[j]);
+                    for (int j = 0; j < 8; ++j) add_sq(u1[j]);
+                }
+                if (q + 8 <= n) {
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) add_sq(u0[j]);
+                    q += 8;
+                }
             }
-            for (; q < n; ++q) add4(t4[q * 64]);
+            for (; q < n; ++q) add_sq(t4[q * 64]);
         }
         __syncthreads();
     }
@@ -98,14 +145,22 @@ __global__ __launch_bounds__(kRmsWaves * 64) void rms_kernel(const float* __rest
     __syncthreads();
     if (src < 0) return;
     const float scale = scale_s[lane];
-    const float4* w4 = reinterpret_cast<const float4*>(weight);
     float4* o4 = reinterpret_cast<float4*>(out) + (size_t)tile * quads * 64 + lane;
     const int per = (quads + kRmsSlices - 1) / kRmsSlices;
-    const int qe = min(quads, (slice + 1) * per);
-    for (int q = slice * per + wave; q < qe; q += kRmsWaves) {
-        const float4 v = xrow[(size_t)q * 64];
-        const float4 w = w4[q];
-        o4[(size_t)q * 64] = make_float4(v.x * scale * w.x, v.y * scale * w.y, v.z * scale * w.z, v.w * scale * w.w);
+    const int qs = slice * per, qe = min(quads, qs + per);
+    auto emit = [&](int q, const float4& v_, const float4& w) {
+        o4[(size_t)q * 64] =
+            make_float4(v_.x * scale * w.x, v_.y * scale * w.y, v_.z * scale * w.z, v_.w * scale * w.w);
+    };
+    if (one_pass) {
+        // The slice's quads that this wavefront holds (q0 = wave*kRmsPer).
+#pragma unroll
+        for (int i = 0; i < kRmsPer; ++i) {
+            const int q = q0 + i;
+            if (q >= qs && q < qe) emit(q, v[i], w_s[q]);
+        }
+    } else {
+        for (int q = qs + wave; q < qe; q += kRmsWaves) emit(q, xrow[(size_t)q * 64], w4[q]);
     }
 }
 
