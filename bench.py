@@ -15,8 +15,10 @@ returns argmax results to the host), so host time over the steps is the
 whole job's time.
 
 roofline: the dominant kernel is paged attention (score, softmax and value
-kernels of one layer = one launch), timed live with HIP events on the
-runner's stream over the timed steps. Algorithmic bytes per launch =
+kernels of one layer = one launch), timed live with HIP events over the
+timed steps: one layer per step (rotating through the layers), the events
+carried by the kernel dispatches on the runner's stream, so the timing adds
+nothing between kernels. Algorithmic bytes per launch =
 sum over sequences of T*kv_width*4*2 (K and V of every attended token, read
 once) + rows*hidden*4*2 (q in, context out). `traffic` is this run's
 algorithmic bytes times the measured/algorithmic ratio recorded in
@@ -70,7 +72,7 @@ def log(msg: str):
 def gpu_leg(args):
     import torch
 
-    from tinyinfer_amd.backend import TIME_ATTENTION, TIME_HEAD, TIME_PROJECTION, kernel_times, set_timing
+    from tinyinfer_amd.backend import TIME_ATTENTION, TIME_HEAD, TIME_PROJECTION, TIME_SAMPLED, kernel_times, set_timing
     from tinyinfer_amd.host import Engine, Runner, Weights
 
     if not torch.cuda.is_available():
@@ -117,7 +119,10 @@ def gpu_leg(args):
         s = step()
         assert s["decode_tokens"] == BATCH and s["prefill_tokens"] == 0, s
     used = {rid: engine.runner.sequence(rid)[1] for rid in ids}
-    set_timing(device, TIME_ATTENTION | (TIME_PROJECTION | TIME_HEAD if args.all_kernels else 0))
+    # Attention is timed on one layer per step (rotating through the layers,
+    # events carried by the kernel dispatches) so that timing costs the
+    # measured throughput nothing; --all-kernels times every launch.
+    set_timing(device, TIME_ATTENTION | (TIME_PROJECTION | TIME_HEAD if args.all_kernels else TIME_SAMPLED))
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
@@ -132,8 +137,9 @@ def gpu_leg(args):
     sum_t = sum(K * u + K * (K + 1) // 2 for u in used.values())  # attended tokens over the timed steps
     kv_width = cfg["kv_heads"] * (cfg["hidden"] // cfg["heads"])
     launches = times["attention_launches"]
-    assert launches == K * cfg["layers"], times
-    att_bytes = cfg["layers"] * (sum_t * kv_width * 4 * 2) + launches * BATCH * cfg["hidden"] * 4 * 2
+    timed_layers = cfg["layers"] if args.all_kernels else 1  # per step
+    assert launches == K * timed_layers, times
+    att_bytes = timed_layers * (sum_t * kv_width * 4 * 2) + launches * BATCH * cfg["hidden"] * 4 * 2
     att_s = times["attention_ns"] * 1e-9
     achieved = att_bytes / att_s / 1e9
     mean_context = sum_t / (K * BATCH)

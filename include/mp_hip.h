@@ -153,8 +153,11 @@ void* mp_hip_stream(const mp_hip* h);
  * the mask resets the totals. One ATTENTION launch is one layer's attention
  * (score, softmax and value kernels); one PROJECTION launch is one GEMM
  * (QKV, O, gate/up or down); one HEAD launch is final norm, LM head and
- * argmax of a call. */
-enum { MP_TIME_ATTENTION = 1, MP_TIME_PROJECTION = 2, MP_TIME_HEAD = 4 };
+ * argmax of a call. Attention events ride on the kernel dispatches; the
+ * others are stream markers between kernels. With MP_TIME_SAMPLED only one
+ * layer per forward call is timed (layer = call count modulo layers), which
+ * keeps the instrumentation's own cost out of a throughput measurement. */
+enum { MP_TIME_ATTENTION = 1, MP_TIME_PROJECTION = 2, MP_TIME_HEAD = 4, MP_TIME_SAMPLED = 8 };
 typedef struct mp_hip_timing_totals {
     uint64_t attention_ns, attention_launches;
     uint64_t projection_ns, projection_launches;

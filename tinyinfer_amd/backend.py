@@ -41,7 +41,7 @@ class KernelTimes(ctypes.Structure):
         "attention_ns", "attention_launches", "projection_ns", "projection_launches", "head_ns", "head_launches")]
 
 
-TIME_ATTENTION, TIME_PROJECTION, TIME_HEAD = 1, 2, 4
+TIME_ATTENTION, TIME_PROJECTION, TIME_HEAD, TIME_SAMPLED = 1, 2, 4, 8
 
 
 class BackendError(RuntimeError):

@@ -18,6 +18,8 @@
 //           output chains, lane = d.
 // Blocks arrive sorted by decreasing length so the longest chains start
 // first.
+#include <hip/hip_ext.h>
+
 #include <type_traits>
 
 #include "dpp.h"
@@ -702,16 +704,28 @@ __global__ __launch_bounds__(kFusedThreads) void attn_decode_kernel(int heads, R
     out[quad_index(row, (kvh * G + wave) * 64 + lane, ldo)] = acc;
 }
 
+// A launch that records `start` as the kernel begins and `stop` as it ends
+// (events carried by the dispatch itself, so timing adds no packets to the
+// stream), or a plain launch when both are null.
+template <typename... P, typename... A>
+void launch_timed(void (*kernel)(P...), dim3 grid, dim3 block, hipStream_t s, hipEvent_t start, hipEvent_t stop,
+                  A... args) {
+    if (start || stop)
+        hipExtLaunchKernelGGL(kernel, grid, block, 0, s, start, stop, 0, args...);
+    else
+        kernel<<<grid, block, 0, s>>>(args...);
+}
+
 hipError_t launch_fused_decode(hipStream_t s, const float* qkv, int ldq, int heads, int kv_heads,
                                const RowMeta& meta, const PagedKv& kv, int layer, float* out, int ldo,
-                               const AttentionWork& w) {
-    attn_scores_kernel<16, 64><<<dim3(w.items_count, kv_heads), kScoreChunk, 0, s>>>(qkv, ldq, heads, kv_heads, 64,
-                                                                                    meta, kv, layer, w);
+                               const AttentionWork& w, const LaunchEvents& ev) {
+    launch_timed(attn_scores_kernel<16, 64>, dim3(w.items_count, kv_heads), dim3(kScoreChunk), s, ev.start, nullptr,
+                 qkv, ldq, heads, kv_heads, 64, meta, kv, layer, w);
     const dim3 grid(w.blocks_count, kv_heads);
     switch (heads / kv_heads) {
-    case 1: attn_decode_kernel<1><<<grid, kFusedThreads, 0, s>>>(heads, meta, kv, layer, w, out, ldo); break;
-    case 2: attn_decode_kernel<2><<<grid, kFusedThreads, 0, s>>>(heads, meta, kv, layer, w, out, ldo); break;
-    case 3: attn_decode_kernel<3><<<grid, kFusedThreads, 0, s>>>(heads, meta, kv, layer, w, out, ldo); break;
+    case 1: launch_timed(attn_decode_kernel<1>, grid, dim3(kFusedThreads), s, nullptr, ev.stop, heads, meta, kv, layer, w, out, ldo); break;
+    case 2: launch_timed(attn_decode_kernel<2>, grid, dim3(kFusedThreads), s, nullptr, ev.stop, heads, meta, kv, layer, w, out, ldo); break;
+    case 3: launch_timed(attn_decode_kernel<3>, grid, dim3(kFusedThreads), s, nullptr, ev.stop, heads, meta, kv, layer, w, out, ldo); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -720,23 +734,24 @@ hipError_t launch_fused_decode(hipStream_t s, const float* qkv, int ldq, int hea
 template <int BT, int DIM>
 hipError_t launch_pair(hipStream_t s, const float* qkv, int ldq, int heads, int kv_heads, int dim,
                        const RowMeta& meta, const PagedKv& kv, int layer, float* out, int ldo,
-                       const AttentionWork& w, bool decode) {
-    attn_scores_kernel<BT, DIM><<<dim3(w.items_count, kv_heads), kScoreChunk, 0, s>>>(qkv, ldq, heads, kv_heads, dim,
-                                                                                      meta, kv, layer, w);
+                       const AttentionWork& w, bool decode, const LaunchEvents& ev) {
+    launch_timed(attn_scores_kernel<BT, DIM>, dim3(w.items_count, kv_heads), dim3(kScoreChunk), s, ev.start, nullptr,
+                 qkv, ldq, heads, kv_heads, dim, meta, kv, layer, w);
     const int group = heads / kv_heads;
     const int block_rows = attention_row_block(heads, kv_heads, dim);
+    const dim3 wg(64);
     if (decode) {
-        attn_pv_kernel<BT, DIM, 1><<<dim3(w.blocks_count, kv_heads, group), 64, 0, s>>>(heads, kv_heads, dim, meta,
-                                                                                       kv, layer, w, out, ldo);
+        launch_timed(attn_pv_kernel<BT, DIM, 1>, dim3(w.blocks_count, kv_heads, group), wg, s, nullptr, ev.stop, heads,
+                     kv_heads, dim, meta, kv, layer, w, out, ldo);
     } else {
         const dim3 grid(w.blocks_count, kv_heads, block_rows);
         switch (group) {
-        case 2: attn_pv_kernel<BT, DIM, 2><<<grid, 64, 0, s>>>(heads, kv_heads, dim, meta, kv, layer, w, out, ldo); break;
-        case 3: attn_pv_kernel<BT, DIM, 3><<<grid, 64, 0, s>>>(heads, kv_heads, dim, meta, kv, layer, w, out, ldo); break;
-        case 4: attn_pv_kernel<BT, DIM, 4><<<grid, 64, 0, s>>>(heads, kv_heads, dim, meta, kv, layer, w, out, ldo); break;
+        case 2: launch_timed(attn_pv_kernel<BT, DIM, 2>, grid, wg, s, nullptr, ev.stop, heads, kv_heads, dim, meta, kv, layer, w, out, ldo); break;
+        case 3: launch_timed(attn_pv_kernel<BT, DIM, 3>, grid, wg, s, nullptr, ev.stop, heads, kv_heads, dim, meta, kv, layer, w, out, ldo); break;
+        case 4: launch_timed(attn_pv_kernel<BT, DIM, 4>, grid, wg, s, nullptr, ev.stop, heads, kv_heads, dim, meta, kv, layer, w, out, ldo); break;
         default:
-            attn_pv_kernel<BT, DIM, 1><<<dim3(w.blocks_count, kv_heads, block_rows * group), 64, 0, s>>>(
-                heads, kv_heads, dim, meta, kv, layer, w, out, ldo);
+            launch_timed(attn_pv_kernel<BT, DIM, 1>, dim3(w.blocks_count, kv_heads, block_rows * group), wg, s, nullptr,
+                         ev.stop, heads, kv_heads, dim, meta, kv, layer, w, out, ldo);
             break;
         }
     }
@@ -754,7 +769,7 @@ int attention_row_block(int heads, int kv_heads, int dim) {
 
 hipError_t launch_attention(hipStream_t s, const float* qkv, int ldq, int rows, int heads, int kv_heads, int dim,
                             const RowMeta& meta, const PagedKv& kv, int layer, float* out, int ldo,
-                            const AttentionWork& w, bool decode) {
+                            const AttentionWork& w, bool decode, const LaunchEvents& ev) {
     if (rows <= 0 || w.blocks_count <= 0) return hipSuccess;
     const int group = heads / kv_heads;
     if (group > kMaxRowHeads || dim % 4 || dim > kMaxDim || kv.block_tokens % 4 ||
@@ -764,10 +779,10 @@ hipError_t launch_attention(hipStream_t s, const float* qkv, int ldq, int rows, 
     // KV head and contexts up to kFusedMaxT (stride = longest context
     // rounded up to 16): one fused kernel.
     if (decode && kv.block_tokens == 16 && dim == 64 && group <= 3 && w.stride <= kFusedMaxT)
-        return launch_fused_decode(s, qkv, ldq, heads, kv_heads, meta, kv, layer, out, ldo, w);
+        return launch_fused_decode(s, qkv, ldq, heads, kv_heads, meta, kv, layer, out, ldo, w, ev);
     if (kv.block_tokens == 16 && dim == 64)
-        return launch_pair<16, 64>(s, qkv, ldq, heads, kv_heads, dim, meta, kv, layer, out, ldo, w, decode);
-    return launch_pair<0, 0>(s, qkv, ldq, heads, kv_heads, dim, meta, kv, layer, out, ldo, w, decode);
+        return launch_pair<16, 64>(s, qkv, ldq, heads, kv_heads, dim, meta, kv, layer, out, ldo, w, decode, ev);
+    return launch_pair<0, 0>(s, qkv, ldq, heads, kv_heads, dim, meta, kv, layer, out, ldo, w, decode, ev);
 }
 
 }  // namespace mphip

@@ -642,10 +642,18 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
     work.chunk_max = h->scratch + (size_t)R * c.heads * work.stride;
     hipStream_t s = h->stream;
     // Launches of an enabled timing class are bracketed by a pair of events
-    // from the pool that mp_hip_set_timing sized for one forward call.
+    // from the pool that mp_hip_set_timing sized for one forward call:
+    // recorded by the kernel dispatches themselves for attention, as stream
+    // markers around the launch otherwise.
     h->spans.clear();
+    const bool sampled = (h->timing & MP_TIME_SAMPLED) != 0;
+    const int sample_layer = (int)(h->stats.forward_calls % (uint64_t)c.layers);
+    int layer_now = -1;  // the layer being launched, -1 outside the layers
+    auto timing_on = [&](uint32_t cls) {
+        return (h->timing & cls) && (!sampled || layer_now == sample_layer);
+    };
     auto timed = [&](uint32_t cls, auto&& launch) -> hipError_t {
-        if (!(h->timing & cls)) return launch();
+        if (!timing_on(cls)) return launch();
         const size_t pair = 2 * h->spans.size();
         hipError_t r = hipEventRecord(h->events[pair], s);
         if (r == hipSuccess) r = launch();
@@ -653,7 +661,17 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
         h->spans.push_back(cls);
         return r;
     };
-    const uint32_t P = MP_TIME_PROJECTION, A = MP_TIME_ATTENTION;
+    auto attention_events = [&]() {
+        mphip::LaunchEvents ev;
+        if (timing_on(MP_TIME_ATTENTION)) {
+            const size_t pair = 2 * h->spans.size();
+            ev.start = h->events[pair];
+            ev.stop = h->events[pair + 1];
+            h->spans.push_back(MP_TIME_ATTENTION);
+        }
+        return ev;
+    };
+    const uint32_t P = MP_TIME_PROJECTION;
     auto gemm = [&](mphip::Epilogue epi, const float* x, int rows, int inner, const float* w, const float* w2,
                     int columns, float* out) {
         mphip::GemmArgs a{};
@@ -670,15 +688,17 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
     const float eps = c.rms_epsilon;
     hipError_t e = mphip::launch_embed(s, h->embedding, meta.tokens, h->x, R, hd);
     for (int l = 0; l < c.layers && e == hipSuccess; ++l) {
+        layer_now = l;
         e = mphip::launch_rms(s, h->x, nullptr, h->input_norm[l], h->xn, R, hd, eps);
         if (e == hipSuccess) e = timed(P, [&] { return gemm(mphip::kStore, h->xn, R, hd, h->qkv[l], nullptr, qw, h->qkv_out); });
         if (e == hipSuccess) e = mphip::launch_rope_append(s, h->qkv_out, qw, R, c.heads, c.kv_heads, dim, h->cos_table, h->sin_table, meta, kv, l);
-        if (e == hipSuccess) e = timed(A, [&] { return mphip::launch_attention(s, h->qkv_out, qw, R, c.heads, c.kv_heads, dim, meta, kv, l, h->ctx, hd, work, decode); });
+        if (e == hipSuccess) e = mphip::launch_attention(s, h->qkv_out, qw, R, c.heads, c.kv_heads, dim, meta, kv, l, h->ctx, hd, work, decode, attention_events());
         if (e == hipSuccess) e = timed(P, [&] { return gemm(mphip::kResidual, h->ctx, R, hd, h->o[l], nullptr, hd, h->x); });
         if (e == hipSuccess) e = mphip::launch_rms(s, h->x, nullptr, h->post_norm[l], h->xn, R, hd, eps);
         if (e == hipSuccess) e = timed(P, [&] { return gemm(mphip::kSwiglu, h->xn, R, hd, h->gate[l], h->up[l], in, h->ffn); });
         if (e == hipSuccess) e = timed(P, [&] { return gemm(mphip::kResidual, h->ffn, R, in, h->down[l], nullptr, hd, h->x); });
     }
+    layer_now = sampled ? -2 : -1;  // a sampled call times no head
     if (e == hipSuccess) e = timed(MP_TIME_HEAD, [&] {
         // Final norm of each sequence's last row, then the LM head with the
         // greedy argmax folded into its epilogue (logits are written only
@@ -780,7 +800,7 @@ int mp_hip_kv_pools(const mp_hip* h, float** keys, float** values, size_t* eleme
 void* mp_hip_stream(const mp_hip* h) { return h ? (void*)h->stream : nullptr; }
 
 int mp_hip_set_timing(mp_hip* h, uint32_t classes) {
-    if (!h || (classes & ~7u)) return fail(h, MP_INVALID_ARGUMENT, "invalid timing classes");
+    if (!h || (classes & ~15u)) return fail(h, MP_INVALID_ARGUMENT, "invalid timing classes");
     int status = mp_hip_sync(h);
     if (status) return status;
     // One pair per GEMM and attention of every layer plus the head.

@@ -89,9 +89,16 @@ struct AttentionWork {
     int stride, chunks;
 };
 int attention_row_block(int heads, int kv_heads, int dim);
+// Optional timing: `start` is recorded as the first kernel of a launch
+// begins and `stop` as its last kernel ends (events carried by the kernel
+// dispatches, adding nothing to the stream between kernels).
+struct LaunchEvents {
+    hipEvent_t start = nullptr;
+    hipEvent_t stop = nullptr;
+};
 hipError_t launch_attention(hipStream_t s, const float* qkv, int ldq, int rows, int heads, int kv_heads, int dim,
                             const RowMeta& meta, const PagedKv& kv, int layer, float* out, int ldo,
-                            const AttentionWork& work, bool decode);
+                            const AttentionWork& work, bool decode, const LaunchEvents& events = LaunchEvents());
 // Stand-alone single-row variant over a caller page table (plain layouts).
 hipError_t launch_attention_single(hipStream_t s, const float* q, const float* keys, const float* values,
                                    const int32_t* table, int length, int layer, int layers, int block_tokens,
