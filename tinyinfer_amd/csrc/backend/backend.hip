@@ -80,6 +80,7 @@ struct mp_hip {
     int32_t* host_results = nullptr;
     size_t host_results_capacity = 0;
     hipEvent_t staged = nullptr;
+    hipEvent_t done = nullptr;  // end of a forward call's queued work
     std::vector<void*> allocations;
     // kernel timing (mp_hip_set_timing): event pairs of one forward call
     uint32_t timing = 0;
@@ -103,6 +104,19 @@ int check(mp_hip* h, hipError_t e, const char* what) {
 
 // Waits for the context's stream (internal: buffers about to be replaced).
 int stream_sync(mp_hip* h) { return check(h, hipStreamSynchronize(h->stream), "model completion"); }
+
+// Waits for the work queued on the stream so far by polling an event: the
+// forward's result download is what the next step waits on, and a polling
+// wait returns as soon as it lands, where a blocking wait adds the wake-up.
+int stream_wait_polling(mp_hip* h, const char* what) {
+    hipError_t e = hipEventRecord(h->done, h->stream);
+    while (e == hipSuccess) {
+        e = hipEventQuery(h->done);
+        if (e == hipErrorNotReady) e = hipSuccess;
+        else break;
+    }
+    return check(h, e, what);
+}
 
 int device_alloc(mp_hip* h, void** out, size_t bytes, const char* what) {
     void* p = nullptr;
@@ -338,6 +352,7 @@ int mp_hip_create(const mp_model_desc* model, const mp_kv_desc* kv, mp_hip** out
     int status = check(h, hipGetDevice(&h->device), "get device");
     if (!status) status = check(h, hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking), "create model stream");
     if (!status) status = check(h, hipEventCreateWithFlags(&h->staged, hipEventDisableTiming), "create upload event");
+    if (!status) status = check(h, hipEventCreateWithFlags(&h->done, hipEventDisableTiming), "create completion event");
     const size_t hd = c.hidden;
     h->input_norm.assign(c.layers, nullptr);
     h->post_norm.assign(c.layers, nullptr);
@@ -401,6 +416,7 @@ int mp_hip_destroy(mp_hip* h) {
     if (h->stream) (void)hipStreamSynchronize(h->stream);
     for (hipEvent_t ev : h->events) (void)hipEventDestroy(ev);
     if (h->staged) (void)hipEventDestroy(h->staged);
+    if (h->done) (void)hipEventDestroy(h->done);
     if (h->host_meta) (void)hipHostFree(h->host_meta);
     if (h->host_results) (void)hipHostFree(h->host_results);
     for (void* p : h->allocations)
@@ -729,7 +745,7 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
         status = check(h, hipMemcpyAsync(logits, h->logits, sizeof(float) * (size_t)nseq * c.vocabulary, hipMemcpyDeviceToHost, s), "download logits");
         if (!status) h->stats.logits_downloaded_bytes += sizeof(float) * (size_t)nseq * c.vocabulary;
     }
-    if (!status) status = check(h, hipStreamSynchronize(s), "model completion");
+    if (!status) status = stream_wait_polling(h, "model completion");
     if (status) return status;
     for (size_t i = 0; i < h->spans.size(); ++i) {
         float ms = 0.0f;

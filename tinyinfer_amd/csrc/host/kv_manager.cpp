@@ -4,6 +4,8 @@
 // tail for a fresh page to copy into, and only commits tokens on success.
 #include "miniprefix/kv_manager.h"
 
+#include <algorithm>
+
 namespace miniprefix {
 
 KVManager::KVManager(KvCacheConfig config, int layers, int width, int context, int vocabulary)
@@ -150,7 +152,10 @@ KVManager::Append::Append(KVManager& owner, const RequestId& id, const std::vect
     if (tokens.empty() || tokens.size() > static_cast<std::size_t>(owner.context_ - sequence.used))
         throw std::invalid_argument("context overflow/empty input");
     owner.validate_tokens(tokens);
-    sequence.tokens.reserve(static_cast<std::size_t>(sequence.used) + tokens.size());
+    // Room for commit() to append without throwing, grown geometrically so
+    // that a decode step does not copy the whole history.
+    const std::size_t need = static_cast<std::size_t>(sequence.used) + tokens.size();
+    if (need > sequence.tokens.capacity()) sequence.tokens.reserve(std::max(need, 2 * sequence.tokens.capacity()));
     const int valid = sequence.used % owner.config().block_tokens;
     bool cow = valid && owner.pool_.references(sequence.blocks.back()) > 1;
     owner.reserve_pages(id, sequence, sequence.used + static_cast<int>(tokens.size()), cow);
