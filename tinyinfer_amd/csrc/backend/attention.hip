@@ -50,10 +50,16 @@ __device__ __forceinline__ float wave_max(float v) {
 }
 
 // BT/DIM: compile-time page size and head dim (0: runtime).
-template <int BT, int DIM>
+// ROPE (decode blocks of one row, 16-token pages, head dim 64): q is
+// rotated while it is staged in LDS, and the block holding the row's new
+// token rotates that token's k, writes it and the v row to the pools and
+// uses the rotated k for the token's own score (the arithmetic of
+// rope_append_kernel; no other block reads that token).
+template <int BT, int DIM, bool ROPE = false>
 __global__ __launch_bounds__(kScoreChunk) void attn_scores_kernel(const float* __restrict__ qkv, int ldq, int heads,
                                                                   int kv_heads, int dim_rt, RowMeta meta, PagedKv kv,
-                                                                  int layer, AttentionWork w) {
+                                                                  int layer, AttentionWork w, RopeTables rope) {
+    static_assert(!ROPE || (BT == 16 && DIM == 64), "fused RoPE shape");
     __shared__ float partial[kScoreChunk / 64][kMaxRowHeads];
     __shared__ float4 q_s[kMaxRowHeads * kMaxDim / 4];
     const int dim = DIM ? DIM : dim_rt;
@@ -75,17 +81,58 @@ __global__ __launch_bounds__(kScoreChunk) void attn_scores_kernel(const float* _
     // The block's q rows (rh x dim) in LDS, all loads in flight together
     // with this token's K row.
     const int dq = dim / 4;
-    for (int e = tid; e < rh * dq; e += kScoreChunk) {
-        const int i = e / dq, c = e - i * dq;
-        const int r = i / group, h = i - r * group;
-        q_s[e] = *reinterpret_cast<const float4*>(qkv + quad_index(r0 + r, (kvh * group + h) * dim + 4 * c, ldq));
+    // (a, b) -> (a*cos - b*sin, b*cos + a*sin); inputs by value, so lo and hi
+    // may be the inputs' own registers.
+    auto rotate = [](const float4 a, const float4 b, const float4 cs, const float4 sn, float4& lo, float4& hi) {
+        lo = make_float4(a.x * cs.x - b.x * sn.x, a.y * cs.y - b.y * sn.y, a.z * cs.z - b.z * sn.z,
+                         a.w * cs.w - b.w * sn.w);
+        hi = make_float4(b.x * cs.x + a.x * sn.x, b.y * cs.y + a.y * sn.y, b.z * cs.z + a.z * sn.z,
+                         b.w * cs.w + a.w * sn.w);
+    };
+    const float4* cs4 = ROPE ? reinterpret_cast<const float4*>(rope.cos + (size_t)pos0 * (DIM / 2)) : nullptr;
+    const float4* sn4 = ROPE ? reinterpret_cast<const float4*>(rope.sin + (size_t)pos0 * (DIM / 2)) : nullptr;
+    __shared__ float4 rope_s[ROPE ? 2 * (DIM / 8) : 1];  // cos then sin of the row's position
+    const bool new_token = ROPE && t == pos0;
+    const int hidden = heads * (DIM ? DIM : dim);
+    if (ROPE) {
+        // One row (nr = 1): quads c and c + 8 of each head form the rotated pairs.
+        for (int e = tid; e < group * (DIM / 8); e += kScoreChunk) {
+            const int h = e / (DIM / 8), c = e - h * (DIM / 8);
+            const int col = (kvh * group + h) * DIM;
+            const float4 a = *reinterpret_cast<const float4*>(qkv + quad_index(r0, col + 4 * c, ldq));
+            const float4 b = *reinterpret_cast<const float4*>(qkv + quad_index(r0, col + DIM / 2 + 4 * c, ldq));
+            rotate(a, b, cs4[c], sn4[c], q_s[h * (DIM / 4) + c], q_s[h * (DIM / 4) + c + DIM / 8]);
+        }
+        if (tid < 2 * (DIM / 8)) rope_s[tid] = tid < DIM / 8 ? cs4[tid] : sn4[tid - DIM / 8];
+    } else {
+        for (int e = tid; e < rh * dq; e += kScoreChunk) {
+            const int i = e / dq, c = e - i * dq;
+            const int r = i / group, h = i - r * group;
+            q_s[e] = *reinterpret_cast<const float4*>(qkv + quad_index(r0 + r, (kvh * group + h) * dim + 4 * c, ldq));
+        }
     }
+    // This token's K row; the row's new token takes its unrotated k from the
+    // projection instead (rotated below, then written to the page).
     float4 kreg[DIM ? DIM / 4 : 1];
     if (DIM) {
+        // Consecutive quads of a row are 256 floats apart in the quad layout,
+        // bt*4 apart in a K page.
+        const float* src = new_token ? qkv + quad_index(r0, hidden + kvh * DIM, ldq) : kbase;
+        const int step = new_token ? 256 : BT * 4;
 #pragma unroll
-        for (int c = 0; c < DIM / 4; ++c) kreg[c] = *reinterpret_cast<const float4*>(kbase + (size_t)c * bt * 4);
+        for (int c = 0; c < DIM / 4; ++c) kreg[c] = *reinterpret_cast<const float4*>(src + c * step);
     }
+    // The wavefront holding the new token copies its v row at the end (lane = d).
+    const bool v_wave = ROPE && pos0 >= chunk * kScoreChunk + wave * 64 && pos0 < chunk * kScoreChunk + wave * 64 + 64;
+    float vnew = 0.0f;
+    if (v_wave) vnew = qkv[quad_index(r0, hidden + kv.kv_width + kvh * DIM + lane, ldq)];
     __syncthreads();
+    if (new_token) {
+#pragma unroll
+        for (int c = 0; c < DIM / 8; ++c) rotate(kreg[c], kreg[c + DIM / 8], rope_s[c], rope_s[DIM / 8 + c], kreg[c], kreg[c + DIM / 8]);
+#pragma unroll
+        for (int c = 0; c < DIM / 4; ++c) *reinterpret_cast<float4*>(kv.keys + (kbase - kv.keys) + (size_t)c * BT * 4) = kreg[c];
+    }
     const float root = sqrtf((float)dim);
     for (int i = 0; i < rh; ++i) {
         const int r = i / group, h = i - r * group;
@@ -123,6 +170,10 @@ __global__ __launch_bounds__(kScoreChunk) void attn_scores_kernel(const float* _
         for (int j = 1; j < kScoreChunk / 64; ++j) m = fmaxf(m, partial[j][tid]);
         const int r = tid / group, h = tid - r * group;
         w.chunk_max[((size_t)(r0 + r) * heads + kvh * group + h) * w.chunks + chunk] = m;
+    }
+    if (v_wave) {
+        const size_t base = kv_page_base(table[pos0 / BT], layer, kv.layers, BT, kv.kv_width);
+        kv.values[base + value_offset(pos0 % BT, kvh, lane, BT, DIM)] = vnew;
     }
 }
 
@@ -718,9 +769,9 @@ void launch_timed(void (*kernel)(P...), dim3 grid, dim3 block, hipStream_t s, hi
 
 hipError_t launch_fused_decode(hipStream_t s, const float* qkv, int ldq, int heads, int kv_heads,
                                const RowMeta& meta, const PagedKv& kv, int layer, float* out, int ldo,
-                               const AttentionWork& w, const LaunchEvents& ev) {
-    launch_timed(attn_scores_kernel<16, 64>, dim3(w.items_count, kv_heads), dim3(kScoreChunk), s, ev.start, nullptr,
-                 qkv, ldq, heads, kv_heads, 64, meta, kv, layer, w);
+                               const AttentionWork& w, const RopeTables& rope, const LaunchEvents& ev) {
+    launch_timed(attn_scores_kernel<16, 64, true>, dim3(w.items_count, kv_heads), dim3(kScoreChunk), s, ev.start,
+                 nullptr, qkv, ldq, heads, kv_heads, 64, meta, kv, layer, w, rope);
     const dim3 grid(w.blocks_count, kv_heads);
     switch (heads / kv_heads) {
     case 1: launch_timed(attn_decode_kernel<1>, grid, dim3(kFusedThreads), s, nullptr, ev.stop, heads, meta, kv, layer, w, out, ldo); break;
@@ -736,7 +787,7 @@ hipError_t launch_pair(hipStream_t s, const float* qkv, int ldq, int heads, int 
                        const RowMeta& meta, const PagedKv& kv, int layer, float* out, int ldo,
                        const AttentionWork& w, bool decode, const LaunchEvents& ev) {
     launch_timed(attn_scores_kernel<BT, DIM>, dim3(w.items_count, kv_heads), dim3(kScoreChunk), s, ev.start, nullptr,
-                 qkv, ldq, heads, kv_heads, dim, meta, kv, layer, w);
+                 qkv, ldq, heads, kv_heads, dim, meta, kv, layer, w, RopeTables{nullptr, nullptr});
     const int group = heads / kv_heads;
     const int block_rows = attention_row_block(heads, kv_heads, dim);
     const dim3 wg(64);
@@ -767,9 +818,9 @@ int attention_row_block(int heads, int kv_heads, int dim) {
     return rows < 16 ? rows : 16;
 }
 
-hipError_t launch_attention(hipStream_t s, const float* qkv, int ldq, int rows, int heads, int kv_heads, int dim,
+hipError_t launch_attention(hipStream_t s, float* qkv, int ldq, int rows, int heads, int kv_heads, int dim,
                             const RowMeta& meta, const PagedKv& kv, int layer, float* out, int ldo,
-                            const AttentionWork& w, bool decode, const LaunchEvents& ev) {
+                            const AttentionWork& w, bool decode, const RopeTables& rope, const LaunchEvents& ev) {
     if (rows <= 0 || w.blocks_count <= 0) return hipSuccess;
     const int group = heads / kv_heads;
     if (group > kMaxRowHeads || dim % 4 || dim > kMaxDim || kv.block_tokens % 4 ||
@@ -779,7 +830,9 @@ hipError_t launch_attention(hipStream_t s, const float* qkv, int ldq, int rows, 
     // KV head and contexts up to kFusedMaxT (stride = longest context
     // rounded up to 16): one fused kernel.
     if (decode && kv.block_tokens == 16 && dim == 64 && group <= 3 && w.stride <= kFusedMaxT)
-        return launch_fused_decode(s, qkv, ldq, heads, kv_heads, meta, kv, layer, out, ldo, w, ev);
+        return launch_fused_decode(s, qkv, ldq, heads, kv_heads, meta, kv, layer, out, ldo, w, rope, ev);
+    const hipError_t e = launch_rope_append(s, qkv, ldq, rows, heads, kv_heads, dim, rope.cos, rope.sin, meta, kv, layer);
+    if (e != hipSuccess) return e;
     if (kv.block_tokens == 16 && dim == 64)
         return launch_pair<16, 64>(s, qkv, ldq, heads, kv_heads, dim, meta, kv, layer, out, ldo, w, decode, ev);
     return launch_pair<0, 0>(s, qkv, ldq, heads, kv_heads, dim, meta, kv, layer, out, ldo, w, decode, ev);

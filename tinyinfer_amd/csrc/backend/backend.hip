@@ -707,8 +707,9 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
         layer_now = l;
         e = mphip::launch_rms(s, h->x, nullptr, h->input_norm[l], h->xn, R, hd, eps);
         if (e == hipSuccess) e = timed(P, [&] { return gemm(mphip::kStore, h->xn, R, hd, h->qkv[l], nullptr, qw, h->qkv_out); });
-        if (e == hipSuccess) e = mphip::launch_rope_append(s, h->qkv_out, qw, R, c.heads, c.kv_heads, dim, h->cos_table, h->sin_table, meta, kv, l);
-        if (e == hipSuccess) e = mphip::launch_attention(s, h->qkv_out, qw, R, c.heads, c.kv_heads, dim, meta, kv, l, h->ctx, hd, work, decode, attention_events());
+        if (e == hipSuccess)
+            e = mphip::launch_attention(s, h->qkv_out, qw, R, c.heads, c.kv_heads, dim, meta, kv, l, h->ctx, hd, work,
+                                        decode, mphip::RopeTables{h->cos_table, h->sin_table}, attention_events());
         if (e == hipSuccess) e = timed(P, [&] { return gemm(mphip::kResidual, h->ctx, R, hd, h->o[l], nullptr, hd, h->x); });
         if (e == hipSuccess) e = mphip::launch_rms(s, h->x, nullptr, h->post_norm[l], h->xn, R, hd, eps);
         if (e == hipSuccess) e = timed(P, [&] { return gemm(mphip::kSwiglu, h->xn, R, hd, h->gate[l], h->up[l], in, h->ffn); });

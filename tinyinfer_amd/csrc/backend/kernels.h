@@ -96,9 +96,19 @@ struct LaunchEvents {
     hipEvent_t start = nullptr;
     hipEvent_t stop = nullptr;
 };
-hipError_t launch_attention(hipStream_t s, const float* qkv, int ldq, int rows, int heads, int kv_heads, int dim,
+// RoPE tables [position][dim/2] (cos, sin) of the rows' positions.
+struct RopeTables {
+    const float* cos;
+    const float* sin;
+};
+// Attention of the rows, including RoPE of q and k and the append of the
+// rows' K/V to the pools (rope_append_kernel ahead of the attention kernels,
+// or folded into the scores kernel on the fused decode path). qkv is
+// [rows][heads*dim + 2*kv_width] in quad layout; q may be rotated in place.
+hipError_t launch_attention(hipStream_t s, float* qkv, int ldq, int rows, int heads, int kv_heads, int dim,
                             const RowMeta& meta, const PagedKv& kv, int layer, float* out, int ldo,
-                            const AttentionWork& work, bool decode, const LaunchEvents& events = LaunchEvents());
+                            const AttentionWork& work, bool decode, const RopeTables& rope,
+                            const LaunchEvents& events = LaunchEvents());
 // Stand-alone single-row variant over a caller page table (plain layouts).
 hipError_t launch_attention_single(hipStream_t s, const float* q, const float* keys, const float* values,
                                    const int32_t* table, int length, int layer, int layers, int block_tokens,
