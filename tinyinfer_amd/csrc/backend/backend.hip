@@ -702,17 +702,35 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
     };
     const int hd = c.hidden, in = c.intermediate;
     const float eps = c.rms_epsilon;
+    // RMSNorm of the residual stream h->x followed by a projection: one
+    // launch where the shape allows, else rms_kernel into h->xn and the GEMM.
+    auto normed_gemm = [&](mphip::Epilogue epi, const float* norm, int rows, int inner, const float* w,
+                           const float* w2, int columns, float* out) {
+        mphip::GemmArgs a{};
+        a.x = h->x;
+        a.w = w;
+        a.w2 = w2;
+        a.out = out;
+        a.rows = rows;
+        a.inner = inner;
+        a.columns = columns;
+        a.norm = norm;
+        a.eps = eps;
+        if (mphip::gemm_normed_fits(epi, a)) return mphip::launch_gemm_normed(s, epi, a);
+        hipError_t r = mphip::launch_rms(s, h->x, nullptr, norm, h->xn, rows, inner, eps);
+        if (r == hipSuccess) r = gemm(epi, h->xn, rows, inner, w, w2, columns, out);
+        return r;
+    };
     hipError_t e = mphip::launch_embed(s, h->embedding, meta.tokens, h->x, R, hd);
     for (int l = 0; l < c.layers && e == hipSuccess; ++l) {
         layer_now = l;
-        e = mphip::launch_rms(s, h->x, nullptr, h->input_norm[l], h->xn, R, hd, eps);
-        if (e == hipSuccess) e = timed(P, [&] { return gemm(mphip::kStore, h->xn, R, hd, h->qkv[l], nullptr, qw, h->qkv_out); });
+        e = timed(P, [&] { return normed_gemm(mphip::kStore, h->input_norm[l], R, hd, h->qkv[l], nullptr, qw, h->qkv_out); });
         if (e == hipSuccess)
             e = mphip::launch_attention(s, h->qkv_out, qw, R, c.heads, c.kv_heads, dim, meta, kv, l, h->ctx, hd, work,
                                         decode, mphip::RopeTables{h->cos_table, h->sin_table}, attention_events());
         if (e == hipSuccess) e = timed(P, [&] { return gemm(mphip::kResidual, h->ctx, R, hd, h->o[l], nullptr, hd, h->x); });
-        if (e == hipSuccess) e = mphip::launch_rms(s, h->x, nullptr, h->post_norm[l], h->xn, R, hd, eps);
-        if (e == hipSuccess) e = timed(P, [&] { return gemm(mphip::kSwiglu, h->xn, R, hd, h->gate[l], h->up[l], in, h->ffn); });
+        if (e == hipSuccess)
+            e = timed(P, [&] { return normed_gemm(mphip::kSwiglu, h->post_norm[l], R, hd, h->gate[l], h->up[l], in, h->ffn); });
         if (e == hipSuccess) e = timed(P, [&] { return gemm(mphip::kResidual, h->ffn, R, in, h->down[l], nullptr, hd, h->x); });
     }
     layer_now = sampled ? -2 : -1;  // a sampled call times no head

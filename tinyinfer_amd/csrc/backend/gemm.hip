@@ -372,10 +372,22 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, 
 // order, so a weight block fetched from HBM during the loop stalls every x
 // ring wait behind it, while fetched up front it costs one round trip per
 // launch.
-template <int M, int NW, int EPI, int D = kColBlocks, bool RELOAD = true>
+// With NORM the kernel first forms the RMSNorm of its row tile
+// (llama_runner.cpp:10-16, rows.hip's rms_kernel arithmetic): the raw tile
+// lands in LDS by DMA, wavefront 0 runs the 64 sum-of-squares chains over
+// it, and every wavefront rewrites its share of the tile as (x*scale)*w;
+// the products then read x from LDS. Requires !RELOAD and inner <= 64*D
+// (the tile fits the work-group's LDS).
+constexpr int kNormBlocks = 9;  // inner <= 576 for the folded RMSNorm
+
+template <int M, int NW, int EPI, int D = kColBlocks, bool RELOAD = true, bool NORM = false>
 __global__ __launch_bounds__(NW * 64) void gemm_column_kernel(GemmArgs a) {
     constexpr int RX = kColRing;
     static_assert((D * 16) % RX == 0, "ring slots repeat every D blocks");
+    static_assert(!NORM || (!RELOAD && D == kNormBlocks), "folded RMSNorm holds the whole tile");
+    __shared__ f4v tile_s[NORM ? kNormBlocks * 16 * 64 : 1];  // [quad][row]
+    __shared__ float scale_s[NORM ? 64 : 1];
+    __shared__ float4 norm_s[NORM ? kNormBlocks * 16 : 1];  // RMSNorm weights by quad
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int tile = blockIdx.y;
@@ -389,6 +401,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_column_kernel(GemmArgs a) {
     ws[0] = reinterpret_cast<const f4v*>(a.w) + (size_t)n * kq + (lane & 15);
     ws[1] = reinterpret_cast<const f4v*>(M == 2 ? a.w2 : a.w) + (size_t)n * kq + (lane & 15);
     auto load_x = [&](int q) {
+        if (NORM) return tile_s[min(q, kq - 1) * 64 + lane];
         return __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(xrs, xoff, min(q, kq - 1) * 1024, 0));
     };
 
@@ -401,6 +414,71 @@ __global__ __launch_bounds__(NW * 64) void gemm_column_kernel(GemmArgs a) {
     for (int d = 0; d < D; ++d)
 #pragma unroll
         for (int m = 0; m < M; ++m) wr[d][m] = ws[m][min(d, KB - 1) * 16];
+    if (NORM) {
+        // The raw tile into LDS: quads wave, wave + NW, ... (1 KB per copy).
+        const float4* xg = reinterpret_cast<const float4*>(a.x) + (size_t)tile * kq * 64 + lane;
+        for (int q = wave; q < kq; q += NW)
+            __builtin_amdgcn_global_load_lds((const void*)(xg + (size_t)q * 64), (LdsPtr)(&tile_s[q * 64]), 16, 0, 0);
+        if ((int)threadIdx.x < kq) norm_s[threadIdx.x] = reinterpret_cast<const float4*>(a.norm)[threadIdx.x];
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (wave == 0) {
+            // sum of squares in column order; the squares of the next quad
+            // are formed between the four adds of the pending one (pp starts
+            // as four zero squares: their adds leave sum at +0.0f).
+            float sum = 0.0f;
+            float pp[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            auto step = [&](const f4v& v) {
+                sum = sum + pp[0];
+                pp[0] = v.x * v.x;
+                __builtin_amdgcn_sched_barrier(0);
+                sum = sum + pp[1];
+                pp[1] = v.y * v.y;
+                __builtin_amdgcn_sched_barrier(0);
+                sum = sum + pp[2];
+                pp[2] = v.z * v.z;
+                __builtin_amdgcn_sched_barrier(0);
+                sum = sum + pp[3];
+                pp[3] = v.w * v.w;
+                __builtin_amdgcn_sched_barrier(0);
+            };
+            const f4v* t4 = tile_s + lane;
+            f4v u0[8], u1[8];
+            auto read8 = [&](int q, f4v (&u)[8]) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) u[j] = t4[min(q + j, kq - 1) * 64];
+            };
+            int q = 0;
+            read8(0, u0);
+            for (; q + 16 <= kq; q += 16) {
+                read8(q + 8, u1);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) step(u0[j]);
+                read8(q + 16, u0);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) step(u1[j]);
+            }
+            if (q + 8 <= kq) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) step(u0[j]);
+                q += 8;
+            }
+            for (; q < kq; ++q) step(t4[q * 64]);
+            sum = sum + pp[0];
+            sum = sum + pp[1];
+            sum = sum + pp[2];
+            sum = sum + pp[3];
+            scale_s[lane] = 1.0f / sqrtf(sum / (float)a.inner + a.eps);
+        }
+        __syncthreads();
+        const float scale = scale_s[lane];
+        for (int q = wave; q < kq; q += NW) {
+            const f4v v = tile_s[q * 64 + lane];
+            const float4 g = norm_s[q];
+            tile_s[q * 64 + lane] = f4v{v.x * scale * g.x, v.y * scale * g.y, v.z * scale * g.z, v.w * scale * g.w};
+        }
+        __syncthreads();
+    }
 #pragma unroll
     for (int i = 0; i < RX; ++i) xr[i] = load_x(i);
     float pn[M][4];  // products of the next quad
@@ -474,10 +552,10 @@ __global__ __launch_bounds__(NW * 64) void gemm_column_kernel(GemmArgs a) {
 }
 
 
-template <int M, int NW, int EPI, int D, bool RELOAD>
+template <int M, int NW, int EPI, int D, bool RELOAD, bool NORM = false>
 hipError_t launch_column(hipStream_t s, const GemmArgs& a) {
     const dim3 grid((a.columns + NW - 1) / NW, (a.rows + 63) / 64);
-    gemm_column_kernel<M, NW, EPI, D, RELOAD><<<grid, NW * 64, 0, s>>>(a);
+    gemm_column_kernel<M, NW, EPI, D, RELOAD, NORM><<<grid, NW * 64, 0, s>>>(a);
     return hipGetLastError();
 }
 
@@ -494,6 +572,19 @@ hipError_t launch_column_one(hipStream_t s, const GemmArgs& a) {
 }  // namespace
 
 int head_groups(int columns) { return (columns + kHeadColumns - 1) / kHeadColumns; }
+
+bool gemm_normed_fits(Epilogue epilogue, const GemmArgs& a) {
+    return a.rows > 0 && a.rows <= 64 && a.columns > 0 && a.inner > 0 && a.inner % 64 == 0 &&
+           a.inner <= 64 * kNormBlocks && a.norm && (epilogue == kStore || epilogue == kSwiglu);
+}
+
+hipError_t launch_gemm_normed(hipStream_t s, Epilogue epilogue, const GemmArgs& a) {
+    if (!gemm_normed_fits(epilogue, a)) return hipErrorInvalidValue;
+    // The LDS tile allows one work-group per CU: four wavefronts for one
+    // matrix, eight for gate and up.
+    if (epilogue == kStore) return launch_column<1, 4, kStore, kNormBlocks, false, true>(s, a);
+    return launch_column<2, 8, kSwiglu, kNormBlocks, false, true>(s, a);
+}
 
 hipError_t launch_gemm(hipStream_t s, Epilogue epilogue, const GemmArgs& a) {
     if (a.rows <= 0 || a.columns <= 0) return hipSuccess;

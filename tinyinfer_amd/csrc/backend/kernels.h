@@ -44,6 +44,10 @@ struct GemmArgs {
     const float* w2;
     float* out;
     int rows, inner, columns;
+    // RMSNorm folded into the projection (launch_gemm_normed): x is the raw
+    // residual stream and norm the RMSNorm weights of width `inner`.
+    const float* norm;
+    float eps;
     float* best_value;
     int32_t* best_index;
     int32_t* bad;
@@ -52,6 +56,12 @@ struct GemmArgs {
 constexpr int kHeadColumns = 64;
 int head_groups(int columns);
 hipError_t launch_gemm(hipStream_t s, Epilogue epilogue, const GemmArgs& args);
+// The same projection of RMSNorm(x) (llama_runner.cpp:10-16 then :30-36)
+// in one launch where the shape allows (one row tile, inner <= 576 and a
+// multiple of 64, kStore or kSwiglu); false when it does not, and nothing
+// is launched.
+bool gemm_normed_fits(Epilogue epilogue, const GemmArgs& args);
+hipError_t launch_gemm_normed(hipStream_t s, Epilogue epilogue, const GemmArgs& args);
 // argmax[r] = first index of the row maximum, nonfinite[r] = any non-finite
 // logit, from the kHead partials of `args`.
 hipError_t launch_head_argmax(hipStream_t s, const GemmArgs& args, int32_t* argmax, int32_t* nonfinite);
