@@ -356,6 +356,11 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, 
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
 
+// Quad q of a quad-layout row tile (lane = row) through a buffer resource.
+__device__ __forceinline__ f4v load_x_global(__amdgpu_buffer_rsrc_t rsrc, int lane_bytes, int q) {
+    return __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(rsrc, lane_bytes, q * 1024, 0));
+}
+
 // out[r][n] for the 64 rows r of tile blockIdx.y (lane = row) and column
 // n = blockIdx.x*NW + wave; M = 2 runs the gate (w) and up (w2) chains side
 // by side for the SwiGLU epilogue. k advances in quads (4 k) and 64-k blocks
@@ -373,11 +378,12 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, 
 // ring wait behind it, while fetched up front it costs one round trip per
 // launch.
 // With NORM the kernel first forms the RMSNorm of its row tile
-// (llama_runner.cpp:10-16, rows.hip's rms_kernel arithmetic): the raw tile
-// lands in LDS by DMA, wavefront 0 runs the 64 sum-of-squares chains over
-// it, and every wavefront rewrites its share of the tile as (x*scale)*w;
-// the products then read x from LDS. Requires !RELOAD and inner <= 64*D
-// (the tile fits the work-group's LDS).
+// (llama_runner.cpp:10-16, rows.hip's rms_kernel arithmetic): the
+// wavefronts load the raw tile into registers, wavefront 0 runs the 64
+// sum-of-squares chains (its own quads from registers, the others' squares
+// through LDS), and every wavefront writes its share of the tile as
+// (x*scale)*w into LDS, from where the products read x. Requires !RELOAD and
+// inner <= 64*D (the tile fits the work-group's LDS).
 constexpr int kNormBlocks = 9;  // inner <= 576 for the folded RMSNorm
 
 template <int M, int NW, int EPI, int D = kColBlocks, bool RELOAD = true, bool NORM = false>
@@ -385,7 +391,8 @@ __global__ __launch_bounds__(NW * 64) void gemm_column_kernel(GemmArgs a) {
     constexpr int RX = kColRing;
     static_assert((D * 16) % RX == 0, "ring slots repeat every D blocks");
     static_assert(!NORM || (!RELOAD && D == kNormBlocks), "folded RMSNorm holds the whole tile");
-    __shared__ f4v tile_s[NORM ? kNormBlocks * 16 * 64 : 1];  // [quad][row]
+    // [quad][row]; NW spare quads take the writes of quads past the tile
+    __shared__ f4v tile_s[NORM ? (kNormBlocks * 16 + NW) * 64 : 1];
     __shared__ float scale_s[NORM ? 64 : 1];
     __shared__ float4 norm_s[NORM ? kNormBlocks * 16 : 1];  // RMSNorm weights by quad
     const int lane = threadIdx.x & 63;
@@ -415,67 +422,96 @@ __global__ __launch_bounds__(NW * 64) void gemm_column_kernel(GemmArgs a) {
 #pragma unroll
         for (int m = 0; m < M; ++m) wr[d][m] = ws[m][min(d, KB - 1) * 16];
     if (NORM) {
-        // The raw tile into LDS: quads wave, wave + NW, ... (1 KB per copy).
-        const float4* xg = reinterpret_cast<const float4*>(a.x) + (size_t)tile * kq * 64 + lane;
-        for (int q = wave; q < kq; q += NW)
-            __builtin_amdgcn_global_load_lds((const void*)(xg + (size_t)q * 64), (LdsPtr)(&tile_s[q * 64]), 16, 0, 0);
+        // Wavefront w holds quads [w*S, (w+1)*S) of the raw tile in
+        // registers. Wavefront 0 sums its own quads' squares at once while
+        // the others write their squares into the tile's LDS slots; then
+        // wavefront 0 continues with adds only over those, and every
+        // wavefront writes its quads, normalized, into the same slots.
+        constexpr int kShare = kNormBlocks * 16 / NW;  // quads per wavefront at most
+        static_assert(kNormBlocks * 16 % NW == 0, "tile split");
+        const int S = kq / NW, q0 = wave * S;  // kq is a multiple of 16 and NW divides 16
+        f4v v[kShare];
+#pragma unroll
+        for (int i = 0; i < kShare; ++i) v[i] = load_x_global(xrs, xoff, min(q0 + i, kq - 1));
         if ((int)threadIdx.x < kq) norm_s[threadIdx.x] = reinterpret_cast<const float4*>(a.norm)[threadIdx.x];
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
+        // Sum of squares in column order (llama_runner.cpp:10-16).
+        float sum = 0.0f;
         if (wave == 0) {
-            // sum of squares in column order; the squares of the next quad
-            // are formed between the four adds of the pending one (pp starts
-            // as four zero squares: their adds leave sum at +0.0f).
-            float sum = 0.0f;
+            // The squares of the next quad are formed between the four adds
+            // of the pending one; pp starts as four zero squares, whose adds
+            // leave sum at +0.0f.
             float pp[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-            auto step = [&](const f4v& v) {
-                sum = sum + pp[0];
-                pp[0] = v.x * v.x;
-                __builtin_amdgcn_sched_barrier(0);
-                sum = sum + pp[1];
-                pp[1] = v.y * v.y;
-                __builtin_amdgcn_sched_barrier(0);
-                sum = sum + pp[2];
-                pp[2] = v.z * v.z;
-                __builtin_amdgcn_sched_barrier(0);
-                sum = sum + pp[3];
-                pp[3] = v.w * v.w;
-                __builtin_amdgcn_sched_barrier(0);
-            };
-            const f4v* t4 = tile_s + lane;
-            f4v u0[8], u1[8];
-            auto read8 = [&](int q, f4v (&u)[8]) {
 #pragma unroll
-                for (int j = 0; j < 8; ++j) u[j] = t4[min(q + j, kq - 1) * 64];
-            };
-            int q = 0;
-            read8(0, u0);
-            for (; q + 16 <= kq; q += 16) {
-                read8(q + 8, u1);
-#pragma unroll
-                for (int j = 0; j < 8; ++j) step(u0[j]);
-                read8(q + 16, u0);
-#pragma unroll
-                for (int j = 0; j < 8; ++j) step(u1[j]);
+            for (int i = 0; i < kShare; ++i) {
+                if (i < S) {
+                    sum = sum + pp[0];
+                    pp[0] = v[i].x * v[i].x;
+                    __builtin_amdgcn_sched_barrier(0);
+                    sum = sum + pp[1];
+                    pp[1] = v[i].y * v[i].y;
+                    __builtin_amdgcn_sched_barrier(0);
+                    sum = sum + pp[2];
+                    pp[2] = v[i].z * v[i].z;
+                    __builtin_amdgcn_sched_barrier(0);
+                    sum = sum + pp[3];
+                    pp[3] = v[i].w * v[i].w;
+                    __builtin_amdgcn_sched_barrier(0);
+                }
             }
-            if (q + 8 <= kq) {
-#pragma unroll
-                for (int j = 0; j < 8; ++j) step(u0[j]);
-                q += 8;
-            }
-            for (; q < kq; ++q) step(t4[q * 64]);
             sum = sum + pp[0];
             sum = sum + pp[1];
             sum = sum + pp[2];
             sum = sum + pp[3];
+        } else {
+#pragma unroll
+            for (int i = 0; i < kShare; ++i) {
+                const int slot = i < S ? q0 + i : kNormBlocks * 16 + wave;
+                tile_s[slot * 64 + lane] = v[i] * v[i];
+            }
+        }
+        __syncthreads();
+        if (wave == 0) {
+            // Squares of quads S..kq-1, eight read while eight are added.
+            auto add_sq = [&](const f4v& q) {
+                sum = sum + q.x;
+                sum = sum + q.y;
+                sum = sum + q.z;
+                sum = sum + q.w;
+            };
+            const int n = kq - S;
+            const f4v* t4 = tile_s + S * 64 + lane;
+            int q = 0;
+            if (n >= 8) {
+                f4v u0[8], u1[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) u0[j] = t4[j * 64];
+                for (; q + 16 <= n; q += 16) {
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) u1[j] = t4[(q + 8 + j) * 64];
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) add_sq(u0[j]);
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) u0[j] = t4[min(q + 16 + j, n - 1) * 64];
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) add_sq(u1[j]);
+                }
+                if (q + 8 <= n) {
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) add_sq(u0[j]);
+                    q += 8;
+                }
+            }
+            for (; q < n; ++q) add_sq(t4[q * 64]);
             scale_s[lane] = 1.0f / sqrtf(sum / (float)a.inner + a.eps);
         }
         __syncthreads();
         const float scale = scale_s[lane];
-        for (int q = wave; q < kq; q += NW) {
-            const f4v v = tile_s[q * 64 + lane];
-            const float4 g = norm_s[q];
-            tile_s[q * 64 + lane] = f4v{v.x * scale * g.x, v.y * scale * g.y, v.z * scale * g.z, v.w * scale * g.w};
+#pragma unroll
+        for (int i = 0; i < kShare; ++i) {
+            const float4 g = norm_s[min(q0 + i, kq - 1)];
+            const int slot = i < S ? q0 + i : kNormBlocks * 16 + wave;
+            tile_s[slot * 64 + lane] =
+                f4v{v[i].x * scale * g.x, v[i].y * scale * g.y, v[i].z * scale * g.z, v[i].w * scale * g.w};
         }
         __syncthreads();
     }
