@@ -85,6 +85,23 @@ def test_smollm_shape_two_layers(torch_cuda):
     _run_sequence(model, backend, 16, chunks, table)
 
 
+def test_wide_shape_streamed_weight_paths(torch_cuda):
+    """hidden 640 / intermediate 1600 / 5 query heads per KV head: the
+    decode projections stream weight blocks through the register ring (gate
+    and up over 640, down over 1600), RMSNorm runs as its own kernel (wider
+    than the folded path takes), and decode attention takes the generic
+    kernels with the separate RoPE/append kernel."""
+    cfg = tiny_config(hidden=640, intermediate=1600, heads=10, kv_heads=2, vocabulary=512, context=128, tied=1)
+    model = OracleModel(cfg, seed=17)
+    backend = HipBackend(cfg, block_tokens=16, max_blocks=16, max_sequences=2)
+    upload_model(backend, model)
+    o = Oracle()
+    prompt = o.fill_tokens(29, 17, 3100, cfg["vocabulary"])
+    table = o.permutation(16, 17, 3101)[:8].copy()
+    chunks = [list(prompt[:20]), list(prompt[20:29])] + [[int(t)] for t in o.fill_tokens(4, 17, 3102, 512)]
+    _run_sequence(model, backend, 16, chunks, table)
+
+
 def test_batched_rows_match_single_sequences(torch_cuda):
     """Several sequences in one forward call == each appended alone."""
     cfg = smollm_config(layers=2, context=256)
