@@ -417,10 +417,11 @@ __global__ __launch_bounds__(NW * 64) void gemm_column_kernel(GemmArgs a) {
     for (int m = 0; m < M; ++m) acc[m] = 0.0f;
     f4v wr[D][M];
     f4v xr[RX];
+    // Weights are read once per step: non-temporal loads.
 #pragma unroll
     for (int d = 0; d < D; ++d)
 #pragma unroll
-        for (int m = 0; m < M; ++m) wr[d][m] = ws[m][min(d, KB - 1) * 16];
+        for (int m = 0; m < M; ++m) wr[d][m] = __builtin_nontemporal_load(&ws[m][min(d, KB - 1) * 16]);
     if (NORM) {
         // Wavefront w holds quads [w*S, (w+1)*S) of the raw tile in
         // registers. Wavefront 0 sums its own quads' squares at once while
