@@ -596,13 +596,107 @@ hipError_t launch_column(hipStream_t s, const GemmArgs& a) {
     return hipGetLastError();
 }
 
+// One row tile, M = 1, no folded RMSNorm (the O and down projections): the
+// same chains as gemm_column_kernel, k in order from 0, but the weight
+// column is staged in LDS (QMAX quads at most) and reaches the lanes through
+// broadcast reads (every lane reads the same 16 bytes), so each product is a
+// plain v_mul_f32 rather than a DPP row broadcast. Each wavefront writes and
+// reads only its own column: LDS orders a wavefront's accesses, no barrier.
+constexpr int kColWeightAhead = 4;  // weight quads read ahead from LDS
+
+template <int NW, int EPI, int QMAX>
+__global__ __launch_bounds__(NW * 64) void gemm_column_lds_kernel(GemmArgs a) {
+    constexpr int RX = kColRing, RW = kColWeightAhead;
+    static_assert(16 % RX == 0 || RX % 16 == 0, "x ring slots repeat every 16 quads");
+    static_assert(16 % RW == 0, "weight ring slots repeat every 16 quads");
+    // RW + 1 spare quads per column take the reads past its end (the last
+    // step reads quad kq + RW, whose products are never added).
+    __shared__ f4v wl_s[NW][QMAX + RW + 1];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int tile = blockIdx.y;
+    const int N = a.columns;
+    const int col = blockIdx.x * NW + wave;
+    const int n = min(col, N - 1);
+    const int kq = a.inner >> 2;
+    const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(a.x + (size_t)tile * kq * 256, (uint32_t)kq * 1024u);
+    const int xoff = lane * 16;
+    auto load_x = [&](int q) { return load_x_global(xrs, xoff, min(q, kq - 1)); };
+    // The column, all loads in flight with the first x quads.
+    constexpr int WJ = (QMAX + 63) / 64;
+    const f4v* wsrc = reinterpret_cast<const f4v*>(a.w) + (size_t)n * kq;
+    f4v wt[WJ];
+#pragma unroll
+    for (int j = 0; j < WJ; ++j) wt[j] = __builtin_nontemporal_load(&wsrc[min(j * 64 + lane, kq - 1)]);
+    f4v xr[RX];
+#pragma unroll
+    for (int i = 0; i < RX; ++i) xr[i] = load_x(i);
+    f4v* const wl = wl_s[wave];
+#pragma unroll
+    for (int j = 0; j < WJ; ++j)
+        if (j * 64 + lane < kq) wl[j * 64 + lane] = wt[j];
+    f4v wq[RW];
+#pragma unroll
+    for (int i = 0; i < RW; ++i) wq[i] = wl[i];
+
+    float acc = 0.0f;
+    float pn[4];  // products of the next quad
+    {
+        const f4v xv = xr[0], wv = wq[0];
+        xr[0] = load_x(RX);
+        wq[0] = wl[RW];
+        pn[0] = wv.x * xv.x;
+        pn[1] = wv.y * xv.y;
+        pn[2] = wv.z * xv.z;
+        pn[3] = wv.w * xv.w;
+    }
+    for (int q0 = 0; q0 < kq; q0 += 16) {
+        const f4v* const wlq = wl + q0 + 1 + RW;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            // Add quad q0+i's products in k order while forming quad q0+i+1's.
+            const int sx = (i + 1) % RX, sw = (i + 1) % RW;
+            const f4v xv = xr[sx], wv = wq[sw];
+            xr[sx] = load_x(q0 + i + 1 + RX);
+            wq[sw] = wlq[i];
+            float t = acc;
+            t = t + pn[0];
+            pn[0] = wv.x * xv.x;
+            __builtin_amdgcn_sched_barrier(0);
+            t = t + pn[1];
+            pn[1] = wv.y * xv.y;
+            __builtin_amdgcn_sched_barrier(0);
+            t = t + pn[2];
+            pn[2] = wv.z * xv.z;
+            __builtin_amdgcn_sched_barrier(0);
+            t = t + pn[3];
+            pn[3] = wv.w * xv.w;
+            __builtin_amdgcn_sched_barrier(0);
+            acc = t;
+        }
+    }
+
+    const int row = tile * 64 + lane;
+    if (row >= a.rows || col >= N) return;
+    float* o = a.out + quad_index(row, n, N);
+    if (EPI == kStore) *o = acc;
+    else *o = *o + acc;
+}
+
+template <int NW, int EPI, int QMAX>
+hipError_t launch_column_lds(hipStream_t s, const GemmArgs& a) {
+    const dim3 grid((a.columns + NW - 1) / NW, (a.rows + 63) / 64);
+    gemm_column_lds_kernel<NW, EPI, QMAX><<<grid, NW * 64, 0, s>>>(a);
+    return hipGetLastError();
+}
+
 // A weight column of up to 24 64-k blocks (inner <= 1536) is held whole;
 // longer ones stream through a kColBlocks ring.
 template <int EPI>
 hipError_t launch_column_one(hipStream_t s, const GemmArgs& a) {
     const int blocks = a.inner / 64;
-    if (blocks <= 9) return launch_column<1, 4, EPI, 9, false>(s, a);
-    if (blocks <= 24) return launch_column<1, 4, EPI, 24, false>(s, a);
+    if (blocks <= 9) return launch_column_lds<4, EPI, 9 * 16>(s, a);
+    if (blocks <= 24) return launch_column_lds<4, EPI, 24 * 16>(s, a);
     return launch_column<1, 4, EPI, kColBlocks, true>(s, a);
 }
 
