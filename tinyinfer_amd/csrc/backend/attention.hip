@@ -555,6 +555,7 @@ __global__ __launch_bounds__(kFusedThreads) void attn_decode_kernel(int heads, R
     // its scores requested here, so the producers wait on one round trip.
     constexpr int kProducerBatches = (kFusedMaxT / 64 + kProducers - 1) / kProducers;
     float sall[kProducerBatches][G], cmax[G];
+    float touch[kTouchPages];  // producers: V pages read ahead, see below
     if (wave >= G) {
 #pragma unroll
         for (int h = 0; h < G; ++h) {
@@ -596,17 +597,17 @@ __global__ __launch_bounds__(kFusedThreads) void attn_decode_kernel(int heads, R
         // Then touch this KV head's V pages (one dword per 64 bytes, a page
         // per instruction; this wavefront's share of the first
         // kTouchPages * kProducers pages, all in flight together) so that the
-        // output chains find them in cache rather than in HBM.
+        // output chains find them in cache rather than in HBM. The loaded
+        // values are consumed only when the producers leave (phase 5): the
+        // barriers in between wait for LDS work only, not for these loads.
         const float* vf = kv.values;
-        float touch[kTouchPages];
 #pragma unroll
         for (int i = 0; i < kTouchPages; ++i)
             touch[i] = vf[(size_t)voff_s[min(wave - G + i * kProducers, last_page)] * 4 + lane * 16];
-        float sink = 0.0f;
-#pragma unroll
-        for (int i = 0; i < kTouchPages; ++i) sink += touch[i];
-        asm volatile("" ::"v"(sink));
     } else {
+        // Consumer: its adds are the work-group's critical path, so it takes
+        // issue priority over the producer sharing its SIMD until den is out.
+        __builtin_amdgcn_s_setprio(3);
         // Consumer: head h = wave sums its e_t in token order, every lane the
         // same chain, a batch as soon as its flag is up. The wait is bounded;
         // every flag below `batches` is set by a producer.
@@ -667,6 +668,7 @@ __global__ __launch_bounds__(kFusedThreads) void attn_decode_kernel(int heads, R
             for (int t = 64 * full; t < len; ++t) den = den + es[t];
         }
         if (lane == 0) den_s[wave] = den;
+        __builtin_amdgcn_s_setprio(0);
     }
     lds_barrier();
     // ---- 4. p_t = e_t / den
@@ -678,7 +680,13 @@ __global__ __launch_bounds__(kFusedThreads) void attn_decode_kernel(int heads, R
     lds_barrier();
 
     // ---- 5. output chains (no barrier from here on)
-    if (wave >= G) return;
+    if (wave >= G) {
+        float sink = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kTouchPages; ++i) sink += touch[i];
+        asm volatile("" ::"v"(sink));
+        return;
+    }
     // p of 64-token group g: lane l holds p[64g + 4(l%16) .. +3], so the p of
     // token 64g + 4i + c is component c of lane i of every 16-lane row and
     // reaches all lanes through a DPP row broadcast folded into the multiply.
