@@ -386,6 +386,106 @@ __device__ __forceinline__ f4v load_x_global(__amdgpu_buffer_rsrc_t rsrc, int la
 // inner <= 64*D (the tile fits the work-group's LDS).
 constexpr int kNormBlocks = 9;  // inner <= 576 for the folded RMSNorm
 
+// RMSNorm of a 64-row tile (llama_runner.cpp:10-16, rows.hip's rms_kernel
+// arithmetic) into tile_s ([quad][row]; NW spare quads take the writes of
+// quads past the tile), for the products to read x from LDS. Wavefront w
+// holds quads [w*S, (w+1)*S) of the raw tile in registers; wavefront 0 sums
+// its own quads' squares at once while the others write their squares into
+// the tile's slots, then continues with adds only over those, and every
+// wavefront writes its quads, normalized, into the same slots. Ends with a
+// barrier.
+template <int NW>
+__device__ __forceinline__ void norm_tile(const GemmArgs& a, __amdgpu_buffer_rsrc_t xrs, int xoff, int lane, int wave,
+                                          int kq, f4v* tile_s, float* scale_s, float4* norm_s) {
+    constexpr int kShare = kNormBlocks * 16 / NW;  // quads per wavefront at most
+    static_assert(kNormBlocks * 16 % NW == 0, "tile split");
+    const int S = kq / NW, q0 = wave * S;  // kq is a multiple of 16 and NW divides 16
+    f4v v[kShare];
+#pragma unroll
+    for (int i = 0; i < kShare; ++i) v[i] = load_x_global(xrs, xoff, min(q0 + i, kq - 1));
+    if ((int)threadIdx.x < kq) norm_s[threadIdx.x] = reinterpret_cast<const float4*>(a.norm)[threadIdx.x];
+    // Sum of squares in column order (llama_runner.cpp:10-16).
+    float sum = 0.0f;
+    if (wave == 0) {
+        // The squares of the next quad are formed between the four adds
+        // of the pending one; pp starts as four zero squares, whose adds
+        // leave sum at +0.0f.
+        float pp[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int i = 0; i < kShare; ++i) {
+            if (i < S) {
+                sum = sum + pp[0];
+                pp[0] = v[i].x * v[i].x;
+                __builtin_amdgcn_sched_barrier(0);
+                sum = sum + pp[1];
+                pp[1] = v[i].y * v[i].y;
+                __builtin_amdgcn_sched_barrier(0);
+                sum = sum + pp[2];
+                pp[2] = v[i].z * v[i].z;
+                __builtin_amdgcn_sched_barrier(0);
+                sum = sum + pp[3];
+                pp[3] = v[i].w * v[i].w;
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        sum = sum + pp[0];
+        sum = sum + pp[1];
+        sum = sum + pp[2];
+        sum = sum + pp[3];
+    } else {
+#pragma unroll
+        for (int i = 0; i < kShare; ++i) {
+            const int slot = i < S ? q0 + i : kNormBlocks * 16 + wave;
+            tile_s[slot * 64 + lane] = v[i] * v[i];
+        }
+    }
+    __syncthreads();
+    if (wave == 0) {
+        // Squares of quads S..kq-1, eight read while eight are added.
+        auto add_sq = [&](const f4v& q) {
+            sum = sum + q.x;
+            sum = sum + q.y;
+            sum = sum + q.z;
+            sum = sum + q.w;
+        };
+        const int n = kq - S;
+        const f4v* t4 = tile_s + S * 64 + lane;
+        int q = 0;
+        if (n >= 8) {
+            f4v u0[8], u1[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) u0[j] = t4[j * 64];
+            for (; q + 16 <= n; q += 16) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) u1[j] = t4[(q + 8 + j) * 64];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) add_sq(u0[j]);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) u0[j] = t4[min(q + 16 + j, n - 1) * 64];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) add_sq(u1[j]);
+            }
+            if (q + 8 <= n) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) add_sq(u0[j]);
+                q += 8;
+            }
+        }
+        for (; q < n; ++q) add_sq(t4[q * 64]);
+        scale_s[lane] = 1.0f / sqrtf(sum / (float)a.inner + a.eps);
+    }
+    __syncthreads();
+    const float scale = scale_s[lane];
+#pragma unroll
+    for (int i = 0; i < kShare; ++i) {
+        const float4 g = norm_s[min(q0 + i, kq - 1)];
+        const int slot = i < S ? q0 + i : kNormBlocks * 16 + wave;
+        tile_s[slot * 64 + lane] =
+            f4v{v[i].x * scale * g.x, v[i].y * scale * g.y, v[i].z * scale * g.z, v[i].w * scale * g.w};
+    }
+    __syncthreads();
+}
+
 template <int M, int NW, int EPI, int D = kColBlocks, bool RELOAD = true, bool NORM = false>
 __global__ __launch_bounds__(NW * 64) void gemm_column_kernel(GemmArgs a) {
     constexpr int RX = kColRing;
@@ -422,100 +522,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_column_kernel(GemmArgs a) {
     for (int d = 0; d < D; ++d)
 #pragma unroll
         for (int m = 0; m < M; ++m) wr[d][m] = __builtin_nontemporal_load(&ws[m][min(d, KB - 1) * 16]);
-    if (NORM) {
-        // Wavefront w holds quads [w*S, (w+1)*S) of the raw tile in
-        // registers. Wavefront 0 sums its own quads' squares at once while
-        // the others write their squares into the tile's LDS slots; then
-        // wavefront 0 continues with adds only over those, and every
-        // wavefront writes its quads, normalized, into the same slots.
-        constexpr int kShare = kNormBlocks * 16 / NW;  // quads per wavefront at most
-        static_assert(kNormBlocks * 16 % NW == 0, "tile split");
-        const int S = kq / NW, q0 = wave * S;  // kq is a multiple of 16 and NW divides 16
-        f4v v[kShare];
-#pragma unroll
-        for (int i = 0; i < kShare; ++i) v[i] = load_x_global(xrs, xoff, min(q0 + i, kq - 1));
-        if ((int)threadIdx.x < kq) norm_s[threadIdx.x] = reinterpret_cast<const float4*>(a.norm)[threadIdx.x];
-        // Sum of squares in column order (llama_runner.cpp:10-16).
-        float sum = 0.0f;
-        if (wave == 0) {
-            // The squares of the next quad are formed between the four adds
-            // of the pending one; pp starts as four zero squares, whose adds
-            // leave sum at +0.0f.
-            float pp[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int i = 0; i < kShare; ++i) {
-                if (i < S) {
-                    sum = sum + pp[0];
-                    pp[0] = v[i].x * v[i].x;
-                    __builtin_amdgcn_sched_barrier(0);
-                    sum = sum + pp[1];
-                    pp[1] = v[i].y * v[i].y;
-                    __builtin_amdgcn_sched_barrier(0);
-                    sum = sum + pp[2];
-                    pp[2] = v[i].z * v[i].z;
-                    __builtin_amdgcn_sched_barrier(0);
-                    sum = sum + pp[3];
-                    pp[3] = v[i].w * v[i].w;
-                    __builtin_amdgcn_sched_barrier(0);
-                }
-            }
-            sum = sum + pp[0];
-            sum = sum + pp[1];
-            sum = sum + pp[2];
-            sum = sum + pp[3];
-        } else {
-#pragma unroll
-            for (int i = 0; i < kShare; ++i) {
-                const int slot = i < S ? q0 + i : kNormBlocks * 16 + wave;
-                tile_s[slot * 64 + lane] = v[i] * v[i];
-            }
-        }
-        __syncthreads();
-        if (wave == 0) {
-            // Squares of quads S..kq-1, eight read while eight are added.
-            auto add_sq = [&](const f4v& q) {
-                sum = sum + q.x;
-                sum = sum + q.y;
-                sum = sum + q.z;
-                sum = sum + q.w;
-            };
-            const int n = kq - S;
-            const f4v* t4 = tile_s + S * 64 + lane;
-            int q = 0;
-            if (n >= 8) {
-                f4v u0[8], u1[8];
-#pragma unroll
-                for (int j = 0; j < 8; ++j) u0[j] = t4[j * 64];
-                for (; q + 16 <= n; q += 16) {
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) u1[j] = t4[(q + 8 + j) * 64];
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) add_sq(u0[j]);
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) u0[j] = t4[min(q + 16 + j, n - 1) * 64];
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) add_sq(u1[j]);
-                }
-                if (q + 8 <= n) {
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) add_sq(u0[j]);
-                    q += 8;
-                }
-            }
-            for (; q < n; ++q) add_sq(t4[q * 64]);
-            scale_s[lane] = 1.0f / sqrtf(sum / (float)a.inner + a.eps);
-        }
-        __syncthreads();
-        const float scale = scale_s[lane];
-#pragma unroll
-        for (int i = 0; i < kShare; ++i) {
-            const float4 g = norm_s[min(q0 + i, kq - 1)];
-            const int slot = i < S ? q0 + i : kNormBlocks * 16 + wave;
-            tile_s[slot * 64 + lane] =
-                f4v{v[i].x * scale * g.x, v[i].y * scale * g.y, v[i].z * scale * g.z, v[i].w * scale * g.w};
-        }
-        __syncthreads();
-    }
+    if (NORM) norm_tile<NW>(a, xrs, xoff, lane, wave, kq, tile_s, scale_s, norm_s);
 #pragma unroll
     for (int i = 0; i < RX; ++i) xr[i] = load_x(i);
     float pn[M][4];  // products of the next quad
@@ -596,17 +603,23 @@ hipError_t launch_column(hipStream_t s, const GemmArgs& a) {
     return hipGetLastError();
 }
 
-// One row tile, M = 1, no folded RMSNorm (the O and down projections): the
-// same chains as gemm_column_kernel, k in order from 0, but the weight
-// column is staged in LDS (QMAX quads at most) and reaches the lanes through
-// broadcast reads (every lane reads the same 16 bytes), so each product is a
-// plain v_mul_f32 rather than a DPP row broadcast. Each wavefront writes and
-// reads only its own column: LDS orders a wavefront's accesses, no barrier.
+// One row tile, M = 1 (QKV with the folded RMSNorm, O, down): the same
+// chains as gemm_column_kernel, k in order from 0, but the weight column is
+// staged in LDS (QMAX quads at most) and reaches the lanes through broadcast
+// reads (every lane reads the same 16 bytes), so each product is a plain
+// v_mul_f32 rather than a DPP row broadcast. Each wavefront writes and reads
+// only its own column: LDS orders a wavefront's accesses, no barrier. With
+// NORM, x is the RMSNorm of the tile formed by norm_tile in LDS (inner <=
+// 576; with four wavefronts the tile and the columns just fit the 160 KB).
 constexpr int kColWeightAhead = 4;  // weight quads read ahead from LDS
 
-template <int NW, int EPI, int QMAX>
+template <int NW, int EPI, int QMAX, bool NORM = false>
 __global__ __launch_bounds__(NW * 64) void gemm_column_lds_kernel(GemmArgs a) {
     constexpr int RX = kColRing, RW = kColWeightAhead;
+    static_assert(!NORM || QMAX == kNormBlocks * 16, "the folded RMSNorm holds the whole tile");
+    __shared__ f4v tile_s[NORM ? (kNormBlocks * 16 + NW) * 64 : 1];
+    __shared__ float scale_s[NORM ? 64 : 1];
+    __shared__ float4 norm_s[NORM ? kNormBlocks * 16 : 1];
     static_assert(16 % RX == 0 || RX % 16 == 0, "x ring slots repeat every 16 quads");
     static_assert(16 % RW == 0, "weight ring slots repeat every 16 quads");
     // RW + 1 spare quads per column take the reads past its end (the last
@@ -621,13 +634,18 @@ __global__ __launch_bounds__(NW * 64) void gemm_column_lds_kernel(GemmArgs a) {
     const int kq = a.inner >> 2;
     const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(a.x + (size_t)tile * kq * 256, (uint32_t)kq * 1024u);
     const int xoff = lane * 16;
-    auto load_x = [&](int q) { return load_x_global(xrs, xoff, min(q, kq - 1)); };
-    // The column, all loads in flight with the first x quads.
+    auto load_x = [&](int q) {
+        if (NORM) return tile_s[min(q, kq - 1) * 64 + lane];
+        return load_x_global(xrs, xoff, min(q, kq - 1));
+    };
+    // The column, all loads in flight with the first x quads (or the raw
+    // tile of the folded RMSNorm).
     constexpr int WJ = (QMAX + 63) / 64;
     const f4v* wsrc = reinterpret_cast<const f4v*>(a.w) + (size_t)n * kq;
     f4v wt[WJ];
 #pragma unroll
     for (int j = 0; j < WJ; ++j) wt[j] = __builtin_nontemporal_load(&wsrc[min(j * 64 + lane, kq - 1)]);
+    if (NORM) norm_tile<NW>(a, xrs, xoff, lane, wave, kq, tile_s, scale_s, norm_s);
     f4v xr[RX];
 #pragma unroll
     for (int i = 0; i < RX; ++i) xr[i] = load_x(i);
@@ -683,10 +701,10 @@ __global__ __launch_bounds__(NW * 64) void gemm_column_lds_kernel(GemmArgs a) {
     else *o = *o + acc;
 }
 
-template <int NW, int EPI, int QMAX>
+template <int NW, int EPI, int QMAX, bool NORM = false>
 hipError_t launch_column_lds(hipStream_t s, const GemmArgs& a) {
     const dim3 grid((a.columns + NW - 1) / NW, (a.rows + 63) / 64);
-    gemm_column_lds_kernel<NW, EPI, QMAX><<<grid, NW * 64, 0, s>>>(a);
+    gemm_column_lds_kernel<NW, EPI, QMAX, NORM><<<grid, NW * 64, 0, s>>>(a);
     return hipGetLastError();
 }
 
@@ -713,7 +731,7 @@ hipError_t launch_gemm_normed(hipStream_t s, Epilogue epilogue, const GemmArgs& 
     if (!gemm_normed_fits(epilogue, a)) return hipErrorInvalidValue;
     // The LDS tile allows one work-group per CU: four wavefronts for one
     // matrix, eight for gate and up.
-    if (epilogue == kStore) return launch_column<1, 4, kStore, kNormBlocks, false, true>(s, a);
+    if (epilogue == kStore) return launch_column_lds<4, kStore, kNormBlocks * 16, true>(s, a);
     return launch_column<2, 8, kSwiglu, kNormBlocks, false, true>(s, a);
 }
 
