@@ -486,15 +486,22 @@ __device__ __forceinline__ void norm_tile(const GemmArgs& a, __amdgpu_buffer_rsr
     __syncthreads();
 }
 
-template <int M, int NW, int EPI, int D = kColBlocks, bool RELOAD = true, bool NORM = false>
+// UP (M = 2, whole column held): the second matrix's weights (up) also go
+// through a per-wavefront LDS ring of two 64-k blocks, written from the
+// registers one block ahead by lanes 0-15 and read back at one address four
+// quads ahead, so its products are plain v_mul_f32; the first (gate) keeps
+// the DPP broadcast. The ring is the wavefront's own: no barrier.
+template <int M, int NW, int EPI, int D = kColBlocks, bool RELOAD = true, bool NORM = false, bool UP = false>
 __global__ __launch_bounds__(NW * 64) void gemm_column_kernel(GemmArgs a) {
     constexpr int RX = kColRing;
     static_assert((D * 16) % RX == 0, "ring slots repeat every D blocks");
     static_assert(!NORM || (!RELOAD && D == kNormBlocks), "folded RMSNorm holds the whole tile");
+    static_assert(!UP || (M == 2 && !RELOAD), "the up ring is filled from the held column");
     // [quad][row]; NW spare quads take the writes of quads past the tile
     __shared__ f4v tile_s[NORM ? (kNormBlocks * 16 + NW) * 64 : 1];
     __shared__ float scale_s[NORM ? 64 : 1];
     __shared__ float4 norm_s[NORM ? kNormBlocks * 16 : 1];  // RMSNorm weights by quad
+    __shared__ f4v up_s[UP ? NW * 32 : 1];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int tile = blockIdx.y;
@@ -525,48 +532,76 @@ __global__ __launch_bounds__(NW * 64) void gemm_column_kernel(GemmArgs a) {
     if (NORM) norm_tile<NW>(a, xrs, xoff, lane, wave, kq, tile_s, scale_s, norm_s);
 #pragma unroll
     for (int i = 0; i < RX; ++i) xr[i] = load_x(i);
+    // UP: ring quads 0-15 hold block J (even J) or 16-31 (odd J); uq holds
+    // the up weights of quads q+1 .. q+4 (slot (q+1) % 4 is used next).
+    f4v* const ur = up_s + (UP ? wave * 32 : 0);
+    f4v uq[4];
+    if (UP) {
+        if (lane < 16) {
+            ur[lane] = wr[0][M - 1];
+            ur[16 + lane] = wr[D > 1 ? 1 : 0][M - 1];
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) uq[k] = ur[k];
+    }
     float pn[M][4];  // products of the next quad
     {
         const f4v xv = xr[0];
         xr[0] = load_x(RX);
 #pragma unroll
         for (int m = 0; m < M; ++m) {
-            pn[m][0] = mul_bcast<0>(wr[0][m].x, xv.x);
-            pn[m][1] = mul_bcast<0>(wr[0][m].y, xv.y);
-            pn[m][2] = mul_bcast<0>(wr[0][m].z, xv.z);
-            pn[m][3] = mul_bcast<0>(wr[0][m].w, xv.w);
+            if (UP && m == 1) {
+                pn[m][0] = uq[0].x * xv.x;
+                pn[m][1] = uq[0].y * xv.y;
+                pn[m][2] = uq[0].z * xv.z;
+                pn[m][3] = uq[0].w * xv.w;
+            } else {
+                pn[m][0] = mul_bcast<0>(wr[0][m].x, xv.x);
+                pn[m][1] = mul_bcast<0>(wr[0][m].y, xv.y);
+                pn[m][2] = mul_bcast<0>(wr[0][m].z, xv.z);
+                pn[m][3] = mul_bcast<0>(wr[0][m].w, xv.w);
+            }
         }
+        if (UP) uq[0] = ur[4];
     }
     for (int J0 = 0; J0 < KB; J0 += D) {
 #pragma unroll
         for (int d = 0; d < D; ++d) {
             const int J = J0 + d;
             if (J >= KB) break;
+            // UP: block J+1 goes into the ring slot block J-1 has left.
+            if (UP && d >= 1 && lane < 16 && J + 1 < KB) ur[((J + 1) & 1) * 16 + lane] = wr[d + 1 < D ? d + 1 : d][M - 1];
+            const int jb = (J & 1) * 16;
             // Quad i of block J: add its products in k order while forming
             // those of the next quad (lane i+1 of this block, or lane 0 of
-            // the next block held in wr[(d+1)%D]).
+            // the next block held in wr[(d+1)%D]; for UP's second matrix the
+            // ring quad read four quads ago).
+#define MP_COLUMN_MUL(i, m, c) \
+    ((UP && (m) == 1) ? uv.c * xv.c : mul_bcast<((i) + 1) & 15>(wr[dn][m].c, xv.c))
 #define MP_COLUMN_QUAD(i)                                                               \
     {                                                                                   \
         const int slot = (d * 16 + (i) + 1) % RX;                                       \
         const int dn = (i) == 15 ? (d + 1) % D : d;                                     \
         const f4v xv = xr[slot];                                                        \
         xr[slot] = load_x(J * 16 + (i) + 1 + RX);                                       \
+        const f4v uv = uq[((i) + 1) % 4];                                               \
         for (int m = 0; m < M; ++m) {                                                   \
             float t = acc[m];                                                           \
             t = t + pn[m][0];                                                           \
-            pn[m][0] = mul_bcast<((i) + 1) & 15>(wr[dn][m].x, xv.x);                    \
+            pn[m][0] = MP_COLUMN_MUL(i, m, x);                                           \
             __builtin_amdgcn_sched_barrier(0);                                          \
             t = t + pn[m][1];                                                           \
-            pn[m][1] = mul_bcast<((i) + 1) & 15>(wr[dn][m].y, xv.y);                    \
+            pn[m][1] = MP_COLUMN_MUL(i, m, y);                                           \
             __builtin_amdgcn_sched_barrier(0);                                          \
             t = t + pn[m][2];                                                           \
-            pn[m][2] = mul_bcast<((i) + 1) & 15>(wr[dn][m].z, xv.z);                    \
+            pn[m][2] = MP_COLUMN_MUL(i, m, z);                                           \
             __builtin_amdgcn_sched_barrier(0);                                          \
             t = t + pn[m][3];                                                           \
-            pn[m][3] = mul_bcast<((i) + 1) & 15>(wr[dn][m].w, xv.w);                    \
+            pn[m][3] = MP_COLUMN_MUL(i, m, w);                                           \
             __builtin_amdgcn_sched_barrier(0);                                          \
             acc[m] = t;                                                                 \
         }                                                                               \
+        if (UP) uq[((i) + 1) % 4] = ur[(jb + (i) + 5) & 31];                            \
     }
             MP_COLUMN_QUAD(0) MP_COLUMN_QUAD(1) MP_COLUMN_QUAD(2) MP_COLUMN_QUAD(3)
             MP_COLUMN_QUAD(4) MP_COLUMN_QUAD(5) MP_COLUMN_QUAD(6) MP_COLUMN_QUAD(7)
@@ -579,6 +614,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_column_kernel(GemmArgs a) {
             }
             MP_COLUMN_QUAD(15)
 #undef MP_COLUMN_QUAD
+#undef MP_COLUMN_MUL
         }
     }
 
@@ -596,10 +632,10 @@ __global__ __launch_bounds__(NW * 64) void gemm_column_kernel(GemmArgs a) {
 }
 
 
-template <int M, int NW, int EPI, int D, bool RELOAD, bool NORM = false>
+template <int M, int NW, int EPI, int D, bool RELOAD, bool NORM = false, bool UP = false>
 hipError_t launch_column(hipStream_t s, const GemmArgs& a) {
     const dim3 grid((a.columns + NW - 1) / NW, (a.rows + 63) / 64);
-    gemm_column_kernel<M, NW, EPI, D, RELOAD, NORM><<<grid, NW * 64, 0, s>>>(a);
+    gemm_column_kernel<M, NW, EPI, D, RELOAD, NORM, UP><<<grid, NW * 64, 0, s>>>(a);
     return hipGetLastError();
 }
 
@@ -732,7 +768,7 @@ hipError_t launch_gemm_normed(hipStream_t s, Epilogue epilogue, const GemmArgs& 
     // The LDS tile allows one work-group per CU: four wavefronts for one
     // matrix, eight for gate and up.
     if (epilogue == kStore) return launch_column_lds<4, kStore, kNormBlocks * 16, true>(s, a);
-    return launch_column<2, 8, kSwiglu, kNormBlocks, false, true>(s, a);
+    return launch_column<2, 8, kSwiglu, kNormBlocks, false, true, true>(s, a);
 }
 
 hipError_t launch_gemm(hipStream_t s, Epilogue epilogue, const GemmArgs& a) {
