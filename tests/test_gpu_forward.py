@@ -102,6 +102,24 @@ def test_wide_shape_streamed_weight_paths(torch_cuda):
     _run_sequence(model, backend, 16, chunks, table)
 
 
+def test_narrow_shape_short_weight_columns(torch_cuda):
+    """hidden 128 / intermediate 192: the decode projections run on the
+    one-row-tile kernels with columns of 2 and 3 64-k blocks. QKV takes the
+    folded RMSNorm with LDS-held weights, gate/up the folded RMSNorm with the
+    up-weight ring past its last block, and O and down the LDS-held weights
+    well short of their capacity. Decode attention takes the fused kernels
+    (head dim 64, two query heads per KV head)."""
+    cfg = tiny_config(hidden=128, intermediate=192, heads=2, kv_heads=1, vocabulary=256, context=128, tied=0)
+    model = OracleModel(cfg, seed=23)
+    backend = HipBackend(cfg, block_tokens=16, max_blocks=16, max_sequences=2)
+    upload_model(backend, model)
+    o = Oracle()
+    prompt = o.fill_tokens(37, 23, 3200, cfg["vocabulary"])
+    table = o.permutation(16, 23, 3201)[:8].copy()
+    chunks = [list(prompt[:24]), list(prompt[24:37])] + [[int(t)] for t in o.fill_tokens(5, 23, 3202, 256)]
+    _run_sequence(model, backend, 16, chunks, table)
+
+
 def test_batched_rows_match_single_sequences(torch_cuda):
     """Several sequences in one forward call == each appended alone."""
     cfg = smollm_config(layers=2, context=256)
