@@ -768,6 +768,9 @@ hipError_t launch_gemm_normed(hipStream_t s, Epilogue epilogue, const GemmArgs& 
     // The LDS tile allows one work-group per CU: four wavefronts for one
     // matrix, eight for gate and up.
     if (epilogue == kStore) return launch_column_lds<4, kStore, kNormBlocks * 16, true>(s, a);
+    // Six wavefronts where they split the tile evenly (inner a multiple of
+    // 96): one work-group per CU at 1,536 columns, fewer waves on its LDS.
+    if ((a.inner / 4) % 6 == 0) return launch_column<2, 6, kSwiglu, kNormBlocks, false, true, true>(s, a);
     return launch_column<2, 8, kSwiglu, kNormBlocks, false, true, true>(s, a);
 }
 
