@@ -106,8 +106,14 @@ int mp_hip_ready(const mp_hip* h, int32_t* ready);
 int mp_hip_table_write(mp_hip* h, int32_t slot, int32_t first, const int32_t* blocks, int32_t count);
 
 /* Copy-on-write of a shared partial tail: copies the region in BOTH the K
- * and the V pool with one kernel (llama_runner.cu:130-137). Asynchronous on
- * the context's stream; ordered before the next forward. */
+ * and the V pool with one kernel (llama_runner.cu:130-137). The region must
+ * be one KVManager forms: pitch = block_tokens*kv_width, rows = layers,
+ * width = valid tokens * kv_width, source and destination page bases.
+ * Inside a page the pools use the device order, and the copy moves the
+ * valid tokens' K and V in that order (the same bytes the reference's 2-D
+ * copy moves, counted the same way in the COW statistics). Other regions
+ * are MP_INVALID_ARGUMENT. Asynchronous on the context's stream; ordered
+ * before the next forward. */
 int mp_hip_copy_tail(mp_hip* h, const mp_tail_region* region);
 
 /* Same copy, timed with device events around it (the reference's opt-in

@@ -618,15 +618,20 @@ __global__ __launch_bounds__(kFusedThreads) void attn_decode_kernel(int heads, R
         typedef uint32_t u4v __attribute__((ext_vector_type(4)));
         typedef __attribute__((address_space(3))) u4v LdsU4;
         volatile LdsU4* const flags4 = (volatile LdsU4*)ready_s[wave];
+        // A wait that runs out (it cannot while every producer runs) records
+        // a device error that the host turns into a failed forward; the
+        // work-group still runs to its end so every wave leaves normally.
         auto wait_group = [&](int g) {
-            for (int spin = 0; spin < (1 << 16); ++spin) {
+            bool ok = false;
+            for (int spin = 0; spin < (1 << 16) && !ok; ++spin) {
                 const u4v f = flags4[g];
                 const int b = 4 * g;
-                const bool ok = (f.x | (b >= batches)) && (f.y | (b + 1 >= batches)) &&
-                                (f.z | (b + 2 >= batches)) && (f.w | (b + 3 >= batches));
-                if (__builtin_amdgcn_readfirstlane(ok ? 1 : 0)) break;
-                __builtin_amdgcn_s_sleep(1);
+                const bool set = (f.x | (b >= batches)) && (f.y | (b + 1 >= batches)) &&
+                                 (f.z | (b + 2 >= batches)) && (f.w | (b + 3 >= batches));
+                ok = __builtin_amdgcn_readfirstlane(set ? 1 : 0) != 0;
+                if (!ok) __builtin_amdgcn_s_sleep(1);
             }
+            if (!ok && lane == 0 && w.error) __hip_atomic_fetch_or(w.error, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             asm volatile("" ::: "memory");
         };
         auto read_batch = [&](int b, float4 (&ev)[16]) {

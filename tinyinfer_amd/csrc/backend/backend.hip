@@ -68,7 +68,7 @@ struct mp_hip {
     size_t staging_floats = 0;
     int32_t* meta = nullptr;  // tokens | row_seq | row_pos | seq_slot | seq_last_row | blocks | items
     size_t meta_capacity = 0;   // int32 entries
-    int32_t* results = nullptr;  // argmax[seqs] | nonfinite[seqs]
+    int32_t* results = nullptr;  // argmax[seqs] | nonfinite[seqs] | device error word
     // Block-table entries written since the last flush (table index ->
     // block id): applied on the device at the start of the next forward
     // (or sync), uploaded with that call's metadata.
@@ -224,7 +224,7 @@ int ensure_workspace(mp_hip* h, int rows, int seqs, int max_length) {
         {(void**)&h->ffn, sizeof(float) * R * (size_t)c.intermediate},
         {(void**)&h->last, sizeof(float) * S * hd},
         {(void**)&h->logits, sizeof(float) * S * (size_t)c.vocabulary},
-        {(void**)&h->results, sizeof(int32_t) * 2 * (size_t)S},
+        {(void**)&h->results, sizeof(int32_t) * (2 * (size_t)S + 4)},
         {(void**)&h->best_value, sizeof(float) * S * groups},
         {(void**)&h->best_index, sizeof(int32_t) * S * groups},
         {(void**)&h->best_bad, sizeof(int32_t) * S * groups},
@@ -437,8 +437,9 @@ int mp_hip_upload_tensor(mp_hip* h, int32_t layer, int32_t slot, const float* da
         return fail(h, MP_INVALID_ARGUMENT, "invalid tensor slot");
     const size_t expected = tensor_elements(c, layer, slot);
     if (!expected || count != expected) return fail(h, MP_INVALID_ARGUMENT, "tensor shape mismatch");
-    for (size_t i = 0; i < count; ++i)
-        if (!std::isfinite(data[i])) return fail(h, MP_INVALID_ARGUMENT, "nonfinite weights");
+    // Non-finite weights are accepted, as the reference runners accept them
+    // (cow_test.cpp:135): they surface as non-finite logits of the forwards
+    // that read them (MP_NONFINITE), which the runner rolls back.
     const size_t bytes = count * sizeof(float);
     const int hd = c.hidden, kvw = kv_width(c), in = c.intermediate;
     hipError_t e = hipSuccess;
@@ -518,20 +519,22 @@ int mp_hip_table_write(mp_hip* h, int32_t slot, int32_t first, const int32_t* bl
 int mp_hip_copy_tail(mp_hip* h, const mp_tail_region* r) {
     if (!h || !r) return MP_INVALID_ARGUMENT;
     if (!r->rows || !r->width) return MP_OK;
-    // A page region (pitch = one page of one layer) carries the valid tail
-    // tokens somewhere inside each page-layer span in the device layout, so
-    // whole spans are copied; slots beyond the valid tail are rewritten by
-    // later appends before any attention reads them. Other regions are
-    // plain strided copies of `width` floats per row.
-    const uint64_t page = (uint64_t)h->kv.block_tokens * kv_width(h->model);
-    const uint64_t width = r->pitch == page ? page : r->width;
-    const uint64_t span = (r->rows - 1) * r->pitch + width;
-    if (r->width > r->pitch || r->destination + span > h->pool_elements ||
-        r->source + span > h->pool_elements)
-        return fail(h, MP_INVALID_ARGUMENT, "tail copy region out of range");
-    const int status = check(h, mphip::launch_copy_region(h->stream, h->keys, h->values,
-                                                          r->destination, r->source, r->pitch,
-                                                          width, r->rows),
+    // Only the regions KVManager forms (kv_manager.cpp:160-169): one page of
+    // every layer, pitch = one page-layer span, width = valid tokens x
+    // kv_width, page-aligned source and destination. The pools keep the
+    // reference's page bases but their own order inside a page, so the copy
+    // moves the valid slots in that order (launch_copy_tail).
+    const mp_model_desc& c = h->model;
+    const uint64_t kvw = (uint64_t)kv_width(c);
+    const uint64_t page = (uint64_t)h->kv.block_tokens * kvw;
+    const uint64_t block = page * (uint64_t)c.layers;
+    if (r->pitch != page || r->rows != (uint64_t)c.layers || r->width % kvw || r->width > page ||
+        r->destination % block || r->source % block || r->destination / block >= (uint64_t)h->kv.max_blocks ||
+        r->source / block >= (uint64_t)h->kv.max_blocks)
+        return fail(h, MP_INVALID_ARGUMENT, "tail copy region is not a page region of the pools");
+    const int status = check(h, mphip::launch_copy_tail(h->stream, h->keys, h->values, r->destination, r->source,
+                                                        c.layers, (int)(r->width / kvw), h->kv.block_tokens,
+                                                        c.kv_heads, c.hidden / c.heads),
                              "COW copy");
     if (!status) {
         ++h->stats.cow_copies;
@@ -656,6 +659,8 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
     work.stride = score_stride(max_length);
     work.chunks = score_chunks(max_length);
     work.chunk_max = h->scratch + (size_t)R * c.heads * work.stride;
+    int32_t* const device_error = h->results + 2 * (size_t)nseq;
+    work.error = device_error;
     hipStream_t s = h->stream;
     // Launches of an enabled timing class are bracketed by a pair of events
     // from the pool that mp_hip_set_timing sized for one forward call:
@@ -721,7 +726,7 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
         if (r == hipSuccess) r = gemm(epi, h->xn, rows, inner, w, w2, columns, out);
         return r;
     };
-    hipError_t e = mphip::launch_embed(s, h->embedding, meta.tokens, h->x, R, hd);
+    hipError_t e = mphip::launch_embed(s, h->embedding, meta.tokens, h->x, R, hd, device_error);
     for (int l = 0; l < c.layers && e == hipSuccess; ++l) {
         layer_now = l;
         e = timed(P, [&] { return normed_gemm(mphip::kStore, h->input_norm[l], R, hd, h->qkv[l], nullptr, qw, h->qkv_out); });
@@ -755,11 +760,12 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
         return r;
     });
     if ((status = check(h, e, "model kernel launch"))) return status;
-    if ((status = ensure_pinned(h, &h->host_results, &h->host_results_capacity, 2 * (size_t)nseq,
+    if ((status = ensure_pinned(h, &h->host_results, &h->host_results_capacity, 2 * (size_t)nseq + 1,
                                 "allocate pinned results")))
         return status;
     int32_t* const results = h->host_results;
-    status = check(h, hipMemcpyAsync(results, h->results, sizeof(int32_t) * 2 * nseq, hipMemcpyDeviceToHost, s), "download argmax");
+    status = check(h, hipMemcpyAsync(results, h->results, sizeof(int32_t) * (2 * nseq + 1), hipMemcpyDeviceToHost, s),
+                   "download argmax");
     if (!status && logits) {
         status = check(h, hipMemcpyAsync(logits, h->logits, sizeof(float) * (size_t)nseq * c.vocabulary, hipMemcpyDeviceToHost, s), "download logits");
         if (!status) h->stats.logits_downloaded_bytes += sizeof(float) * (size_t)nseq * c.vocabulary;
@@ -776,6 +782,8 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
         if (h->spans[i] == MP_TIME_PROJECTION) t.projection_ns += ns, ++t.projection_launches;
         if (h->spans[i] == MP_TIME_HEAD) t.head_ns += ns, ++t.head_launches;
     }
+    if (results[2 * (size_t)nseq])
+        return fail(h, MP_DEVICE_ERROR, "attention kernel gave up a bounded wait; results discarded");
     std::memcpy(argmax, results, sizeof(int32_t) * nseq);
     if (nonfinite) std::memcpy(nonfinite, results + nseq, sizeof(int32_t) * nseq);
     ++h->stats.forward_calls;

@@ -66,8 +66,10 @@ hipError_t launch_gemm_normed(hipStream_t s, Epilogue epilogue, const GemmArgs& 
 // logit, from the kHead partials of `args`.
 hipError_t launch_head_argmax(hipStream_t s, const GemmArgs& args, int32_t* argmax, int32_t* nonfinite);
 
+// x = embedding rows of `tokens`; also clears the forward's device error
+// word `error` (may be null).
 hipError_t launch_embed(hipStream_t s, const float* embedding, const int32_t* tokens, float* x, int rows,
-                        int hidden);
+                        int hidden, int32_t* error);
 
 // out[r] = (x[r']*scale_r')*w with scale = 1/sqrt(sequential sum of squares/width + eps);
 // r' = row_map[r] when row_map is non-null, else r.
@@ -97,6 +99,9 @@ struct AttentionWork {
     float* scores;
     float* chunk_max;
     int stride, chunks;
+    // Device error word (set non-zero by a kernel that had to give up a
+    // bounded wait); cleared by launch_embed at the start of each forward.
+    int32_t* error;
 };
 int attention_row_block(int heads, int kv_heads, int dim);
 // Optional timing: `start` is recorded as the first kernel of a launch
@@ -126,9 +131,11 @@ hipError_t launch_attention_single(hipStream_t s, const float* q, const float* k
 // Score floats per row that fit in LDS.
 constexpr int kAttentionLdsScores = 10240;
 
-// Copies a strided region inside both pools (rows x width floats, pitch apart).
-hipError_t launch_copy_region(hipStream_t s, float* keys, float* values, uint64_t destination, uint64_t source,
-                              uint64_t pitch, uint64_t width, uint64_t rows);
+// Copy-on-write of a page's first `valid` token slots, layers 0..layers-1,
+// in both pools, in the device page order of layout.h. destination and
+// source are float offsets of (page, layer 0), multiples of a page-layer span.
+hipError_t launch_copy_tail(hipStream_t s, float* keys, float* values, uint64_t destination, uint64_t source,
+                            int layers, int valid, int block_tokens, int kv_heads, int dim);
 
 // tables[updates[i].x] = updates[i].y for i < count (queued block-table
 // entries; the indices are distinct).

@@ -15,7 +15,9 @@ namespace {
 // are zeroed so that later kernels only ever see finite values there.
 __global__ __launch_bounds__(256) void embed_kernel(const float* __restrict__ embedding,
                                                     const int32_t* __restrict__ tokens,
-                                                    float* __restrict__ x, int rows, int hidden) {
+                                                    float* __restrict__ x, int rows, int hidden,
+                                                    int32_t* __restrict__ error) {
+    if (error && blockIdx.x == 0 && threadIdx.x == 0) *error = 0;
     const int quads = hidden >> 2;
     const size_t total = (size_t)((rows + 63) >> 6) * quads * 64;
     float4* x4 = reinterpret_cast<float4*>(x);
@@ -203,20 +205,35 @@ __global__ void rope_append_kernel(float* __restrict__ qkv, int width, int heads
             qkv[quad_index(r, hidden + kv.kv_width + i, width)];
 }
 
-// Copies `rows` consecutive spans of `width` floats, `pitch` apart, in both
-// pools; float4 when everything is 16-byte aligned.
-__global__ void copy_region_kernel(float* keys, float* values, uint64_t destination, uint64_t source,
-                                   uint64_t pitch, uint64_t width) {
-    float* pool = blockIdx.y == 0 ? keys : values;
-    const uint64_t row = blockIdx.x;
-    float* dst = pool + destination + row * pitch;
-    const float* src = pool + source + row * pitch;
-    if (((destination | source | pitch | width) & 3) == 0) {
-        float4* d4 = reinterpret_cast<float4*>(dst);
-        const float4* s4 = reinterpret_cast<const float4*>(src);
-        for (uint64_t i = threadIdx.x; i < width / 4; i += blockDim.x) d4[i] = s4[i];
+// Copy-on-write of the first `valid` token slots of a page, every layer, in
+// both pools (block x = layer, block y = pool). In the device page order the
+// valid slots of a key page are, per (KV head, group of 4 dims), a run of
+// `valid` float4 (key_offset); those of a value page are, per KV head, the
+// first ceil(valid/4) groups of dim float4 (value_offset; the last group may
+// carry slots past the tail, which later appends overwrite before any read).
+// Offsets are float4 indices of the (page, layer 0) spans; `page4` is one
+// page-layer span in float4.
+__global__ void copy_tail_kernel(float4* keys, float4* values, uint64_t destination, uint64_t source,
+                                 uint32_t page4, int valid, int block_tokens, int kv_heads, int dim) {
+    const bool is_key = blockIdx.y == 0;
+    float4* pool = is_key ? keys : values;
+    const uint64_t layer = blockIdx.x;
+    float4* dst = pool + destination + layer * page4;
+    const float4* src = pool + source + layer * page4;
+    const int head4 = block_tokens * dim / 4;  // float4 per KV head in a page-layer span
+    if (is_key) {
+        const int runs = kv_heads * (dim / 4);  // runs of block_tokens float4, one per (head, 4 dims)
+        for (int i = threadIdx.x; i < runs * valid; i += blockDim.x) {
+            const int run = i / valid, slot = i % valid;
+            const int at = run * block_tokens + slot;
+            dst[at] = src[at];
+        }
     } else {
-        for (uint64_t i = threadIdx.x; i < width; i += blockDim.x) dst[i] = src[i];
+        const int per_head = (valid + 3) / 4 * dim;  // float4 of the valid slot groups of one head
+        for (int i = threadIdx.x; i < kv_heads * per_head; i += blockDim.x) {
+            const int at = (i / per_head) * head4 + i % per_head;
+            dst[at] = src[at];
+        }
     }
 }
 
@@ -244,11 +261,11 @@ __global__ void transpose_kernel(const float* __restrict__ src, float* __restric
 }  // namespace
 
 hipError_t launch_embed(hipStream_t s, const float* embedding, const int32_t* tokens, float* x, int rows,
-                        int hidden) {
+                        int hidden, int32_t* error) {
     if (rows <= 0) return hipSuccess;
     const size_t total = quad_floats(rows, hidden) / 4;
     const int blocks = (int)std::min<size_t>((total + 255) / 256, 4096);
-    embed_kernel<<<blocks, 256, 0, s>>>(embedding, tokens, x, rows, hidden);
+    embed_kernel<<<blocks, 256, 0, s>>>(embedding, tokens, x, rows, hidden, error);
     return hipGetLastError();
 }
 
@@ -269,10 +286,13 @@ hipError_t launch_rope_append(hipStream_t s, float* qkv, int width, int rows, in
     return hipGetLastError();
 }
 
-hipError_t launch_copy_region(hipStream_t s, float* keys, float* values, uint64_t destination, uint64_t source,
-                              uint64_t pitch, uint64_t width, uint64_t rows) {
-    if (!rows || !width) return hipSuccess;
-    copy_region_kernel<<<dim3((unsigned)rows, 2), 256, 0, s>>>(keys, values, destination, source, pitch, width);
+hipError_t launch_copy_tail(hipStream_t s, float* keys, float* values, uint64_t destination, uint64_t source,
+                            int layers, int valid, int block_tokens, int kv_heads, int dim) {
+    if (layers <= 0 || valid <= 0) return hipSuccess;
+    const uint32_t page4 = (uint32_t)(block_tokens * kv_heads * dim / 4);
+    copy_tail_kernel<<<dim3((unsigned)layers, 2), 256, 0, s>>>(
+        reinterpret_cast<float4*>(keys), reinterpret_cast<float4*>(values), destination / 4, source / 4, page4,
+        valid, block_tokens, kv_heads, dim);
     return hipGetLastError();
 }
 

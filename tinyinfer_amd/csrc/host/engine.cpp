@@ -1,23 +1,109 @@
-// Engine (reference semantics: miniprefix/src/engine/engine.cpp:13-140).
+// Engine with the observable behaviour of the reference
+// (miniprefix/src/engine/engine.cpp:13-140): the same admission, order of
+// runner calls, events, error messages and failure handling.
 //
-// With a StagedRunner the per-request loop of one step is kept, but each
-// append is staged (its KV transaction commits immediately, in plan order)
-// and the staged forwards run as one device batch. The batch is flushed
-// before any staged request could finish: finishing releases pages, and the
-// reference releases them before the next request's append reserves pages.
+// Design: one queue of unfinished jobs in submission order, whose first
+// `admitted_` entries are the admitted ones, and one executor that carries
+// out a step's appends in plan order. The executor either appends each
+// request at once (ModelRunner::append, the reference's loop) or, with a
+// StagedRunner and batching on, stages the appends and runs them as device
+// batches. A batch is run early when a later append must observe its
+// effects:
+//  - sampling a job that may finish releases its pages, which the next
+//    append's reservation must see (the per-request loop releases them
+//    before the next append);
+//  - a job that maps cached pages written by a queued forward (a prefix
+//    published earlier in the same step) must not read or copy them before
+//    that forward has written them.
 #include "miniprefix/engine.h"
+
+#include "staged_runner.h"
 
 #include <algorithm>
 #include <cmath>
 
 namespace miniprefix {
 namespace {
+
 SchedulerConfig scheduler_config(const EngineConfig& c) {
     if (c.max_batch_size < 1 || c.token_budget < 1 || c.prefill_chunk < 1)
         throw std::invalid_argument("invalid engine configuration");
     return {c.max_batch_size, c.token_budget, c.prefill_chunk};
 }
+
+TokenId greedy(const std::vector<float>& logits) {
+    return static_cast<TokenId>(std::max_element(logits.begin(), logits.end()) - logits.begin());
+}
+
 }  // namespace
+
+class Engine::Executor {
+public:
+    explicit Executor(Engine& engine)
+        : engine_(engine),
+          staged_(engine.batching_ ? dynamic_cast<StagedRunner*>(engine.runner_.get()) : nullptr) {}
+    ~Executor() {
+        if (staged_ && !queue_.empty()) staged_->discard_staged();  // unwinding
+    }
+
+    // After `job` mapped cached pages: they may hold tokens a queued forward
+    // has not written yet.
+    void mapped(const Job& job) {
+        if (staged_ && !queue_.empty() && staged_->shares_staged_pages(job.request.id)) run_queue();
+    }
+
+    void append(Job& job, const std::vector<TokenId>& input, bool prefill) {
+        ModelRunner& runner = *engine_.runner_;
+        const RequestId& id = job.request.id;
+        if (staged_) {
+            staged_->stage(id, input);
+            engine_.account(job, input.size(), prefill);
+            const bool samples = prompt_done(job);
+            queue_.push_back({&job, samples});
+            if (!samples) return;
+            runner.cache_prefix(id);
+            if (may_finish(job)) run_queue();
+            return;
+        }
+        const std::vector<float> logits = runner.append(id, input);
+        engine_.account(job, input.size(), prefill);
+        if (!prompt_done(job)) return;
+        if (logits.size() != static_cast<std::size_t>(runner.config().vocabulary))
+            throw std::runtime_error("invalid logits arity");
+        for (const float v : logits)
+            if (!std::isfinite(v)) throw std::runtime_error("nonfinite model result");
+        // Publish the committed history before sampling: the sampled token has no KV yet.
+        runner.cache_prefix(id);
+        engine_.emit_token(job, greedy(logits));
+    }
+
+    void run_queue() {
+        if (queue_.empty()) return;
+        const std::vector<StagedResult> results = staged_->run_staged();
+        std::vector<Queued> batch;
+        batch.swap(queue_);
+        if (results.size() != batch.size()) throw std::runtime_error("invalid staged result count");
+        for (std::size_t i = 0; i < batch.size(); ++i) {
+            if (!results[i].finite) throw std::runtime_error("nonfinite model result");
+            if (batch[i].samples) engine_.emit_token(*batch[i].job, results[i].argmax);
+        }
+    }
+
+private:
+    struct Queued {
+        Job* job;
+        bool samples;
+    };
+    static bool prompt_done(const Job& job) { return job.prefilled >= job.request.prompt_token_ids.size(); }
+    static bool may_finish(const Job& job) {
+        const GenerationOptions& g = job.request.generation;
+        return g.eos_token_id.has_value() || job.output.size() + 1 == g.max_new_tokens;
+    }
+
+    Engine& engine_;
+    StagedRunner* staged_;
+    std::vector<Queued> queue_;
+};
 
 Engine::Engine(std::unique_ptr<ModelRunner> runner, EngineConfig config)
     : runner_(std::move(runner)), config_(config), scheduler_(scheduler_config(config)) {
@@ -35,244 +121,182 @@ Engine::~Engine() {
 
 void Engine::submit(Request request) {
     if (failed_) throw std::runtime_error("engine failed; create a new engine");
-    const auto& p = request.prompt_token_ids;
-    if (request.id.empty() || seen_.count(request.id) || p.empty() || request.generation.max_new_tokens < 1 ||
-        p.size() + std::uint64_t(request.generation.max_new_tokens) > std::uint64_t(config_.context))
+    const std::vector<TokenId>& prompt = request.prompt_token_ids;
+    const std::uint64_t length = prompt.size() + std::uint64_t(request.generation.max_new_tokens);
+    if (request.id.empty() || seen_.count(request.id) || prompt.empty() || request.generation.max_new_tokens < 1 ||
+        length > std::uint64_t(config_.context))
         throw std::invalid_argument("invalid request, duplicate ID or context overflow");
     const int vocabulary = runner_->config().vocabulary;
-    for (const TokenId t : p)
-        if (t < 0 || t >= vocabulary) throw std::invalid_argument("invalid prompt token");
-    const auto& eos = request.generation.eos_token_id;
+    if (std::any_of(prompt.begin(), prompt.end(), [&](TokenId t) { return t < 0 || t >= vocabulary; }))
+        throw std::invalid_argument("invalid prompt token");
+    const std::optional<TokenId>& eos = request.generation.eos_token_id;
     if (eos && (*eos < 0 || *eos >= vocabulary)) throw std::invalid_argument("invalid EOS");
-    State state;
-    state.request = std::move(request);
-    seen_.insert(state.request.id);
-    waiting_.push_back(std::move(state));
+    seen_.insert(request.id);
+    Job job;
+    job.request = std::move(request);
+    jobs_.push_back(std::move(job));
 }
 
-void Engine::terminal(State& state, FinishReason reason, std::optional<TokenId> token, const std::string& error,
-                      TerminalCleanup cleanup) {
-    if (state.finished) return;
-    // Normal endings release the sequence; after a fatal error the runner's
-    // clear() owns cleanup, so no per-request release is attempted.
-    if (state.resident && cleanup == TerminalCleanup::ReleaseSequence) runner_->release(state.request.id);
-    runner_->release_reservation(state.request.id);
-    state.resident = false;
-    events_.push_back({state.request.id, token, reason, error});
-    state.finished = true;
+void Engine::finish(Job& job, FinishReason reason, std::optional<TokenId> token, const std::string& error,
+                    Cleanup cleanup) {
+    if (job.finished) return;
+    // After a fatal error the runner's clear() owns the sequences; otherwise
+    // the job's sequence is released first (a throw leaves it unfinished).
+    if (job.resident && cleanup == Cleanup::Release) runner_->release(job.request.id);
+    runner_->release_reservation(job.request.id);
+    job.resident = false;
+    events_.push_back({job.request.id, token, reason, error});
+    job.finished = true;
 }
 
-void Engine::remove_finished(bool include_waiting) {
-    const auto done = [](const State& s) { return s.finished; };
-    active_.erase(std::remove_if(active_.begin(), active_.end(), done), active_.end());
-    if (include_waiting) waiting_.erase(std::remove_if(waiting_.begin(), waiting_.end(), done), waiting_.end());
+void Engine::emit_token(Job& job, TokenId token) {
+    const GenerationOptions& g = job.request.generation;
+    job.output.push_back(token);
+    if (g.eos_token_id && token == *g.eos_token_id) finish(job, FinishReason::Eos, token);
+    else if (job.output.size() == g.max_new_tokens) finish(job, FinishReason::Length, token);
+    else events_.push_back({job.request.id, token, std::nullopt, {}});
 }
 
-void Engine::restore_prefix(State& state) {
-    const Request& request = state.request;
-    runner_->create(request.id);
-    state.resident = true;
-    const std::size_t reused = runner_->reuse_prefix(request.id, request.prompt_token_ids);
-    // The runner returns no cached logits: at least one prompt token must
-    // remain to append. A reusable prefix may end inside a page.
+void Engine::account(Job& job, std::size_t tokens, bool prefill) {
+    if (prefill) {
+        job.prefilled += tokens;
+        step_stats_.prefill_tokens += tokens;
+    } else {
+        step_stats_.decode_tokens += tokens;
+    }
+}
+
+void Engine::drop_finished() {
+    jobs_.erase(std::remove_if(jobs_.begin(), jobs_.end(), [](const Job& j) { return j.finished; }), jobs_.end());
+    admitted_ = static_cast<std::size_t>(std::count_if(jobs_.begin(), jobs_.end(), [](const Job& j) { return j.admitted; }));
+}
+
+void Engine::restore_prefix(Job& job) {
+    const Request& r = job.request;
+    runner_->create(r.id);
+    job.resident = true;
+    const std::size_t reused = runner_->reuse_prefix(r.id, r.prompt_token_ids);
+    // The runner keeps no logits: at least one prompt token must be left to
+    // append. A reusable prefix may end inside a page.
     const std::size_t block_tokens = runner_->stats().kv_block_tokens;
-    if (reused >= request.prompt_token_ids.size() || (reused && !block_tokens))
+    if (reused >= r.prompt_token_ids.size() || (reused && !block_tokens))
         throw std::runtime_error("invalid reusable prefix range");
-    state.kv_block_tokens = block_tokens;
-    state.prefilled = reused;
+    job.prefilled = reused;
     step_stats_.prefix_reused_tokens += reused;
 }
 
-void Engine::sample(State& s, TokenId token) {
-    const Request& r = s.request;
-    s.output.push_back(token);
-    std::optional<FinishReason> finish;
-    if (r.generation.eos_token_id && token == *r.generation.eos_token_id) finish = FinishReason::Eos;
-    else if (s.output.size() == r.generation.max_new_tokens) finish = FinishReason::Length;
-    if (finish) terminal(s, *finish, token);
-    else events_.push_back({r.id, token, std::nullopt, {}});
+bool Engine::admit() {
+    bool progressed = false;
+    std::size_t slots = scheduler_.admission_count(admitted_, jobs_.size() - admitted_);
+    while (slots && admitted_ < jobs_.size()) {
+        Job& job = jobs_[admitted_];
+        const Request& r = job.request;
+        // The last sampled token is delivered, never appended to the KV.
+        const std::size_t tokens = r.prompt_token_ids.size() + std::size_t(r.generation.max_new_tokens) - 1;
+        const KvAdmission admission = runner_->reserve_request(r.id, tokens);
+        if (admission == KvAdmission::Wait && admitted_) break;
+        progressed = true;
+        if (admission != KvAdmission::Ready) {
+            finish(job, FinishReason::Error, std::nullopt,
+                   admission == KvAdmission::Impossible ? "request exceeds total KV capacity"
+                                                        : "KV capacity unavailable without active requests to make progress");
+            jobs_.erase(jobs_.begin() + static_cast<std::ptrdiff_t>(admitted_));
+            continue;
+        }
+        job.admitted = true;
+        ++admitted_;
+        --slots;
+    }
+    return progressed;
 }
 
-void Engine::run_plan_sequential(SchedulePlan& plan) {
-    for (const auto& work : plan.order()) {
+void Engine::execute(SchedulePlan& plan) {
+    Executor executor(*this);
+    for (const ScheduledRequest& work : plan.order()) {
         if (!plan.has_budget()) break;
-        State& s = active_[work.active_index];
-        const Request& r = s.request;
+        Job& job = jobs_[work.active_index];
+        const std::vector<TokenId>& prompt = job.request.prompt_token_ids;
         try {
-            if (!s.resident) restore_prefix(s);
-            const bool prefilling = work.phase == SchedulePhase::Prefill;
-            const std::size_t count = plan.take_input(work.phase, r.prompt_token_ids.size() - s.prefilled);
-            std::vector<TokenId> input;
-            if (!prefilling) input = {s.output.back()};
-            else input.assign(r.prompt_token_ids.begin() + static_cast<std::ptrdiff_t>(s.prefilled),
-                              r.prompt_token_ids.begin() + static_cast<std::ptrdiff_t>(s.prefilled + count));
-            const std::vector<float> logits = runner_->append(r.id, input);
-            if (prefilling) {
-                s.prefilled += input.size();
-                step_stats_.prefill_tokens += input.size();
-            } else {
-                step_stats_.decode_tokens += input.size();
+            if (!job.resident) {
+                restore_prefix(job);
+                executor.mapped(job);
             }
-            if (s.prefilled < r.prompt_token_ids.size()) continue;
-            if (logits.size() != static_cast<std::size_t>(runner_->config().vocabulary))
-                throw std::runtime_error("invalid logits arity");
-            for (const float v : logits)
-                if (!std::isfinite(v)) throw std::runtime_error("nonfinite model result");
-            // Publish before sampling: the new output token has no KV yet.
-            runner_->cache_prefix(r.id);
-            sample(s, static_cast<TokenId>(std::max_element(logits.begin(), logits.end()) - logits.begin()));
+            const bool prefill = work.phase == SchedulePhase::Prefill;
+            const std::size_t count = plan.take_input(work.phase, prompt.size() - job.prefilled);
+            std::vector<TokenId> input;
+            if (prefill) {
+                const auto first = prompt.begin() + static_cast<std::ptrdiff_t>(job.prefilled);
+                input.assign(first, first + static_cast<std::ptrdiff_t>(count));
+            } else {
+                input.push_back(job.output.back());
+            }
+            executor.append(job, input, prefill);
         } catch (const KvCapacityError& error) {
-            terminal(s, FinishReason::Error, std::nullopt, error.what());
+            // Request-scoped: earlier requests' results come first, as in
+            // the per-request loop.
+            executor.run_queue();
+            finish(job, FinishReason::Error, std::nullopt, error.what());
         }
     }
+    executor.run_queue();
 }
 
-void Engine::run_plan_staged(SchedulePlan& plan, StagedRunner& staged) {
-    struct Item {
-        std::size_t index;
-        bool samples;
-    };
-    std::vector<Item> items;
-    auto flush = [&]() {
-        if (items.empty()) return;
-        const std::vector<StagedResult> results = staged.run_staged();
-        if (results.size() != items.size()) throw std::runtime_error("invalid staged result count");
-        for (std::size_t i = 0; i < items.size(); ++i) {
-            if (!results[i].finite) throw std::runtime_error("nonfinite model result");
-            if (items[i].samples) sample(active_[items[i].index], results[i].argmax);
-        }
-        items.clear();
-    };
+void Engine::fail_all(const std::string& cause) {
+    // Poison first: the runner's ownership must survive a failed cleanup.
+    failed_ = true;
+    std::string message = cause;
     try {
-        for (const auto& work : plan.order()) {
-            if (!plan.has_budget()) break;
-            State& s = active_[work.active_index];
-            const Request& r = s.request;
-            try {
-                if (!s.resident) restore_prefix(s);
-                const bool prefilling = work.phase == SchedulePhase::Prefill;
-                const std::size_t count = plan.take_input(work.phase, r.prompt_token_ids.size() - s.prefilled);
-                std::vector<TokenId> input;
-                if (!prefilling) input = {s.output.back()};
-                else input.assign(r.prompt_token_ids.begin() + static_cast<std::ptrdiff_t>(s.prefilled),
-                                  r.prompt_token_ids.begin() + static_cast<std::ptrdiff_t>(s.prefilled + count));
-                staged.stage(r.id, input);
-                if (prefilling) {
-                    s.prefilled += input.size();
-                    step_stats_.prefill_tokens += input.size();
-                } else {
-                    step_stats_.decode_tokens += input.size();
-                }
-                const bool samples = s.prefilled >= r.prompt_token_ids.size();
-                items.push_back({work.active_index, samples});
-                if (!samples) continue;
-                runner_->cache_prefix(r.id);
-                // A request that may finish now releases its pages when
-                // sampled; later appends must see that release first.
-                const bool may_finish = r.generation.eos_token_id.has_value() ||
-                                        s.output.size() + 1 == r.generation.max_new_tokens;
-                if (may_finish) flush();
-            } catch (const KvCapacityError& error) {
-                // Deliver the events of earlier staged requests first, so the
-                // event order is the reference's plan order.
-                flush();
-                terminal(s, FinishReason::Error, std::nullopt, error.what());
-            }
-        }
-        flush();
+        runner_->clear();
+    } catch (const std::exception& cleanup) {
+        message += "; cleanup failed: ";
+        message += cleanup.what();
     } catch (...) {
-        staged.discard_staged();
-        throw;
+        message += "; cleanup failed: unknown exception";
     }
+    for (Job& job : jobs_) finish(job, FinishReason::Error, std::nullopt, message, Cleanup::RunnerOwned);
+    drop_finished();
 }
 
 bool Engine::step() {
     step_stats_ = {};
     if (failed_) throw std::runtime_error("engine failed");
-    bool progressed = false;
     try {
-        std::size_t slots = scheduler_.admission_count(active_.size(), waiting_.size());
-        while (slots && !waiting_.empty()) {
-            State& state = waiting_.front();
-            const Request& request = state.request;
-            // The final sampled token is delivered, never appended to KV.
-            const std::size_t tokens =
-                request.prompt_token_ids.size() + std::size_t(request.generation.max_new_tokens) - 1;
-            const KvAdmission admission = runner_->reserve_request(request.id, tokens);
-            if (admission == KvAdmission::Wait && !active_.empty()) break;
-            if (admission != KvAdmission::Ready) {
-                terminal(state, FinishReason::Error, std::nullopt,
-                         admission == KvAdmission::Impossible
-                             ? "request exceeds total KV capacity"
-                             : "KV capacity unavailable without active requests to make progress");
-                waiting_.pop_front();
-                progressed = true;
-                continue;
-            }
-            active_.push_back(std::move(state));
-            waiting_.pop_front();
-            --slots;
-            progressed = true;
-        }
-        if (active_.empty()) return progressed;
-        std::vector<SchedulePhase> phases;
-        phases.reserve(active_.size());
-        for (const State& s : active_) phases.push_back(s.output.empty() ? SchedulePhase::Prefill : SchedulePhase::Decode);
+        const bool progressed = admit();
+        if (!admitted_) return progressed;
+        std::vector<SchedulePhase> phases(admitted_);
+        for (std::size_t i = 0; i < admitted_; ++i)
+            phases[i] = jobs_[i].output.empty() ? SchedulePhase::Prefill : SchedulePhase::Decode;
         SchedulePlan plan = scheduler_.plan(phases);
-        StagedRunner* staged = batching_ ? dynamic_cast<StagedRunner*>(runner_.get()) : nullptr;
-        if (staged) run_plan_staged(plan, *staged);
-        else run_plan_sequential(plan);
-        remove_finished();
+        execute(plan);
+        drop_finished();
     } catch (const std::exception& error) {
-        // Poison first: backend ownership must survive a failed cleanup.
-        failed_ = true;
-        std::string message = error.what();
-        try {
-            runner_->clear();
-        } catch (const std::exception& cleanup) {
-            message += "; cleanup failed: ";
-            message += cleanup.what();
-        } catch (...) {
-            message += "; cleanup failed: unknown exception";
-        }
-        for (State& s : active_) terminal(s, FinishReason::Error, std::nullopt, message, TerminalCleanup::RunnerManaged);
-        for (State& s : waiting_) terminal(s, FinishReason::Error, std::nullopt, message, TerminalCleanup::RunnerManaged);
-        remove_finished(true);
+        fail_all(error.what());
     }
     return true;
 }
 
 std::vector<GenerationEvent> Engine::poll_events() {
-    std::vector<GenerationEvent> out = std::move(events_);
-    events_.clear();
+    std::vector<GenerationEvent> out;
+    out.swap(events_);
     return out;
 }
 
 void Engine::cancel(const RequestId& id) {
-    for (State& s : waiting_)
-        if (s.request.id == id && !s.finished) {
-            terminal(s, FinishReason::Cancelled);
-            remove_finished(true);
-            return;
-        }
-    for (State& s : active_)
-        if (s.request.id == id && !s.finished) {
-            terminal(s, FinishReason::Cancelled);
-            remove_finished();
-            return;
-        }
-    throw std::invalid_argument("request is unknown or already terminal");
+    const auto it = std::find_if(jobs_.begin(), jobs_.end(),
+                                 [&](const Job& j) { return !j.finished && j.request.id == id; });
+    if (it == jobs_.end()) throw std::invalid_argument("request is unknown or already terminal");
+    finish(*it, FinishReason::Cancelled);
+    drop_finished();
 }
 
 void Engine::shutdown() {
     try {
-        for (State& s : active_) terminal(s, FinishReason::Cancelled);
-        for (State& s : waiting_) terminal(s, FinishReason::Cancelled);
+        for (Job& job : jobs_) finish(job, FinishReason::Cancelled);
     } catch (...) {
-        remove_finished(true);
+        drop_finished();
         throw;
     }
-    remove_finished(true);
+    drop_finished();
     runner_->clear();
 }
 

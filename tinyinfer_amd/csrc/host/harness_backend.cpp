@@ -23,15 +23,15 @@ bool weights_tensor(const miniprefix::ModelWeights& weights, const std::string& 
                     std::size_t* count) {
     const auto it = weights.tensors.find(name);
     if (it == weights.tensors.end()) return false;
-    *data = it->second.data.data();
-    *count = it->second.data.size();
+    *data = it->second.values.data();
+    *count = it->second.values.size();
     return true;
 }
 
 bool weights_set(miniprefix::ModelWeights& weights, const std::string& name, const float* data, std::size_t count) {
     const auto it = weights.tensors.find(name);
-    if (it == weights.tensors.end() || it->second.data.size() != count) return false;
-    std::memcpy(it->second.data.data(), data, count * sizeof(float));
+    if (it == weights.tensors.end() || it->second.values.size() != count) return false;
+    std::memcpy(it->second.values.data(), data, count * sizeof(float));
     return true;
 }
 

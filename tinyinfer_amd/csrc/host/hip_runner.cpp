@@ -1,17 +1,28 @@
 // HipRunner: the ModelRunner over the device backend's C ABI (include/mp_hip.h).
-// It owns one KVManager exactly as the reference's CudaRunner does
-// (miniprefix/src/backend/cuda/llama_runner.cu:51-186) and keeps the same
+// It owns one KVManager, as the reference's CudaRunner does
+// (miniprefix/src/backend/cuda/llama_runner.cu:51-186), and keeps its
 // transaction discipline: prepare, copy the shared tail, upload new table
 // entries, forward, synchronize, check, then commit -- or roll back and mark
-// the device table dirty. It also implements StagedRunner: the transaction
-// commits at stage() time and run_staged() computes all queued forwards in
-// one device pass.
+// the device table dirty.
+//
+// It also implements StagedRunner (staged_runner.h): stage() commits the
+// transaction and queues the forward; run_staged() computes the queued
+// forwards in one device pass.
+//
+// The file builds against this repository's headers and, unchanged, against
+// the reference's (miniprefix/include/miniprefix/model.h, with weights held
+// as tinyinfer::Tensor): it uses only the reference's ModelRunner, KVManager
+// and ModelWeights interfaces, reads tensors through numel() and data<float>(),
+// and brings its own extension header.
 #include "miniprefix/model.h"
-#include "mp_hip.h"
 
-#include <cmath>
+#include "mp_hip.h"
+#include "staged_runner.h"
+
+#include <map>
 #include <stdexcept>
 #include <string>
+#include <vector>
 
 namespace miniprefix {
 namespace {
@@ -23,10 +34,10 @@ public:
           kv_(kv, config().layers, config().kv_width(), context, config().vocabulary) {
         if (context < 1 || context > config().context) throw std::invalid_argument("invalid runner context");
         const ModelConfig& c = config();
-        mp_model_desc m{c.layers, c.hidden, c.intermediate, c.heads, c.kv_heads, c.vocabulary, context,
-                        c.rms_epsilon, c.rope_theta, c.tied ? 1 : 0};
+        const mp_model_desc m{c.layers, c.hidden, c.intermediate, c.heads, c.kv_heads, c.vocabulary, context,
+                              c.rms_epsilon, c.rope_theta, c.tied ? 1 : 0};
         table_entries_ = static_cast<int>(kv_.max_sequence_blocks());
-        mp_kv_desc d{kv.block_tokens, kv.max_blocks, kMaxSequences, table_entries_};
+        const mp_kv_desc d{kv.block_tokens, kv.max_blocks, kMaxSequences, table_entries_};
         const int status = mp_hip_create(&m, &d, &device_);
         if (status) throw std::runtime_error("create HIP backend: status " + std::to_string(status));
         try {
@@ -36,6 +47,7 @@ public:
             throw;
         }
         for (int s = kMaxSequences - 1; s >= 0; --s) free_slots_.push_back(s);
+        staged_writes_.assign(static_cast<std::size_t>(kv.max_blocks), 0);
     }
     ~HipRunner() override {
         if (device_) mp_hip_destroy(device_);
@@ -68,17 +80,15 @@ public:
     void fork_sequence(const RequestId& source, const RequestId& target) override {
         sync("fork completion");
         kv_.fork_sequence(source, target);
-        tables_.at(target).dirty = true;  // published on the next append
+        tables_.at(target).dirty = true;  // written whole by the next append
     }
     std::size_t reuse_prefix(const RequestId& id, const std::vector<TokenId>& prompt) override {
         const std::size_t used = kv_.reuse_prefix(id, prompt);
         if (used) {
-            const PagedSequence& s = kv_.sequence(id);
             try {
-                upload_table(tables_.at(id).slot, 0, s);
-                sync("prefix table completion");
+                // Queued; the next forward applies the entries before any kernel reads them.
+                write_table(tables_.at(id).slot, 0, kv_.sequence(id));
             } catch (...) {
-                mp_hip_sync(device_);
                 kv_.reset_sequence(id);
                 throw;
             }
@@ -94,13 +104,12 @@ public:
     std::vector<float> append(const RequestId& id, const std::vector<TokenId>& tokens) override {
         if (!staged_.empty()) throw std::logic_error("append while forwards are staged");
         auto tx = kv_.prepare_append(id, tokens);
-        const PagedSequence& s = tx.sequence();
         Table& table = tables_.at(id);
-        const int used = s.used;
+        const int used = tx.sequence().used;
         std::vector<float> logits(static_cast<std::size_t>(config().vocabulary));
         try {
             copy_tail(tx);
-            upload_new_entries(tx, table);
+            write_new_entries(tx, table);
             const mp_seq_step step{table.slot, used, static_cast<std::int32_t>(tokens.size())};
             std::int32_t argmax = 0, nonfinite = 0;
             const int status = mp_hip_forward(device_, &step, 1, tokens.data(), logits.data(), &argmax, &nonfinite);
@@ -120,15 +129,28 @@ public:
     void stage(const RequestId& id, const std::vector<TokenId>& tokens) override {
         auto tx = kv_.prepare_append(id, tokens);
         Table& table = tables_.at(id);
-        const int used = tx.sequence().used;
+        const PagedSequence& s = tx.sequence();
+        const int used = s.used;
         try {
+            if (tx.tail_copy() && staged_writes_[static_cast<std::size_t>(tx.tail_copy()->source)])
+                throw std::logic_error("copy-on-write source holds tokens of a queued forward");
             copy_tail(tx);
-            upload_new_entries(tx, table);
+            write_new_entries(tx, table);
         } catch (...) {
             mp_hip_sync(device_);
             table.dirty = true;
             tx.rollback();
             throw;
+        }
+        // The pages this forward writes: those of positions used..used+n-1.
+        const int bt = kv_.config().block_tokens;
+        const int last = (used + static_cast<int>(tokens.size()) - 1) / bt;
+        for (int p = used / bt; p <= last; ++p) {
+            const int block = s.blocks[static_cast<std::size_t>(p)];
+            if (!staged_writes_[static_cast<std::size_t>(block)]) {
+                staged_writes_[static_cast<std::size_t>(block)] = 1;
+                written_.push_back(block);
+            }
         }
         tx.commit();
         table.dirty = false;
@@ -141,8 +163,7 @@ public:
         std::vector<std::int32_t> argmax(staged_.size()), nonfinite(staged_.size());
         const int status = mp_hip_forward(device_, staged_.data(), static_cast<std::int32_t>(staged_.size()),
                                           staged_tokens_.data(), nullptr, argmax.data(), nonfinite.data());
-        staged_.clear();
-        staged_tokens_.clear();
+        discard_staged();
         if (status != MP_OK && status != MP_NONFINITE) check(status, "model forward");
         for (std::size_t i = 0; i < results.size(); ++i) results[i] = {argmax[i], nonfinite[i] == 0};
         return results;
@@ -150,6 +171,14 @@ public:
     void discard_staged() noexcept override {
         staged_.clear();
         staged_tokens_.clear();
+        for (const int block : written_) staged_writes_[static_cast<std::size_t>(block)] = 0;
+        written_.clear();
+    }
+    bool shares_staged_pages(const RequestId& id) const override {
+        if (written_.empty() || !kv_.contains(id)) return false;
+        for (const int block : kv_.sequence(id).blocks)
+            if (staged_writes_[static_cast<std::size_t>(block)]) return true;
+        return false;
     }
 
     void release(const RequestId& id) override {
@@ -165,7 +194,7 @@ public:
         tables_.clear();
     }
     RunnerStats stats() const override {
-        RunnerStats r = stats_;
+        RunnerStats r;
         mp_hip_counters c{};
         mp_hip_stats(device_, &c);
         r.device_weight_bytes = c.device_weight_bytes;
@@ -200,8 +229,8 @@ private:
     void upload_weights() {
         const ModelConfig& c = config();
         auto put = [&](int layer, int slot, const std::string& name) {
-            const HostTensor& t = weights_->get(name);
-            check(mp_hip_upload_tensor(device_, layer, slot, t.data.data(), t.data.size()), "upload weights");
+            const auto& t = weights_->get(name);
+            check(mp_hip_upload_tensor(device_, layer, slot, t.template data<float>(), t.numel()), "upload weights");
         };
         put(-1, MP_TENSOR_EMBEDDING, "model.embed_tokens.weight");
         put(-1, MP_TENSOR_FINAL_NORM, "model.norm.weight");
@@ -214,18 +243,18 @@ private:
                 put(l, j, "model.layers." + std::to_string(l) + "." + kSlots[j] + ".weight");
     }
 
-    void upload_table(int slot, std::size_t first, const PagedSequence& s) {
+    void write_table(int slot, std::size_t first, const PagedSequence& s) {
         if (s.blocks.size() <= first) return;
         check(mp_hip_table_write(device_, slot, static_cast<std::int32_t>(first), s.blocks.data() + first,
                                  static_cast<std::int32_t>(s.blocks.size() - first)),
               "upload block table entries");
     }
 
-    // New entries only; after a COW swap the swapped slot too; all when dirty.
-    void upload_new_entries(const KVManager::Append& tx, const Table& table) {
+    // New entries only; after a COW swap the swapped entry too; all when dirty.
+    void write_new_entries(const KVManager::Append& tx, const Table& table) {
         const std::size_t original = tx.original_blocks();
         const std::size_t first = table.dirty ? 0 : (tx.tail_copy() ? original - 1 : original);
-        upload_table(table.slot, first, tx.sequence());
+        write_table(table.slot, first, tx.sequence());
     }
 
     void copy_tail(KVManager::Append& tx) {
@@ -259,7 +288,8 @@ private:
     std::vector<int> free_slots_;
     std::vector<mp_seq_step> staged_;
     std::vector<TokenId> staged_tokens_;
-    RunnerStats stats_;
+    std::vector<char> staged_writes_;  // per block: written by a queued forward
+    std::vector<int> written_;         // the blocks marked in staged_writes_
     CostStats costs_;
     bool cost_timing_ = false;
 };

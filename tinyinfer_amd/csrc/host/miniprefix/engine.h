@@ -1,7 +1,8 @@
-// Request lifecycle over a ModelRunner (reference:
+// Request lifecycle over a ModelRunner (reference interface:
 // miniprefix/include/miniprefix/engine.h:8-36). When the runner also
-// implements StagedRunner, every step's appends go to the device as one
-// batch; the KV metadata sequence and the emitted events are unchanged.
+// implements StagedRunner, a step's appends go to the device as batches;
+// the KV metadata sequence and the emitted events are those of the
+// per-request loop.
 #pragma once
 #include "model.h"
 #include "scheduler.h"
@@ -26,7 +27,7 @@ public:
     std::vector<GenerationEvent> poll_events();
     void cancel(const RequestId&);
     void shutdown();
-    bool idle() const { return active_.empty() && waiting_.empty(); }
+    bool idle() const { return jobs_.empty(); }
     bool failed() const { return failed_; }
     ModelRunner& runner() { return *runner_; }
     const EngineStepStats& last_step_stats() const { return step_stats_; }
@@ -34,26 +35,32 @@ public:
     void set_batching(bool enabled) { batching_ = enabled; }
 
 private:
-    struct State {
+    struct Job {
         Request request;
-        std::size_t prefilled = 0, kv_block_tokens = 0;
+        std::size_t prefilled = 0;  // prompt tokens with committed KV
         std::vector<TokenId> output;
-        bool resident = false, finished = false;
+        bool admitted = false, resident = false, finished = false;
     };
-    enum class TerminalCleanup { ReleaseSequence, RunnerManaged };
-    void restore_prefix(State&);
-    void terminal(State&, FinishReason, std::optional<TokenId> token = std::nullopt,
-                  const std::string& error = "", TerminalCleanup cleanup = TerminalCleanup::ReleaseSequence);
-    void remove_finished(bool include_waiting = false);
-    void sample(State& s, TokenId token);
-    void run_plan_sequential(SchedulePlan& plan);
-    void run_plan_staged(SchedulePlan& plan, StagedRunner& staged);
+    class Executor;
+    enum class Cleanup { Release, RunnerOwned };
+
+    bool admit();
+    void execute(SchedulePlan& plan);
+    void restore_prefix(Job& job);
+    void finish(Job& job, FinishReason reason, std::optional<TokenId> token = std::nullopt,
+                const std::string& error = "", Cleanup cleanup = Cleanup::Release);
+    void emit_token(Job& job, TokenId token);
+    void account(Job& job, std::size_t tokens, bool prefill);
+    void drop_finished();
+    void fail_all(const std::string& message);
 
     std::unique_ptr<ModelRunner> runner_;
     EngineConfig config_;
     Scheduler scheduler_;
-    std::deque<State> waiting_;
-    std::vector<State> active_;
+    // Unfinished requests in submission order. Admission takes the oldest
+    // waiting request, so the admitted ones are always the first `admitted_`.
+    std::deque<Job> jobs_;
+    std::size_t admitted_ = 0;
     std::set<RequestId> seen_;
     std::vector<GenerationEvent> events_;
     bool failed_ = false;

@@ -1,5 +1,5 @@
 // Sequence metadata, page references, prefix leases, reservations and the
-// single open append transaction (reference:
+// single open append transaction (reference interface:
 // miniprefix/include/miniprefix/kv_manager.h:10-96). Payload, device tables
 // and completion stay in the backend. Single-threaded.
 #pragma once
@@ -21,9 +21,13 @@ struct KvStats {
 };
 
 class KVManager {
-    struct State {
-        PagedSequence sequence;
+    // Everything known about one request id: its page reservation and/or
+    // its sequence.
+    struct Entry {
+        std::optional<std::size_t> reservation;  // worst-case pages
+        bool live = false;                       // a sequence exists
         bool appending = false;
+        PagedSequence sequence;
     };
 
 public:
@@ -49,8 +53,8 @@ public:
         Append& operator=(Append&&) = delete;
         ~Append();
         const PagedSequence& sequence() const;
-        std::size_t original_blocks() const { return original_blocks_; }
-        const std::optional<TailCopy>& tail_copy() const { return copy_; }
+        std::size_t original_blocks() const { return blocks_before_; }
+        const std::optional<TailCopy>& tail_copy() const { return cow_; }
         // One call per layer row; the copier copies BOTH K and V.
         void copy_shared_tail(const std::function<void(std::size_t, std::size_t, std::size_t)>& copier);
         // One call for the strided region; the copier copies BOTH K and V.
@@ -59,12 +63,12 @@ public:
         void rollback() noexcept;
 
     private:
-        KVManager* owner_;
-        State* state_;
-        std::vector<TokenId> tokens_;
-        std::size_t original_blocks_;
-        std::optional<TailCopy> copy_;
-        bool copied_ = false;
+        KVManager* manager_;  // null once finished
+        Entry* entry_;
+        std::vector<TokenId> input_;
+        std::size_t blocks_before_;
+        std::optional<TailCopy> cow_;
+        bool cow_done_ = false;
     };
 
     KVManager(KvCacheConfig config, int layers, int width, int context, int vocabulary);
@@ -75,13 +79,13 @@ public:
     int context_limit() const { return context_; }
     std::size_t reserved_bytes() const { return pool_.reserved_bytes(); }
     std::size_t max_sequence_blocks() const;
-    bool contains(const RequestId& id) const { return sequences_.count(id) != 0; }
-    const PagedSequence& sequence(const RequestId& id) const { return sequences_.at(id).sequence; }
+    bool contains(const RequestId& id) const;
+    const PagedSequence& sequence(const RequestId& id) const;
     std::size_t offset(const PagedSequence& sequence, int layer, int token) const {
         return pool_.offset(sequence, layer, token, layers_, width_);
     }
     KvAdmission reserve_request(const RequestId& id, std::size_t max_tokens);
-    void release_reservation(const RequestId& id) noexcept { reservations_.erase(id); }
+    void release_reservation(const RequestId& id) noexcept;
     void create(const RequestId& id);
     void fork_sequence(const RequestId& source, const RequestId& target);
     std::size_t reuse_prefix(const RequestId& id, const std::vector<TokenId>& prompt);
@@ -98,19 +102,25 @@ public:
     CostStats cost_stats() const { return costs_; }
 
 private:
-    void require_idle() const;
-    State& idle_state(const RequestId& id);
-    void validate_tokens(const std::vector<TokenId>& tokens) const;
-    std::size_t committed_blocks() const;
-    void reserve_pages(const RequestId& id, PagedSequence& sequence, int end, bool& cow);
+    void require_no_append() const;
+    const Entry& live_entry(const RequestId& id) const;
+    Entry& idle_sequence(const RequestId& id);
+    void check_tokens(const std::vector<TokenId>& tokens, const char* message) const;
+    std::size_t pages_for(std::size_t tokens) const;
+    // Pages held against the pool's capacity: every reservation plus the
+    // blocks of sequences without one. Kept as two running sums.
+    std::size_t committed_pages() const { return reserved_pages_ + unreserved_blocks_; }
+    // Updates the running sum after `entry`'s block count changed from `before`.
+    void recount(const Entry& entry, std::size_t before) noexcept;
+    void make_room(Entry& entry, int end, bool& cow);
 
     int layers_, width_, context_, vocabulary_;
     KvBlockPool pool_;
     ExactPrefixCache prefix_;
-    std::map<RequestId, State> sequences_;
-    std::map<RequestId, std::size_t> reservations_;
+    std::map<RequestId, Entry> entries_;  // by id: clear() releases in id order
+    std::size_t reservations_ = 0, reserved_pages_ = 0, unreserved_blocks_ = 0;
     std::size_t forward_tokens_ = 0;
-    bool append_active_ = false;
+    bool append_open_ = false;
     bool cost_timing_ = false;
     CostStats costs_;
 };

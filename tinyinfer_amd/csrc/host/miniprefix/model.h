@@ -1,13 +1,13 @@
 // Model description, weights and the runner interface (reference:
 // miniprefix/include/miniprefix/model.h:9-62). ModelRunner is the drop-in
-// boundary: unchanged names, signatures and defaults. StagedRunner is an
-// additive, optional extension for cross-request batching.
+// boundary: unchanged names, signatures and defaults.
 #pragma once
 #include "kv_manager.h"
 #include "request.h"
 #include <map>
 #include <memory>
 #include <string>
+#include <type_traits>
 
 namespace miniprefix {
 
@@ -20,11 +20,23 @@ struct ModelConfig {
     void validate() const;
 };
 
-// Row-major FP32 host tensor.
+// Row-major FP32 host tensor. Its element accessors have the names and
+// meaning of tinyinfer::Tensor's (include/tinyinfer/core/tensor.h:46-53), so
+// code that reads weights through them builds against either weight type.
 struct HostTensor {
     std::vector<std::int64_t> shape;
-    std::vector<float> data;
-    std::size_t numel() const { return data.size(); }
+    std::vector<float> values;
+    std::size_t numel() const { return values.size(); }
+    template <class T>
+    const T* data() const {
+        static_assert(std::is_same<T, float>::value, "FP32 tensor");
+        return values.data();
+    }
+    template <class T>
+    T* data() {
+        static_assert(std::is_same<T, float>::value, "FP32 tensor");
+        return values.data();
+    }
 };
 
 struct ModelWeights {
@@ -68,25 +80,6 @@ public:
     virtual RunnerStats stats() const = 0;
     virtual CostStats cost_stats() const { return {}; }
     virtual void set_cost_timing(bool) {}
-};
-
-// Optional cross-request batching. stage() performs an append's KV
-// transaction (reservation, copy-on-write, commit) immediately, in call
-// order, and queues its forward; run_staged() computes every queued forward
-// in one device pass and returns, per staged item in order, the greedy
-// argmax of its last row (std::max_element semantics) and whether all of
-// its logits were finite. Because metadata commits before compute, a
-// non-finite result cannot be rolled back: callers treat it as fatal.
-struct StagedResult {
-    TokenId argmax = 0;
-    bool finite = true;
-};
-class StagedRunner {
-public:
-    virtual ~StagedRunner() = default;
-    virtual void stage(const RequestId& id, const std::vector<TokenId>& tokens) = 0;
-    virtual std::vector<StagedResult> run_staged() = 0;
-    virtual void discard_staged() noexcept = 0;
 };
 
 // Device backend over the C ABI of include/mp_hip.h.

@@ -93,10 +93,10 @@ std::shared_ptr<ModelWeights> ModelWeights::load(const std::string& path) {
         const auto offset = static_cast<std::uint64_t>(file.tellg());
         if (bytes != elements * sizeof(float) || offset > file_bytes || bytes > file_bytes - offset)
             throw std::runtime_error("invalid tensor bytes");
-        tensor.data.resize(elements);
-        if (!file.read(reinterpret_cast<char*>(tensor.data.data()), static_cast<std::streamsize>(bytes)))
+        tensor.values.resize(elements);
+        if (!file.read(reinterpret_cast<char*>(tensor.values.data()), static_cast<std::streamsize>(bytes)))
             throw std::runtime_error("truncated tensor");
-        for (const float v : tensor.data)
+        for (const float v : tensor.values)
             if (!std::isfinite(v)) throw std::runtime_error("nonfinite weights");
         model->tensors.emplace(name, std::move(tensor));
     }
@@ -117,9 +117,9 @@ std::shared_ptr<ModelWeights> ModelWeights::synthetic(const ModelConfig& c, std:
         t.shape = shapes.at(name);
         std::size_t n = 1;
         for (const auto d : t.shape) n *= static_cast<std::size_t>(d);
-        t.data.resize(n);
-        if (ones) std::fill(t.data.begin(), t.data.end(), 1.0f);
-        else synthetic::normal(t.data.data(), n, seed, stream, stddev);
+        t.values.resize(n);
+        if (ones) std::fill(t.values.begin(), t.values.end(), 1.0f);
+        else synthetic::normal(t.values.data(), n, seed, stream, stddev);
         model->tensors.emplace(name, std::move(t));
     };
     // Stream ids: embedding 0, final norm 1, layer l slot j -> 2 + 9l + j,

@@ -1,183 +1,271 @@
-// Exact prefix cache (reference semantics: miniprefix/src/kv/prefix_cache.cpp:8-198).
+// Exact prefix cache with the observable behaviour of the reference
+// (miniprefix/src/kv/prefix_cache.cpp:8-198).
 //
-// Each trie node stands for one page of tokens below its parent's path; the
-// final edge of a path may be shorter than a page. A node may hold one cache
-// lease on the physical page that stores its tokens. Nodes with a lease sit
-// in an LRU list and in their parent's ordered index of leased children,
-// which answers "longest common prefix with this query page" from the two
-// lexicographic neighbours of the query. Observable choices that feed the
-// page allocator follow the reference exactly: eviction is strict LRU,
-// clear() releases leases in lexicographic pre-order, ties on reuse prefer
-// the lower_bound neighbour.
+// Storage: nodes live in one vector and refer to each other by index. A
+// node's children are a vector sorted by edge (lexicographic token order),
+// and the children that hold a lease form a second sorted vector. Recency
+// is a use counter per leased node plus an ordered index from counter to
+// node, so the least recently used lease is the first entry of the index.
+//
+// The choices that decide which physical blocks a sequence receives, and
+// therefore must match the reference exactly:
+//  - reuse walks from the root one page at a time; at each level the leased
+//    child with the longest common prefix with the query page is one of the
+//    two leased children next to the query's position in sorted order, and
+//    on equal length the one at or after that position wins (:118-137); a
+//    match shorter than a page ends the walk;
+//  - a reuse match and a publish of an already leased page count as uses,
+//    in walk order; eviction takes strictly the least recently used lease;
+//  - publishing an unleased page takes its block reference before evicting
+//    for room, and the page being published is never the victim (:176-192);
+//  - clear() releases leases in lexicographic pre-order of the tree
+//    (:104-110), which fixes the pool's free-list order afterwards.
 #include "miniprefix/prefix_cache.h"
 
 #include <algorithm>
-#include <iterator>
 #include <map>
 
 namespace miniprefix {
 namespace {
 
-struct Span {
-    const std::int32_t* begin;
-    const std::int32_t* end;
-};
-inline Span span_of(const std::vector<std::int32_t>& v) { return {v.data(), v.data() + v.size()}; }
-inline Span span_of(const std::vector<std::int32_t>* v) { return span_of(*v); }
-inline Span span_of(const Span& s) { return s; }
+using Edge = std::vector<std::int32_t>;
 
-// Lexicographic order over token runs, usable with spans and vectors.
-struct TokenOrder {
-    using is_transparent = void;
-    template <class A, class B>
-    bool operator()(const A& a, const B& b) const {
-        const Span x = span_of(a), y = span_of(b);
-        return std::lexicographical_compare(x.begin, x.end, y.begin, y.end);
-    }
-};
+bool run_less(const std::int32_t* a, std::size_t na, const std::int32_t* b, std::size_t nb) {
+    return std::lexicographical_compare(a, a + na, b, b + nb);
+}
+
+std::size_t common_prefix(const Edge& edge, const std::int32_t* query, std::size_t n) {
+    const std::size_t limit = std::min(edge.size(), n);
+    std::size_t i = 0;
+    while (i < limit && edge[i] == query[i]) ++i;
+    return i;
+}
 
 }  // namespace
 
-struct ExactPrefixCache::Trie {
+class ExactPrefixCache::Tree {
+public:
+    static constexpr int kRoot = 0;
+    static constexpr int kNone = -1;
+
+private:
     struct Node {
-        Node* parent = nullptr;
-        const std::vector<std::int32_t>* edge = nullptr;  // key in parent->children
-        std::map<std::vector<std::int32_t>, std::unique_ptr<Node>, TokenOrder> children;
-        std::map<const std::vector<std::int32_t>*, Node*, TokenOrder> leased;
-        int block = -1;
-        Node* older = nullptr;
-        Node* newer = nullptr;
+        int parent = kNone;
+        Edge edge;
+        std::vector<int> children;  // sorted by edge
+        std::vector<int> leased;    // the children holding a lease, sorted by edge
+        int block = kNone;
+        std::uint64_t last_use = 0;
     };
 
-    explicit Trie(std::size_t blocks) : leases(blocks, 0) {}
+    Node& at(int id) { return nodes_[static_cast<std::size_t>(id)]; }
+    const Node& at(int id) const { return nodes_[static_cast<std::size_t>(id)]; }
 
-    Node root;
-    Node* oldest = nullptr;
-    Node* newest = nullptr;
-    std::size_t cached = 0, nodes = 0, key_tokens = 0;
-    std::vector<std::size_t> leases;  // cache leases per physical page
+    // First entry of a sorted list whose edge is not less than the run.
+    template <class List>
+    auto first_not_less(List& list, const std::int32_t* run, std::size_t n) const {
+        return std::partition_point(list.begin(), list.end(), [&](int id) {
+            const Edge& e = at(id).edge;
+            return run_less(e.data(), e.size(), run, n);
+        });
+    }
 
-    void lru_remove(Node& n) noexcept {
-        (n.older ? n.older->newer : oldest) = n.newer;
-        (n.newer ? n.newer->older : newest) = n.older;
-        n.older = n.newer = nullptr;
+public:
+
+    explicit Tree(std::size_t blocks) : nodes_(1), leases_per_block_(blocks, 0) {}
+
+    std::size_t leases() const { return leases_; }
+    std::size_t live_nodes() const { return live_nodes_; }
+    std::size_t key_tokens() const { return key_tokens_; }
+    bool leased(int id) const { return at(id).block != kNone; }
+    int block_of(int id) const { return at(id).block; }
+
+    std::size_t cache_only_blocks(const KvBlockPool& pool) const {
+        std::size_t count = 0;
+        for (std::size_t b = 0; b < leases_per_block_.size(); ++b) {
+            const std::size_t leases = leases_per_block_[b];
+            if (leases && pool.references(static_cast<int>(b)) == leases) ++count;
+        }
+        return count;
     }
-    void lru_push(Node& n) noexcept {
-        n.older = newest;
-        n.newer = nullptr;
-        (newest ? newest->newer : oldest) = &n;
-        newest = &n;
+
+    // The child of `parent` whose edge is exactly the run, or kNone.
+    int child(int parent, const std::int32_t* run, std::size_t n) const {
+        const std::vector<int>& list = at(parent).children;
+        const auto it = first_not_less(list, run, n);
+        if (it == list.end()) return kNone;
+        const Edge& e = at(*it).edge;
+        return e.size() == n && std::equal(e.begin(), e.end(), run) ? *it : kNone;
     }
-    void touch(Node& n) noexcept {
-        lru_remove(n);
-        lru_push(n);
+
+    int add_child(int parent, const std::int32_t* run, std::size_t n) {
+        // Room for clear()'s traversal stack, which must not allocate.
+        if (stack_.capacity() < live_nodes_ + 1) stack_.reserve(2 * (live_nodes_ + 1));
+        int id;
+        if (!free_.empty()) {
+            id = free_.back();
+            free_.pop_back();
+        } else {
+            id = static_cast<int>(nodes_.size());
+            nodes_.emplace_back();
+            free_.reserve(nodes_.size());  // prune() pushes slots back without allocating
+        }
+        Node& node = at(id);
+        node.parent = parent;
+        node.edge.assign(run, run + n);
+        std::vector<int>& list = at(parent).children;
+        list.insert(first_not_less(list, run, n), id);
+        ++live_nodes_;
+        key_tokens_ += n;
+        return id;
     }
-    // Removes empty leaves upward from n, never `keep` or the root.
-    void prune(Node* n, Node* keep) noexcept {
-        while (n != &root && n != keep && n->block < 0 && n->children.empty()) {
-            Node* parent = n->parent;
-            key_tokens -= n->edge->size();
-            --nodes;
-            parent->children.erase(parent->children.find(*n->edge));
-            n = parent;
+
+    // The leased child of `parent` sharing the longest prefix with the
+    // query run, and that length (0: none).
+    std::pair<int, std::size_t> best_leased_child(int parent, const std::int32_t* query, std::size_t n) const {
+        const std::vector<int>& list = at(parent).leased;
+        const auto it = first_not_less(list, query, n);
+        int best = kNone;
+        std::size_t length = 0;
+        if (it != list.end()) {
+            best = *it;
+            length = common_prefix(at(best).edge, query, n);
+        }
+        if (it != list.begin()) {
+            const int before = *std::prev(it);
+            const std::size_t l = common_prefix(at(before).edge, query, n);
+            if (l > length) {
+                best = before;
+                length = l;
+            }
+        }
+        return {best, length};
+    }
+
+    void lease(int id, int block) {
+        Node& node = at(id);
+        std::vector<int>& list = at(node.parent).leased;
+        list.insert(first_not_less(list, node.edge.data(), node.edge.size()), id);
+        node.block = block;
+        node.last_use = ++clock_;
+        recency_.emplace(node.last_use, id);
+        ++leases_per_block_[static_cast<std::size_t>(block)];
+        ++leases_;
+    }
+
+    void touch(int id) {
+        Node& node = at(id);
+        recency_.erase(node.last_use);
+        node.last_use = ++clock_;
+        recency_.emplace(node.last_use, id);
+    }
+
+    // Drops the lease of `id` (one block reference) and removes the
+    // unleased leaves this leaves behind, never `keep`.
+    void unlease(KvBlockPool& pool, int id, int keep = kNone) noexcept {
+        Node& node = at(id);
+        std::vector<int>& list = at(node.parent).leased;
+        list.erase(first_not_less(list, node.edge.data(), node.edge.size()));
+        recency_.erase(node.last_use);
+        const int block = node.block;
+        node.block = kNone;
+        --leases_per_block_[static_cast<std::size_t>(block)];
+        --leases_;
+        pool.unref(block);
+        prune(id, keep);
+    }
+
+    void evict_oldest(KvBlockPool& pool, int keep = kNone) noexcept { unlease(pool, recency_.begin()->second, keep); }
+
+    // Removes `id` and then its ancestors while they are unleased leaves.
+    void prune(int id, int keep = kNone) noexcept {
+        while (id != kRoot && id != keep && at(id).block == kNone && at(id).children.empty()) {
+            Node& node = at(id);
+            const int parent = node.parent;
+            std::vector<int>& siblings = at(parent).children;
+            siblings.erase(first_not_less(siblings, node.edge.data(), node.edge.size()));
+            key_tokens_ -= node.edge.size();
+            --live_nodes_;
+            node.parent = kNone;
+            node.edge.clear();
+            free_.push_back(id);  // capacity: at most one slot per node ever made
+            id = parent;
         }
     }
-    void drop_lease(KvBlockPool& pool, Node& n, Node* keep = nullptr) noexcept {
-        n.parent->leased.erase(n.edge);
-        --leases[static_cast<std::size_t>(n.block)];
-        lru_remove(n);
-        pool.unref(n.block);
-        n.block = -1;
-        --cached;
-        prune(&n, keep);
-    }
-    // Next node in lexicographic pre-order, or null.
-    Node* next_preorder(Node* n) noexcept {
-        if (!n->children.empty()) return n->children.begin()->second.get();
-        while (n != &root) {
-            Node* parent = n->parent;
-            auto it = parent->children.upper_bound(*n->edge);
-            if (it != parent->children.end()) return it->second.get();
-            n = parent;
+
+    // Releases every lease in lexicographic pre-order (depth first, children
+    // in edge order), with a stack whose capacity add_child keeps ready.
+    void clear(KvBlockPool& pool) noexcept {
+        stack_.clear();
+        const std::vector<int>& top = at(kRoot).children;
+        stack_.insert(stack_.end(), top.rbegin(), top.rend());
+        while (!stack_.empty()) {
+            const int id = stack_.back();
+            stack_.pop_back();
+            const std::vector<int>& kids = at(id).children;
+            stack_.insert(stack_.end(), kids.rbegin(), kids.rend());
+            // Pruning below only removes this node or nodes already visited.
+            if (leased(id)) unlease(pool, id);
         }
-        return nullptr;
     }
+
+private:
+    std::vector<Node> nodes_;  // nodes_[kRoot] is the empty root
+    std::vector<int> free_;
+    std::vector<int> stack_;
+    std::map<std::uint64_t, int> recency_;  // last use -> leased node, oldest first
+    std::uint64_t clock_ = 0;
+    std::vector<std::size_t> leases_per_block_;
+    std::size_t leases_ = 0, live_nodes_ = 0, key_tokens_ = 0;
 };
 
 ExactPrefixCache::ExactPrefixCache(KvBlockPool& pool)
-    : pool_(pool), trie_(std::make_unique<Trie>(static_cast<std::size_t>(pool.config().max_blocks))) {}
+    : pool_(pool), tree_(std::make_unique<Tree>(static_cast<std::size_t>(pool.config().max_blocks))) {}
 
 ExactPrefixCache::~ExactPrefixCache() { clear(); }
 
-std::size_t ExactPrefixCache::size() const { return trie_->cached; }
-std::size_t ExactPrefixCache::index_nodes() const { return trie_->nodes; }
-std::size_t ExactPrefixCache::key_token_bytes() const { return trie_->key_tokens * sizeof(std::int32_t); }
+std::size_t ExactPrefixCache::size() const { return tree_->leases(); }
+std::size_t ExactPrefixCache::index_nodes() const { return tree_->live_nodes(); }
+std::size_t ExactPrefixCache::key_token_bytes() const { return tree_->key_tokens() * sizeof(std::int32_t); }
+std::size_t ExactPrefixCache::cache_only_blocks() const { return tree_->cache_only_blocks(pool_); }
 
-std::size_t ExactPrefixCache::cache_only_blocks() const {
-    std::size_t count = 0;
-    for (std::size_t b = 0; b < trie_->leases.size(); ++b)
-        if (trie_->leases[b] && pool_.references(static_cast<int>(b)) == trie_->leases[b]) ++count;
-    return count;
-}
+void ExactPrefixCache::clear() noexcept { tree_->clear(pool_); }
 
 bool ExactPrefixCache::evict_one() {
-    if (!trie_->oldest) return false;
-    trie_->drop_lease(pool_, *trie_->oldest);
+    if (!tree_->leases()) return false;
+    tree_->evict_oldest(pool_);
     ++evictions_;
     return true;
-}
-
-void ExactPrefixCache::clear() noexcept {
-    Trie& t = *trie_;
-    Trie::Node* n = t.root.children.empty() ? nullptr : t.root.children.begin()->second.get();
-    while (n) {
-        Trie::Node* next = t.next_preorder(n);  // before pruning can free n
-        if (n->block >= 0) t.drop_lease(pool_, *n);
-        n = next;
-    }
 }
 
 int ExactPrefixCache::reuse(PagedSequence& sequence, const std::vector<std::int32_t>& prompt) {
     if (sequence.used || !sequence.blocks.empty() || !sequence.tokens.empty())
         throw std::invalid_argument("prefix reuse requires an empty sequence");
     if (!pool_.config().prefix_cache_blocks) return 0;
-    const std::size_t bt = static_cast<std::size_t>(pool_.config().block_tokens);
-    // One prompt token always stays uncached so the append produces logits.
+    const std::size_t page = static_cast<std::size_t>(pool_.config().block_tokens);
+    // The last prompt token is never taken from the cache: appending it
+    // produces the logits of the next token.
     const std::size_t limit = prompt.empty() ? 0 : prompt.size() - 1;
-    std::vector<int> pages;
-    Trie::Node* parent = &trie_->root;
-    std::size_t matched_total = 0;
-    while (matched_total < limit) {
-        const std::size_t want = std::min(bt, limit - matched_total);
-        const Span query{prompt.data() + matched_total, prompt.data() + matched_total + want};
-        auto it = parent->leased.lower_bound(query);
-        Trie::Node* best = nullptr;
-        std::size_t best_len = 0;
-        auto consider = [&](Trie::Node* candidate) {
-            const auto& edge = *candidate->edge;
-            std::size_t n = 0;
-            while (n < want && n < edge.size() && edge[n] == query.begin[n]) ++n;
-            if (n > best_len) {
-                best_len = n;
-                best = candidate;
-            }
-        };
-        if (it != parent->leased.end()) consider(it->second);
-        if (it != parent->leased.begin()) consider(std::prev(it)->second);
-        if (!best_len) break;
-        pages.push_back(best->block);
-        trie_->touch(*best);
-        matched_total += best_len;
-        if (best_len != bt) break;  // a partial match ends the walk
-        parent = best;
+    std::vector<int> blocks;
+    std::size_t covered = 0;
+    int parent = Tree::kRoot;
+    while (covered < limit) {
+        const std::size_t want = std::min(page, limit - covered);
+        const auto match = tree_->best_leased_child(parent, prompt.data() + covered, want);
+        if (!match.second) break;
+        blocks.push_back(tree_->block_of(match.first));
+        tree_->touch(match.first);
+        covered += match.second;
+        if (match.second < page) break;  // a partial page ends the path
+        parent = match.first;
     }
-    for (const int page : pages) pool_.retain(page);
-    sequence.blocks = std::move(pages);
-    sequence.tokens.assign(prompt.begin(), prompt.begin() + static_cast<std::ptrdiff_t>(matched_total));
-    sequence.used = static_cast<int>(matched_total);
-    if (matched_total) {
+    for (const int b : blocks) pool_.retain(b);
+    sequence.blocks = std::move(blocks);
+    sequence.tokens.assign(prompt.begin(), prompt.begin() + static_cast<std::ptrdiff_t>(covered));
+    sequence.used = static_cast<int>(covered);
+    if (covered) {
         ++hits_;
-        reused_ += matched_total;
+        reused_ += covered;
     } else {
         ++misses_;
     }
@@ -187,42 +275,33 @@ int ExactPrefixCache::reuse(PagedSequence& sequence, const std::vector<std::int3
 void ExactPrefixCache::publish(const PagedSequence& sequence) {
     if (sequence.tokens.size() != static_cast<std::size_t>(sequence.used))
         throw std::logic_error("invalid committed KV token history");
-    Trie& t = *trie_;
-    const std::size_t bt = static_cast<std::size_t>(pool_.config().block_tokens);
+    const std::size_t page = static_cast<std::size_t>(pool_.config().block_tokens);
     const std::size_t used = static_cast<std::size_t>(sequence.used);
     const std::size_t capacity = static_cast<std::size_t>(pool_.config().prefix_cache_blocks);
-    const std::size_t pages = std::min({sequence.blocks.size(), (used + bt - 1) / bt, capacity});
-    Trie::Node* parent = &t.root;
+    const std::size_t pages = std::min({sequence.blocks.size(), (used + page - 1) / page, capacity});
+    int parent = Tree::kRoot;
     for (std::size_t i = 0; i < pages; ++i) {
-        const std::int32_t* first = sequence.tokens.data() + i * bt;
-        const std::size_t length = std::min(bt, used - i * bt);
-        const Span key{first, first + length};
-        auto found = parent->children.find(key);
-        if (found == parent->children.end()) {
-            auto node = std::make_unique<Trie::Node>();
-            found = parent->children.emplace(std::vector<std::int32_t>(first, first + length), std::move(node)).first;
-            found->second->parent = parent;
-            found->second->edge = &found->first;
-            ++t.nodes;
-            t.key_tokens += length;
-        }
-        Trie::Node& node = *found->second;
-        if (node.block >= 0) {
-            t.touch(node);
+        const std::int32_t* run = sequence.tokens.data() + i * page;
+        const std::size_t length = std::min(page, used - i * page);
+        int node = tree_->child(parent, run, length);
+        if (node == Tree::kNone) node = tree_->add_child(parent, run, length);
+        if (tree_->leased(node)) {
+            tree_->touch(node);
         } else {
-            const int page = sequence.blocks[i];
-            parent->leased.emplace(node.edge, &node);
-            pool_.retain(page);
-            if (t.cached == capacity) {
-                t.drop_lease(pool_, *t.oldest, &node);
+            const int block = sequence.blocks[i];
+            try {
+                pool_.retain(block);  // before any eviction can release the same block
+            } catch (...) {
+                tree_->prune(node);
+                throw;
+            }
+            if (tree_->leases() == capacity) {
+                tree_->evict_oldest(pool_, node);
                 ++evictions_;
             }
-            ++t.leases[static_cast<std::size_t>(page)];
-            node.block = page;
-            t.lru_push(node);
-            ++t.cached;
+            tree_->lease(node, block);
         }
-        parent = &node;
+        parent = node;
     }
 }
 
