@@ -35,3 +35,53 @@ def upload_model(backend: HipBackend, model: OracleModel):
 def pool_elements(config: dict, block_tokens: int, max_blocks: int) -> int:
     kv = config["kv_heads"] * (config["hidden"] // config["heads"])
     return max_blocks * config["layers"] * block_tokens * kv
+
+
+def reference_library():
+    """The reference's own MiniPrefix (Engine, KVManager, CpuRunner) compiled
+    from its sources into oracle/_ref (the checker), or None if not built."""
+    from oracle import ref_library
+    return ref_library()
+
+
+def sin_weight_tensors() -> dict:
+    """The device regression model of the reference's cow_test.cpp:118-137:
+    tiny_config() shape, every non-norm weight 0.15f*sinf(k) for k = 1, 2, ...
+    in the order the reference adds them, norms 1, and embedding row 15 NaN
+    (appending token 15 makes any runner produce non-finite logits)."""
+    import ctypes
+    libm = ctypes.CDLL("libm.so.6")
+    libm.sinf.restype = ctypes.c_float
+    libm.sinf.argtypes = [ctypes.c_float]
+    counter = [0]
+
+    def fill(shape, norm=False):
+        n = int(np.prod(shape))
+        if norm:
+            return np.ones(n, dtype=np.float32)
+        out = np.empty(n, dtype=np.float32)
+        for i in range(n):
+            counter[0] += 1
+            out[i] = np.float32(0.15) * np.float32(libm.sinf(float(counter[0])))
+        return out
+
+    t = {"model.embed_tokens.weight": fill((16, 8)), "lm_head.weight": fill((8, 16)),
+         "model.norm.weight": fill((8,), True)}
+    for layer in range(2):
+        p = f"model.layers.{layer}."
+        t[p + "input_layernorm.weight"] = fill((8,), True)
+        t[p + "post_attention_layernorm.weight"] = fill((8,), True)
+        for name, shape in (("self_attn.q_proj", (8, 8)), ("self_attn.k_proj", (8, 4)), ("self_attn.v_proj", (8, 4)),
+                            ("self_attn.o_proj", (8, 8)), ("mlp.gate_proj", (8, 12)), ("mlp.up_proj", (8, 12)),
+                            ("mlp.down_proj", (12, 8))):
+            t[p + name + ".weight"] = fill(shape)
+    t["model.embed_tokens.weight"][15 * 8:16 * 8] = np.nan
+    return t
+
+
+def weights_with(tensors: dict, config: dict, library=None):
+    from tinyinfer_amd.host import Weights
+    w = Weights.synthetic(config, seed=1, stddev=0.02, library=library)
+    for name, data in tensors.items():
+        w.set_tensor(name, data)
+    return w

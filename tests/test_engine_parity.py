@@ -1,0 +1,121 @@
+"""The HIP Engine against the reference Engine, step by step.
+
+Three engines run the same submissions on the same synthetic weights:
+- this repository's Engine over the HIP runner with batched steps (the
+  path bench.py measures);
+- the same with batching off (one ModelRunner::append per request, the
+  reference's loop);
+- the reference's own Engine and KVManager, compiled from its sources
+  (oracle/_ref), over the C oracle forward (bit-identical to the reference
+  CpuRunner).
+After every step the events (request, token, finish reason, error) and every
+live sequence's committed page table must be identical, and at the end the
+copy-on-write counters. The prefix cache is on: requests publish and reuse
+pages within one step and across steps, partial tails are shared and
+copied, and decoding requests copy their republished tail every step
+(miniprefix/src/engine/engine.cpp:98, prefix_cache.cpp:147-148).
+
+A CPU variant runs the reference Engine over the reference CpuRunner against
+the oracle-KV runner (tokens and events only), which checks the scenario
+itself without a GPU."""
+import numpy as np
+import pytest
+
+from tinyinfer_amd.host import Engine, Runner, Weights, smollm_config
+
+from .helpers import reference_library
+
+SEED = 31
+
+
+def scenario(vocabulary: int):
+    """(step, id, prompt, max_new_tokens) submissions."""
+    rng = np.random.default_rng(SEED)
+    base = [int(t) for t in rng.integers(0, vocabulary, 80)]
+    other = [int(t) for t in rng.integers(0, vocabulary, 40)]
+    return [
+        # seed decodes twice; the followers map its pages in the steps that publish them
+        (0, "seed", base[:37], 2),
+        (0, "follower", base[:37] + other[:6], 3),      # 37 cached tokens: 2 pages + a 5-token tail
+        (0, "interior", base[:20] + other[6:10], 4),    # interior of the seed's second page
+        (1, "late", base[:45], 5),                       # the seed's history after its decode
+        (2, "fresh", other[10:40], 6),
+        (3, "turn2", base[:37] + other[:6] + [7, 8], 3),
+        (4, "aligned", base[:32], 2),                    # whole-page prompt: its last token is recomputed
+    ]
+
+
+def transcript(engine: Engine, runner: Runner | None, submits, steps: int = 40):
+    out, live = [], set()
+    pending = sorted(submits, key=lambda s: s[0])
+    for step in range(steps):
+        while pending and pending[0][0] <= step:
+            _, rid, prompt, n = pending.pop(0)
+            engine.submit(rid, prompt, max_new_tokens=n, eos_token_id=None)
+            live.add(rid)
+        engine.step()
+        events = engine.poll_events()
+        for e in events:
+            if e.get("finish") is not None:
+                live.discard(e["id"])
+        tables = {}
+        if runner is not None:
+            for rid in sorted(live):
+                try:
+                    tables[rid] = runner.sequence(rid)
+                except LookupError:
+                    pass  # admitted but not resident yet
+        out.append((step, engine.last_step_stats(), events, tables))
+        if not pending and engine.idle():
+            break
+    assert engine.idle() and not engine.failed()
+    return out
+
+
+CONFIG = dict(smollm_config(layers=2, context=512))
+KV = dict(block_tokens=16, max_blocks=96, prefix_cache_blocks=48)
+ENGINE = dict(max_batch_size=4, token_budget=96, prefill_chunk=24, context=512)
+
+
+def reference_run(kind: int):
+    ref = reference_library()
+    if ref is None:
+        pytest.skip("oracle/_ref not built")
+    w = Weights.synthetic(CONFIG, seed=SEED, stddev=0.02, library=ref)
+    runner = Runner(w, context=512, kind=kind, **KV)
+    engine = Engine(runner, **ENGINE)
+    t = transcript(engine, runner if kind == 1 else None, scenario(CONFIG["vocabulary"]))
+    costs = runner.cost_stats()
+    engine.shutdown()
+    return t, costs
+
+
+def strip_tables(t):
+    return [(s, st, ev) for s, st, ev, _ in t]
+
+
+def test_scenario_on_reference_runners():
+    """CPU: the reference Engine over the reference CpuRunner and over the
+    oracle-KV runner emit the same events (the oracle forward is the
+    reference's arithmetic)."""
+    cpu, _ = reference_run(0)
+    okv, costs = reference_run(1)
+    assert strip_tables(cpu) == strip_tables(okv)
+    assert costs["cow_pages"] > 0  # the scenario exercises copy-on-write
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("batching", [True, False])
+def test_hip_engine_matches_reference_engine(torch_cuda, batching):
+    want, want_costs = reference_run(1)
+    w = Weights.synthetic(CONFIG, seed=SEED, stddev=0.02)
+    runner = Runner(w, context=512, **KV)
+    engine = Engine(runner, **ENGINE)
+    engine.set_batching(batching)
+    got = transcript(engine, runner, scenario(CONFIG["vocabulary"]))
+    costs = runner.cost_stats()
+    engine.shutdown()
+    for g, r in zip(got, want):
+        assert g == r, f"step {r[0]} differs:\nHIP       {g}\nreference {r}"
+    assert len(got) == len(want)
+    assert costs["cow_pages"] == want_costs["cow_pages"] and costs["cow_bytes"] == want_costs["cow_bytes"]
