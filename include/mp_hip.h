@@ -86,6 +86,8 @@ typedef struct mp_hip mp_hip;
 int mp_hip_create(const mp_model_desc* model, const mp_kv_desc* kv, mp_hip** out);
 /* Synchronizes and frees everything (CudaRunner::~CudaRunner, :88). */
 int mp_hip_destroy(mp_hip* h);
+/* Message of the last failure on `h`; for h = NULL, of the last failed
+ * context-free call (the stand-alone attention entry points) on this thread. */
 const char* mp_hip_last_error(const mp_hip* h);
 
 /* Tensor slots, canonical per-layer order. layer = -1 for the model-level
@@ -141,6 +143,20 @@ int mp_hip_paged_attention_decode(const float* q, const float* keys, const float
                                   const int32_t* table, int32_t length, int32_t layer,
                                   int32_t layers, int32_t block_tokens, int32_t heads,
                                   int32_t kv_heads, int32_t dim, float* out, void* stream);
+
+/* The same attention as mp_hip_paged_attention_decode with no allocation of
+ * any kind: no counterpart in the reference; for callers that cannot
+ * allocate (code under HIP graph capture, serving loops that forbid
+ * allocation). The scores of a long row go to a 1 MiB device array of the
+ * library (one per GPU, held until the process ends) instead of a per-call
+ * hipMalloc; a row must satisfy heads * round_up(length, 16) <= 262144, or
+ * the call returns MP_INVALID_ARGUMENT (message: mp_hip_last_error(NULL)).
+ * Calls that overlap on one GPU share the array and race. Asynchronous on
+ * `stream`. */
+int mp_hip_paged_attention_decode_noalloc(const float* q, const float* keys, const float* values,
+                                          const int32_t* table, int32_t length, int32_t layer,
+                                          int32_t layers, int32_t block_tokens, int32_t heads,
+                                          int32_t kv_heads, int32_t dim, float* out, void* stream);
 
 /* Waits for all work on the context's stream (StreamBlas::synchronize). */
 int mp_hip_sync(mp_hip* h);

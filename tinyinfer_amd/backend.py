@@ -65,6 +65,7 @@ def _bind(lib):
     lib.mp_hip_forward.argtypes = [vp, ctypes.POINTER(SeqStep), ctypes.c_int32, I32P, F32P, I32P, I32P]
     lib.mp_hip_copy_tail_timed.argtypes = [vp, ctypes.POINTER(TailRegion), ctypes.POINTER(ctypes.c_uint64)]
     lib.mp_hip_paged_attention_decode.argtypes = [vp, vp, vp, vp] + [ctypes.c_int32] * 7 + [vp, vp]
+    lib.mp_hip_paged_attention_decode_noalloc.argtypes = [vp, vp, vp, vp] + [ctypes.c_int32] * 7 + [vp, vp]
     lib.mp_hip_sync.argtypes = [vp]
     lib.mp_hip_stats.argtypes = [vp, ctypes.POINTER(Counters)]
     lib.mp_hip_kv_pools.argtypes = [vp, ctypes.POINTER(vp), ctypes.POINTER(vp), ctypes.POINTER(ctypes.c_size_t)]
@@ -182,4 +183,17 @@ def paged_attention_decode(q, keys, values, table, length: int, layer: int, laye
     status = lib().mp_hip_paged_attention_decode(q, keys, values, table, length, layer, layers, block_tokens,
                                                  heads, kv_heads, dim, out, stream)
     if status:
-        raise BackendError(status, f"mp_hip_paged_attention_decode failed ({status})")
+        message = (lib().mp_hip_last_error(None) or b"").decode()
+        raise BackendError(status, f"mp_hip_paged_attention_decode failed ({status}): {message}")
+
+
+def paged_attention_decode_noalloc(q, keys, values, table, length: int, layer: int, layers: int,
+                                   block_tokens: int, heads: int, kv_heads: int, dim: int, out,
+                                   stream: int | None = None):
+    """The same attention with no allocation (the library's static device
+    scratch holds a long row's scores)."""
+    status = lib().mp_hip_paged_attention_decode_noalloc(q, keys, values, table, length, layer, layers,
+                                                         block_tokens, heads, kv_heads, dim, out, stream)
+    if status:
+        message = (lib().mp_hip_last_error(None) or b"").decode()
+        raise BackendError(status, f"mp_hip_paged_attention_decode_noalloc failed ({status}): {message}")

@@ -323,6 +323,13 @@ int flush_tables(mp_hip* h) {
 
 }  // namespace
 
+namespace mphip {
+namespace {
+thread_local std::string g_free_error = "no error";
+}  // namespace
+void set_free_error(const std::string& message) { g_free_error = message; }
+}  // namespace mphip
+
 extern "C" {
 
 int mp_hip_create(const mp_model_desc* model, const mp_kv_desc* kv, mp_hip** out) {
@@ -426,7 +433,7 @@ int mp_hip_destroy(mp_hip* h) {
     return MP_OK;
 }
 
-const char* mp_hip_last_error(const mp_hip* h) { return h ? h->error.c_str() : "null context"; }
+const char* mp_hip_last_error(const mp_hip* h) { return h ? h->error.c_str() : mphip::g_free_error.c_str(); }
 
 int mp_hip_upload_tensor(mp_hip* h, int32_t layer, int32_t slot, const float* data, size_t count) {
     if (!h || !data) return fail(h, MP_INVALID_ARGUMENT, "null tensor");
@@ -799,8 +806,10 @@ int mp_hip_paged_attention_decode(const float* q, const float* keys, const float
                                   int32_t kv_heads, int32_t dim, float* out, void* stream) {
     if (!q || !keys || !values || !table || !out || length < 1 || layer < 0 || layer >= layers ||
         block_tokens < 1 || heads < 1 || kv_heads < 1 || heads % kv_heads || dim < 4 || dim % 4 ||
-        dim > 256 || heads / kv_heads > 8)
+        dim > 256 || heads / kv_heads > 8) {
+        mphip::set_free_error("invalid paged attention arguments");
         return MP_INVALID_ARGUMENT;
+    }
     const int group = heads / kv_heads;
     float* scratch = nullptr;
     hipStream_t s = static_cast<hipStream_t>(stream);
