@@ -250,11 +250,15 @@ class Runner:
 
     def sequence(self, rid: str) -> tuple[list[int], int]:
         """(page table, used tokens) of a committed sequence."""
-        cap = 1 << 16
-        blocks = np.empty(cap, dtype=np.int32)
+        blocks = getattr(self, "_table_buffer", None)
+        if blocks is None:
+            blocks = self._table_buffer = np.empty(1 << 12, dtype=np.int32)
         n, used = ctypes.c_int32(), ctypes.c_int32()
-        _check(self.lib, self.lib.mpx_runner_sequence(self.handle, _b(rid), blocks.ctypes.data_as(I32P), cap,
+        _check(self.lib, self.lib.mpx_runner_sequence(self.handle, _b(rid), blocks.ctypes.data_as(I32P), blocks.size,
                                                       ctypes.byref(n), ctypes.byref(used)))
+        if n.value > blocks.size:  # grow and read again
+            self._table_buffer = np.empty(n.value, dtype=np.int32)
+            return self.sequence(rid)
         return blocks[: n.value].tolist(), used.value
 
 
