@@ -45,7 +45,9 @@ int mpx_weights_tensor(const void* weights, const char* name, const float** data
 int mpx_weights_set(void* weights, const char* name, const float* data, size_t count);
 void mpx_weights_free(void* weights);
 
-/* ModelRunner. kind 0 is the library's device runner. */
+/* ModelRunner. kind 0 is the library's device runner in the exact arithmetic
+ * (logits bit-identical to the reference CPU path), kind 2 the same runner in
+ * the fast arithmetic (MP_ARITHMETIC_FAST of mp_hip.h). */
 void* mpx_runner_create(void* weights, int32_t kind, int32_t context, int32_t block_tokens, int32_t max_blocks,
                         int32_t prefix_cache_blocks);
 void mpx_runner_free(void* runner);

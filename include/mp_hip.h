@@ -20,11 +20,12 @@
  *  - a context is single-threaded, like the reference's KVManager
  *    (miniprefix/include/miniprefix/kv_manager.h:18-19).
  *
- * Arithmetic: every kernel reproduces the reference CPU path's floating-point
- * evaluation order (sequential-k projections with separate multiply and add,
- * sequential RMSNorm and softmax sums, two-pass softmax, glibc-compatible
- * expf, host-computed RoPE angles), so logits are bit-identical to
- * miniprefix/src/backend/cpu/llama_runner.cpp:60-104.
+ * Arithmetic: in the exact mode every kernel reproduces the reference CPU
+ * path's floating-point evaluation order (sequential-k projections with
+ * separate multiply and add, sequential RMSNorm and softmax sums, two-pass
+ * softmax, glibc-compatible expf, host-computed RoPE angles), so logits are
+ * bit-identical to miniprefix/src/backend/cpu/llama_runner.cpp:60-104; the
+ * fast mode trades that for matrix cores (MP_ARITHMETIC_FAST below).
  */
 #ifndef MP_HIP_H
 #define MP_HIP_H
@@ -43,11 +44,26 @@ enum {
     MP_NONFINITE = -4         /* runtime_error("nonfinite ... logits"), llama_runner.cu:173 */
 };
 
-/* Model shape; same fields and limits as ModelConfig (model.h:9-16, model.cpp:9-15). */
+/* Arithmetic of a context (mp_model_desc.arithmetic):
+ * - MP_ARITHMETIC_EXACT: every sum in the reference CPU path's order
+ *   (sequential k, separate multiply and add, two-pass softmax): logits
+ *   bit-identical to miniprefix/src/backend/cpu/llama_runner.cpp:60-104;
+ * - MP_ARITHMETIC_FAST: projections and the LM head on FP32 matrix cores and
+ *   decode attention split over the context (flash-decoding), in their own
+ *   summation order: logits within 1e-3 relative and decode attention within
+ *   1e-4 absolute of the reference, greedy tokens checked against it.
+ *   Prefill attention keeps the exact kernels. Needs hidden, intermediate,
+ *   q+2*kv width and vocabulary multiples of 16, else the context computes
+ *   exactly. */
+enum { MP_ARITHMETIC_EXACT = 0, MP_ARITHMETIC_FAST = 1 };
+
+/* Model shape; same fields and limits as ModelConfig (model.h:9-16,
+ * model.cpp:9-15), plus the arithmetic mode (no counterpart in the reference). */
 typedef struct mp_model_desc {
     int32_t layers, hidden, intermediate, heads, kv_heads, vocabulary, context;
     float rms_epsilon, rope_theta;
     int32_t tied;
+    int32_t arithmetic;
 } mp_model_desc;
 
 /* Paged KV geometry (KvCacheConfig, paged_kv.h:13-17) plus the device block

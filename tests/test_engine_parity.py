@@ -105,11 +105,14 @@ def test_scenario_on_reference_runners():
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("kind", [0, 2], ids=["exact", "fast"])
 @pytest.mark.parametrize("batching", [True, False])
-def test_hip_engine_matches_reference_engine(torch_cuda, batching):
+def test_hip_engine_matches_reference_engine(torch_cuda, batching, kind):
+    """Exact arithmetic (kind 0) and fast arithmetic (kind 2) alike: the same
+    events, tokens and page tables as the reference engine at every step."""
     want, want_costs = reference_run(1)
     w = Weights.synthetic(CONFIG, seed=SEED, stddev=0.02)
-    runner = Runner(w, context=512, **KV)
+    runner = Runner(w, context=512, kind=kind, **KV)
     engine = Engine(runner, **ENGINE)
     engine.set_batching(batching)
     got = transcript(engine, runner, scenario(CONFIG["vocabulary"]))

@@ -2,8 +2,9 @@
 written from the reference's own MiniPrefix (tests/golden/make_fixtures.py).
 
 Each workload (tinyinfer_amd/workloads.py: configs 2, 3, 4, 5A, 5B) runs
-through this repository's Engine with batched steps over the HIP runner, as
-bench.py runs it. After every engine step the digest of every resident
+through this repository's Engine with batched steps over the HIP runner in
+the fast arithmetic, as bench.py runs it (configs 2 and 4 also in the exact
+arithmetic). After every engine step the digest of every resident
 sequence's committed page table and the step's token counts must equal the
 reference Engine's; the copy-on-write counters must equal its counts at the
 end; and the greedy tokens of the fixture's requests must equal the
@@ -36,10 +37,10 @@ def digest(runner, ids):
     return h.hexdigest()[:16]
 
 
-def run_workload(name):
+def run_workload(name, kind):
     wl = WORKLOADS[name]()
     weights = Weights.synthetic(wl.config(), seed=wl.weight_seed, stddev=0.02)
-    runner = Runner(weights, context=wl.context, **wl.kv_args())
+    runner = Runner(weights, context=wl.context, kind=kind, **wl.kv_args())
     engine = Engine(runner, **wl.engine_args())
     engine.set_batching(True)
     tokens = {r.id: [] for r in wl.requests}
@@ -66,12 +67,17 @@ def run_workload(name):
     return wl, tokens, digests, np.array(stats), costs
 
 
-@pytest.mark.parametrize("name", ["config2", "config3", "config4", "config5b", "config5a"])
-def test_workload_matches_reference(torch_cuda, name):
+CASES = [(name, 2) for name in ("config2", "config3", "config4", "config5b", "config5a")] + \
+        [("config2", 0), ("config4", 0)]
+
+
+@pytest.mark.parametrize("name,kind", CASES, ids=[f"{n}-{'fast' if k == 2 else 'exact'}" for n, k in CASES])
+def test_workload_matches_reference(torch_cuda, name, kind):
+    """kind 2: the fast arithmetic (bench.py's runner); kind 0: the exact one."""
     path = GOLDEN / f"{name}.npz"
     assert path.exists(), f"missing fixture {path}"
     fx = np.load(path, allow_pickle=False)
-    wl, tokens, digests, stats, costs = run_workload(name)
+    wl, tokens, digests, stats, costs = run_workload(name, kind)
     assert list(fx["table_hash"]) == digests, "page tables differ from the reference engine's"
     assert np.array_equal(fx["step_stats"], stats)
     assert [costs["cow_pages"], costs["cow_bytes"]] == fx["cow"].tolist()

@@ -9,12 +9,14 @@ from ._native import F32P, I32P, library
 
 MP_OK, MP_INVALID_ARGUMENT, MP_DEVICE_ERROR, MP_OUT_OF_MEMORY, MP_NONFINITE = 0, -1, -2, -3, -4
 TENSOR_EMBEDDING, TENSOR_FINAL_NORM, TENSOR_LM_HEAD = 100, 101, 102
+ARITHMETIC_EXACT, ARITHMETIC_FAST = 0, 1
 
 
 class ModelDesc(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int32) for n in
                 ("layers", "hidden", "intermediate", "heads", "kv_heads", "vocabulary", "context")] + [
-        ("rms_epsilon", ctypes.c_float), ("rope_theta", ctypes.c_float), ("tied", ctypes.c_int32)]
+        ("rms_epsilon", ctypes.c_float), ("rope_theta", ctypes.c_float), ("tied", ctypes.c_int32),
+        ("arithmetic", ctypes.c_int32)]
 
 
 class KvDesc(ctypes.Structure):
@@ -85,11 +87,12 @@ class HipBackend:
     """One device context: resident weights, paged K/V pools, block tables."""
 
     def __init__(self, config: dict, block_tokens: int, max_blocks: int, max_sequences: int = 64,
-                 max_sequence_blocks: int | None = None):
+                 max_sequence_blocks: int | None = None, arithmetic: int = ARITHMETIC_EXACT):
         self.lib = lib()
         self.config = dict(config)
         m = ModelDesc(**{k: config[k] for k in ("layers", "hidden", "intermediate", "heads", "kv_heads",
-                                                "vocabulary", "context", "rms_epsilon", "rope_theta", "tied")})
+                                                "vocabulary", "context", "rms_epsilon", "rope_theta", "tied")},
+                      arithmetic=arithmetic)
         if max_sequence_blocks is None:
             max_sequence_blocks = -(-config["context"] // block_tokens)
         k = KvDesc(block_tokens, max_blocks, max_sequences, max_sequence_blocks)

@@ -61,6 +61,14 @@ struct mp_hip {
     float *x = nullptr, *xn = nullptr, *qkv_out = nullptr, *ctx = nullptr, *ffn = nullptr;
     float *last = nullptr, *logits = nullptr, *scratch = nullptr;
     size_t scratch_floats = 0;
+    // Fast arithmetic (MP_ARITHMETIC_FAST with shapes that allow it): row
+    // sums of squares of the residual stream in 16-column partials
+    // [hidden/16][workspace rows] for the RMSNorm of the next projection, and
+    // the decode attention's split partials (grow-only).
+    bool fast = false;
+    float* ssq = nullptr;
+    float* fast_partials = nullptr;
+    size_t fast_partial_floats = 0;
     float* best_value = nullptr;  // LM-head partials [seqs][groups]
     int32_t* best_index = nullptr;
     int32_t* best_bad = nullptr;
@@ -209,12 +217,14 @@ int ensure_workspace(mp_hip* h, int rows, int seqs, int max_length) {
     const int S = ((seqs > h->workspace_seqs ? seqs : h->workspace_seqs) + 63) / 64 * 64;
     for (void* p : {(void*)h->x, (void*)h->xn, (void*)h->qkv_out, (void*)h->ctx, (void*)h->ffn,
                     (void*)h->last, (void*)h->logits, (void*)h->results,
-                    (void*)h->best_value, (void*)h->best_index, (void*)h->best_bad})
+                    (void*)h->best_value, (void*)h->best_index, (void*)h->best_bad, (void*)h->ssq})
         device_free(h, p);
-    h->x = h->xn = h->qkv_out = h->ctx = h->ffn = h->last = h->logits = h->best_value = nullptr;
+    h->x = h->xn = h->qkv_out = h->ctx = h->ffn = h->last = h->logits = h->best_value = h->ssq = nullptr;
     h->results = h->best_index = h->best_bad = nullptr;
     h->workspace_rows = h->workspace_seqs = 0;
-    const size_t hd = c.hidden, groups = mphip::head_groups(c.vocabulary);
+    const size_t hd = c.hidden;
+    const size_t groups = h->fast ? std::max<size_t>(mphip::head_groups(c.vocabulary), c.vocabulary / 16)
+                                  : mphip::head_groups(c.vocabulary);
     struct Item { void** p; size_t bytes; };
     const Item items[] = {
         {(void**)&h->x, sizeof(float) * R * hd},
@@ -228,6 +238,7 @@ int ensure_workspace(mp_hip* h, int rows, int seqs, int max_length) {
         {(void**)&h->best_value, sizeof(float) * S * groups},
         {(void**)&h->best_index, sizeof(int32_t) * S * groups},
         {(void**)&h->best_bad, sizeof(int32_t) * S * groups},
+        {(void**)&h->ssq, h->fast ? sizeof(float) * R * (hd / 16) : 0},
     };
     size_t total = 0;
     for (const auto& it : items) {
@@ -340,6 +351,12 @@ int mp_hip_create(const mp_model_desc* model, const mp_kv_desc* kv, mp_hip** out
     h->model = *model;
     h->kv = *kv;
     const mp_model_desc& c = h->model;
+    if (c.arithmetic != MP_ARITHMETIC_EXACT && c.arithmetic != MP_ARITHMETIC_FAST) {
+        delete h;
+        return MP_INVALID_ARGUMENT;
+    }
+    h->fast = c.arithmetic == MP_ARITHMETIC_FAST && c.hidden % 16 == 0 && c.intermediate % 16 == 0 &&
+              qkv_width(c) % 16 == 0 && c.vocabulary % 16 == 0;
     // Pages are streamed as float4 runs of tokens: the device path needs a
     // page size that is a multiple of 4 tokens, head_dim a multiple of 4 and
     // at most 64 (one output lane per d) and at most 8 query heads per KV
@@ -612,8 +629,33 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
     for (const Block& b : blocks) items += (size_t)(b.length + 255) / 256;
     const size_t nblocks = blocks.size();
     const size_t table_pairs = h->pending_tables.size();
-    const size_t entries = 3 * (size_t)R + 2 * (size_t)nseq + 2 * nblocks + 2 * items + 2 * table_pairs;
+    // Fast-mode decode attention: work items (row, KV head, first token,
+    // tokens) over 128-token splits, and per row (first item, splits per KV
+    // head). The split depends on nothing but the row, so a row's result
+    // does not depend on the rest of the batch.
+    const int dim_ = c.hidden / c.heads, group_ = c.heads / c.kv_heads;
+    const bool fast_decode = h->fast && decode && h->kv.block_tokens == 16 && dim_ == 64 && group_ <= 4;
+    const int split = 128;
+    size_t fast_items = 0;
+    if (fast_decode)
+        for (int q = 0; q < nseq; ++q) fast_items += (size_t)c.kv_heads * ((steps[q].used + 1 + split - 1) / split);
+    const size_t base_entries = 3 * (size_t)R + 2 * (size_t)nseq + 2 * nblocks + 2 * items + 2 * table_pairs;
+    const size_t fast_at = (base_entries + 3) / 4 * 4;  // int4 items need 16-byte alignment
+    const size_t entries = fast_decode ? fast_at + 4 * fast_items + 2 * (size_t)R : base_entries;
     if ((status = ensure_call_buffers(h, entries))) return status;
+    if (fast_decode) {
+        const size_t need = fast_items * group_ * (64 + 2);
+        if (need > h->fast_partial_floats) {
+            if ((status = stream_sync(h))) return status;
+            device_free(h, h->fast_partials);
+            h->fast_partials = nullptr;
+            h->fast_partial_floats = 0;
+            const size_t grow = need + need / 2;
+            if ((status = device_alloc(h, (void**)&h->fast_partials, sizeof(float) * grow, "allocate attention partials")))
+                return status;
+            h->fast_partial_floats = grow;
+        }
+    }
     int32_t* const m0 = h->host_meta;
     int32_t* m_tokens = m0;
     int32_t* m_seq = m_tokens + R;
@@ -641,6 +683,24 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
         for (int ch = 0; ch < (blocks[b].length + 255) / 256; ++ch, ++it) {
             m_items[2 * it] = (int32_t)b;
             m_items[2 * it + 1] = ch;
+        }
+    }
+    int32_t* const m_fast = m0 + fast_at;
+    int32_t* const m_row_items = m_fast + 4 * fast_items;
+    if (fast_decode) {
+        // Decode: row q is sequence q's only row.
+        size_t f = 0;
+        for (int q = 0; q < nseq; ++q) {
+            const int length = steps[q].used + 1, splits = (length + split - 1) / split;
+            m_row_items[2 * q] = (int32_t)f;
+            m_row_items[2 * q + 1] = splits;
+            for (int kvh = 0; kvh < c.kv_heads; ++kvh)
+                for (int sp = 0; sp < splits; ++sp, ++f) {
+                    m_fast[4 * f] = q;
+                    m_fast[4 * f + 1] = kvh;
+                    m_fast[4 * f + 2] = sp * split;
+                    m_fast[4 * f + 3] = std::min(split, length - sp * split);
+                }
         }
     }
     status = check(h, hipMemcpyAsync(h->meta, m0, sizeof(int32_t) * entries, hipMemcpyHostToDevice, h->stream),
@@ -734,7 +794,90 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
         return r;
     };
     hipError_t e = mphip::launch_embed(s, h->embedding, meta.tokens, h->x, R, hd, device_error);
-    for (int l = 0; l < c.layers && e == hipSuccess; ++l) {
+    if (h->fast) {
+        // Matrix-core projections; RMSNorm folded into the next projection
+        // through per-16-column sums of squares of the residual stream.
+        const int ssq_stride = h->workspace_rows, parts = hd / 16;
+        auto fast = [&](mphip::Epilogue epi, const float* x, int inner, const float* w, const float* w2, int columns,
+                        float* out, const float* norm) {
+            mphip::FastGemmArgs a{};
+            a.x = x;
+            a.w = w;
+            a.w2 = w2;
+            a.out = out;
+            a.rows = R;
+            a.inner = inner;
+            a.columns = columns;
+            a.norm = norm;
+            a.eps = eps;
+            a.ssq_in = h->ssq;
+            a.ssq_out = h->ssq;
+            a.ssq_parts = parts;
+            a.ssq_stride = ssq_stride;
+            return mphip::launch_fast_gemm(s, epi, a);
+        };
+        mphip::FastAttentionWork fw{};
+        fw.items = h->meta + (m_fast - m0);
+        fw.items_count = (int)fast_items;
+        fw.row_items = h->meta + (m_row_items - m0);
+        fw.partial_out = h->fast_partials;
+        fw.partial_ml = h->fast_partials + fast_items * group_ * 64;
+        if (e == hipSuccess) e = mphip::launch_fast_ssq(s, h->x, R, hd, h->ssq, ssq_stride);
+        for (int l = 0; l < c.layers && e == hipSuccess; ++l) {
+            layer_now = l;
+            e = timed(P, [&] { return fast(mphip::kStore, h->x, hd, h->qkv[l], nullptr, qw, h->qkv_out, h->input_norm[l]); });
+            if (e == hipSuccess) {
+                if (fast_decode) {
+                    e = timed(MP_TIME_ATTENTION, [&] {
+                        hipError_t r = mphip::launch_rope_append(s, h->qkv_out, qw, R, c.heads, c.kv_heads, dim,
+                                                                 h->cos_table, h->sin_table, meta, kv, l);
+                        if (r == hipSuccess)
+                            r = mphip::launch_fast_attention(s, h->qkv_out, qw, R, c.heads, c.kv_heads, meta, kv, l,
+                                                             h->ctx, hd, fw);
+                        return r;
+                    });
+                } else {
+                    e = mphip::launch_attention(s, h->qkv_out, qw, R, c.heads, c.kv_heads, dim, meta, kv, l, h->ctx, hd,
+                                                work, decode, mphip::RopeTables{h->cos_table, h->sin_table},
+                                                attention_events());
+                }
+            }
+            if (e == hipSuccess) e = timed(P, [&] { return fast(mphip::kResidual, h->ctx, hd, h->o[l], nullptr, hd, h->x, nullptr); });
+            if (e == hipSuccess)
+                e = timed(P, [&] { return fast(mphip::kSwiglu, h->x, hd, h->gate[l], h->up[l], in, h->ffn, h->post_norm[l]); });
+            if (e == hipSuccess) e = timed(P, [&] { return fast(mphip::kResidual, h->ffn, in, h->down[l], nullptr, hd, h->x, nullptr); });
+        }
+        layer_now = sampled ? -2 : -1;
+        if (e == hipSuccess) e = timed(MP_TIME_HEAD, [&] {
+            mphip::FastGemmArgs a{};
+            a.x = h->x;
+            a.w = h->head;
+            a.rows = nseq;
+            a.inner = hd;
+            a.columns = c.vocabulary;
+            a.norm = h->final_norm;
+            a.eps = eps;
+            a.ssq_in = h->ssq;
+            a.ssq_parts = parts;
+            a.ssq_stride = ssq_stride;
+            a.row_map = meta.seq_last_row;
+            a.logits = logits ? h->logits : nullptr;
+            a.best_value = h->best_value;
+            a.best_index = h->best_index;
+            a.bad = h->best_bad;
+            a.groups = c.vocabulary / 16;
+            hipError_t r = mphip::launch_fast_gemm(s, mphip::kHead, a);
+            mphip::GemmArgs g{};
+            g.rows = nseq;
+            g.best_value = h->best_value;
+            g.best_index = h->best_index;
+            g.bad = h->best_bad;
+            g.groups = a.groups;
+            if (r == hipSuccess) r = mphip::launch_head_argmax(s, g, h->results, h->results + nseq);
+            return r;
+        });
+    }
+    for (int l = 0; !h->fast && l < c.layers && e == hipSuccess; ++l) {
         layer_now = l;
         e = timed(P, [&] { return normed_gemm(mphip::kStore, h->input_norm[l], R, hd, h->qkv[l], nullptr, qw, h->qkv_out); });
         if (e == hipSuccess)
@@ -745,8 +888,8 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
             e = timed(P, [&] { return normed_gemm(mphip::kSwiglu, h->post_norm[l], R, hd, h->gate[l], h->up[l], in, h->ffn); });
         if (e == hipSuccess) e = timed(P, [&] { return gemm(mphip::kResidual, h->ffn, R, in, h->down[l], nullptr, hd, h->x); });
     }
-    layer_now = sampled ? -2 : -1;  // a sampled call times no head
-    if (e == hipSuccess) e = timed(MP_TIME_HEAD, [&] {
+    if (!h->fast) layer_now = sampled ? -2 : -1;  // a sampled call times no head
+    if (!h->fast && e == hipSuccess) e = timed(MP_TIME_HEAD, [&] {
         // Final norm of each sequence's last row, then the LM head with the
         // greedy argmax folded into its epilogue (logits are written only
         // when the caller asks for them).

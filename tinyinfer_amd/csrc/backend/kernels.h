@@ -66,6 +66,59 @@ hipError_t launch_gemm_normed(hipStream_t s, Epilogue epilogue, const GemmArgs& 
 // logit, from the kHead partials of `args`.
 hipError_t launch_head_argmax(hipStream_t s, const GemmArgs& args, int32_t* argmax, int32_t* nonfinite);
 
+// Fast arithmetic mode (fast_gemm.hip): the same projections on FP32 matrix
+// cores, in their summation order. x and out in the quad layout (kHead:
+// logits row-major [rows][columns]); w (and w2, the up matrix of kSwiglu) is
+// [columns][inner]. inner and columns multiples of 16.
+// - norm (kStore, kSwiglu, kHead): RMSNorm of x with weights `norm`; the row
+//   sums of squares come from ssq_in: ssq_parts partial sums per row at
+//   ssq_in[p*ssq_stride + row] (written by the producer of x).
+// - kResidual: out += result, and ssq_out[c*ssq_stride + row] = sum of
+//   squares of the updated row over columns 16c..16c+15.
+// - kHead: row i of the result reads x row row_map[i]; per row and 16-column
+//   block, the first maximum into best_value/best_index/bad [rows][groups]
+//   (groups = columns/16), logits written when `logits` is non-null.
+struct FastGemmArgs {
+    const float* x;
+    const float* w;
+    const float* w2;
+    float* out;
+    int rows, inner, columns;
+    const float* norm;
+    float eps;
+    const float* ssq_in;
+    float* ssq_out;
+    int ssq_parts, ssq_stride;
+    const int32_t* row_map;
+    float* logits;
+    float* best_value;
+    int32_t* best_index;
+    int32_t* bad;
+    int groups;
+};
+bool fast_gemm_fits(const FastGemmArgs& args);
+hipError_t launch_fast_gemm(hipStream_t s, Epilogue epilogue, const FastGemmArgs& args);
+// Per-16-column sums of squares of x's rows (quad layout, `width` columns)
+// into ssq[p*stride + row], for the first RMSNorm after the embedding.
+hipError_t launch_fast_ssq(hipStream_t s, const float* x, int rows, int width, float* ssq, int stride);
+
+// Fast-mode decode attention (fast_attention.hip): every row is one new
+// token (already rotated q, its K/V already in the pools). Flash-decoding
+// split over the context: work item (row, KV head, split of `split` tokens)
+// keeps a running maximum, denominator and output per query head; then one
+// merge per (row, head). Scratch: partial outputs [items][group][dim] and
+// (max, denominator) pairs [items][group][2]. head dim 64, page 16.
+struct FastAttentionWork {
+    const int32_t* items;  // per work item: row, kv head, first token, token count (int4)
+    int items_count;
+    const int32_t* row_items;  // per row: first work item of kv head 0 and splits per kv head (int2)
+    float* partial_out;
+    float* partial_ml;
+};
+hipError_t launch_fast_attention(hipStream_t s, const float* qkv, int ldq, int rows, int heads, int kv_heads,
+                                 const RowMeta& meta, const PagedKv& kv, int layer, float* out, int ldo,
+                                 const FastAttentionWork& work);
+
 // x = embedding rows of `tokens`; also clears the forward's device error
 // word `error` (may be null).
 hipError_t launch_embed(hipStream_t s, const float* embedding, const int32_t* tokens, float* x, int rows,

@@ -1,6 +1,8 @@
 // Weights and runners of this library for the C entry points.
 #include "harness_backend.h"
 
+#include "mp_hip.h"
+
 #include <cstring>
 
 namespace miniprefix {
@@ -35,10 +37,13 @@ bool weights_set(miniprefix::ModelWeights& weights, const std::string& name, con
     return true;
 }
 
+// Kind 0: the HIP runner in the exact arithmetic (logits bit-identical to the
+// reference CPU path); kind 2: the HIP runner in the fast arithmetic.
 std::unique_ptr<miniprefix::ModelRunner> make_runner(int kind, std::shared_ptr<miniprefix::ModelWeights> weights,
                                                      int context, miniprefix::KvCacheConfig kv) {
-    if (kind != 0) throw std::invalid_argument("unknown runner kind");
-    return miniprefix::make_hip_runner(std::move(weights), context, kv);
+    if (kind == 0) return miniprefix::make_hip_runner(std::move(weights), context, kv);
+    if (kind == 2) return miniprefix::make_hip_runner(std::move(weights), context, kv, MP_ARITHMETIC_FAST);
+    throw std::invalid_argument("unknown runner kind");
 }
 
 void set_batching(miniprefix::Engine& engine, bool enabled) { engine.set_batching(enabled); }

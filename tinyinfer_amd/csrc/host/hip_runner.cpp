@@ -29,13 +29,13 @@ namespace {
 
 class HipRunner final : public ModelRunner, public StagedRunner {
 public:
-    HipRunner(std::shared_ptr<ModelWeights> weights, int context, KvCacheConfig kv)
+    HipRunner(std::shared_ptr<ModelWeights> weights, int context, KvCacheConfig kv, int arithmetic)
         : weights_(std::move(weights)),
           kv_(kv, config().layers, config().kv_width(), context, config().vocabulary) {
         if (context < 1 || context > config().context) throw std::invalid_argument("invalid runner context");
         const ModelConfig& c = config();
         const mp_model_desc m{c.layers, c.hidden, c.intermediate, c.heads, c.kv_heads, c.vocabulary, context,
-                              c.rms_epsilon, c.rope_theta, c.tied ? 1 : 0};
+                              c.rms_epsilon, c.rope_theta, c.tied ? 1 : 0, arithmetic};
         table_entries_ = static_cast<int>(kv_.max_sequence_blocks());
         const mp_kv_desc d{kv.block_tokens, kv.max_blocks, kMaxSequences, table_entries_};
         const int status = mp_hip_create(&m, &d, &device_);
@@ -297,7 +297,14 @@ private:
 }  // namespace
 
 std::unique_ptr<ModelRunner> make_hip_runner(std::shared_ptr<ModelWeights> weights, int context, KvCacheConfig kv) {
-    return std::make_unique<HipRunner>(std::move(weights), context, kv);
+    return std::make_unique<HipRunner>(std::move(weights), context, kv, MP_ARITHMETIC_EXACT);
+}
+
+// The same runner with a chosen arithmetic (MP_ARITHMETIC_EXACT or
+// MP_ARITHMETIC_FAST, include/mp_hip.h).
+std::unique_ptr<ModelRunner> make_hip_runner(std::shared_ptr<ModelWeights> weights, int context, KvCacheConfig kv,
+                                             int arithmetic) {
+    return std::make_unique<HipRunner>(std::move(weights), context, kv, arithmetic);
 }
 
 // Page table of a sequence for runners built by make_hip_runner.

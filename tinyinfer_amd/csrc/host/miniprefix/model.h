@@ -82,7 +82,11 @@ public:
     virtual void set_cost_timing(bool) {}
 };
 
-// Device backend over the C ABI of include/mp_hip.h.
+// Device backend over the C ABI of include/mp_hip.h: exact arithmetic (logits
+// bit-identical to the reference CPU path), or the arithmetic chosen by
+// `arithmetic` (MP_ARITHMETIC_EXACT or MP_ARITHMETIC_FAST).
 std::unique_ptr<ModelRunner> make_hip_runner(std::shared_ptr<ModelWeights>, int context, KvCacheConfig kv = {});
+std::unique_ptr<ModelRunner> make_hip_runner(std::shared_ptr<ModelWeights>, int context, KvCacheConfig kv,
+                                             int arithmetic);
 
 }  // namespace miniprefix
