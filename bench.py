@@ -82,7 +82,7 @@ def gpu_leg(args):
     t = time.perf_counter()
     weights = Weights.synthetic(cfg, seed=args.seed, stddev=0.02)
     runner = Runner(weights, context=cfg["context"], block_tokens=PAGE, max_blocks=max_blocks,
-                    prefix_cache_blocks=0)
+                    prefix_cache_blocks=0, kind=2 if args.arithmetic == "fast" else 0)
     device = runner.device()
     engine = Engine(runner, max_batch_size=BATCH, token_budget=BUDGET, prefill_chunk=CHUNK, context=cfg["context"])
     engine.set_batching(True)
@@ -147,17 +147,6 @@ def gpu_leg(args):
         value=BATCH * K / elapsed, ms_per_step=elapsed / K * 1e3, prefill_steps=prefill_steps,
         mean_context=mean_context, attention_us_per_launch=att_s / launches * 1e6,
         attention_bytes_per_launch=att_bytes / launches, achieved=achieved, times=times)
-    if args.traffic_probe:
-        from tinyinfer_amd.backend import TailRegion, lib
-        # A plain copy of known size for counter calibration: 4096 rows of
-        # 4096 floats in each pool (64 MiB read + 64 MiB written per pool).
-        region = TailRegion(0, 4096 * 4096, 4096, 4096, 4096)
-        for _ in range(3):
-            status = lib().mp_hip_copy_tail(device, region)
-            if status:
-                raise RuntimeError(f"copy probe failed ({status})")
-        torch.cuda.synchronize()
-        result["copy_probe_bytes"] = 2 * 2 * 4096 * 4096 * 4
     engine.shutdown()
     engine.close()
     return result
@@ -206,7 +195,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--all-kernels", action="store_true", help="also time projections and the LM head")
-    ap.add_argument("--traffic-probe", action="store_true", help="run a copy of known size after the timed steps")
+    ap.add_argument("--arithmetic", choices=["fast", "exact"], default="fast")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (decode would shard by request, "
