@@ -67,6 +67,8 @@ struct mp_hip {
     // the decode attention's split partials (grow-only).
     bool fast = false;
     float* ssq = nullptr;
+    int32_t* row_block = nullptr;  // [workspace rows]: page of each row's position (decode)
+    float* row_rope = nullptr;     // [workspace rows][head dim]: cos | sin at each row's position
     float* fast_partials = nullptr;
     size_t fast_partial_floats = 0;
     float* best_value = nullptr;  // LM-head partials [seqs][groups]
@@ -217,10 +219,12 @@ int ensure_workspace(mp_hip* h, int rows, int seqs, int max_length) {
     const int S = ((seqs > h->workspace_seqs ? seqs : h->workspace_seqs) + 63) / 64 * 64;
     for (void* p : {(void*)h->x, (void*)h->xn, (void*)h->qkv_out, (void*)h->ctx, (void*)h->ffn,
                     (void*)h->last, (void*)h->logits, (void*)h->results,
-                    (void*)h->best_value, (void*)h->best_index, (void*)h->best_bad, (void*)h->ssq})
+                    (void*)h->best_value, (void*)h->best_index, (void*)h->best_bad, (void*)h->ssq,
+                    (void*)h->row_block, (void*)h->row_rope})
         device_free(h, p);
     h->x = h->xn = h->qkv_out = h->ctx = h->ffn = h->last = h->logits = h->best_value = h->ssq = nullptr;
-    h->results = h->best_index = h->best_bad = nullptr;
+    h->results = h->best_index = h->best_bad = h->row_block = nullptr;
+    h->row_rope = nullptr;
     h->workspace_rows = h->workspace_seqs = 0;
     const size_t hd = c.hidden;
     const size_t groups = h->fast ? std::max<size_t>(mphip::head_groups(c.vocabulary), c.vocabulary / 16)
@@ -239,6 +243,8 @@ int ensure_workspace(mp_hip* h, int rows, int seqs, int max_length) {
         {(void**)&h->best_index, sizeof(int32_t) * S * groups},
         {(void**)&h->best_bad, sizeof(int32_t) * S * groups},
         {(void**)&h->ssq, h->fast ? sizeof(float) * R * (hd / 16) : 0},
+        {(void**)&h->row_block, h->fast ? sizeof(int32_t) * R : 0},
+        {(void**)&h->row_rope, h->fast ? sizeof(float) * R * (size_t)(hd / c.heads) : 0},
     };
     size_t total = 0;
     for (const auto& it : items) {
@@ -635,7 +641,7 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
     // does not depend on the rest of the batch.
     const int dim_ = c.hidden / c.heads, group_ = c.heads / c.kv_heads;
     const bool fast_decode = h->fast && decode && h->kv.block_tokens == 16 && dim_ == 64 && group_ <= 4;
-    const int split = 128;
+    const int split = mphip::fast_attention_split_tokens();
     size_t fast_items = 0;
     if (fast_decode)
         for (int q = 0; q < nseq; ++q) fast_items += (size_t)c.kv_heads * ((steps[q].used + 1 + split - 1) / split);
@@ -697,7 +703,7 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
             for (int kvh = 0; kvh < c.kv_heads; ++kvh)
                 for (int sp = 0; sp < splits; ++sp, ++f) {
                     m_fast[4 * f] = q;
-                    m_fast[4 * f + 1] = kvh;
+                    m_fast[4 * f + 1] = steps[q].table_slot * c.kv_heads + kvh;
                     m_fast[4 * f + 2] = sp * split;
                     m_fast[4 * f + 3] = std::min(split, length - sp * split);
                 }
@@ -793,7 +799,12 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
         if (r == hipSuccess) r = gemm(epi, h->xn, rows, inner, w, w2, columns, out);
         return r;
     };
-    hipError_t e = mphip::launch_embed(s, h->embedding, meta.tokens, h->x, R, hd, device_error);
+    // The fast decode's q|k|v projection takes each row's page and rotation
+    // from per-row arrays that the embedding kernel fills.
+    mphip::RowRope row_rope{meta, h->tables, h->kv.max_sequence_blocks, h->kv.block_tokens, dim / 2,
+                            h->cos_table, h->sin_table, h->row_block, h->row_rope};
+    hipError_t e = mphip::launch_embed(s, h->embedding, meta.tokens, h->x, R, hd, device_error,
+                                       fast_decode ? &row_rope : nullptr);
     if (h->fast) {
         // Matrix-core projections; RMSNorm folded into the next projection
         // through per-16-column sums of squares of the residual stream.
@@ -822,19 +833,41 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
         fw.row_items = h->meta + (m_row_items - m0);
         fw.partial_out = h->fast_partials;
         fw.partial_ml = h->fast_partials + fast_items * group_ * 64;
+        fw.kv_heads = c.kv_heads;
         if (e == hipSuccess) e = mphip::launch_fast_ssq(s, h->x, R, hd, h->ssq, ssq_stride);
         for (int l = 0; l < c.layers && e == hipSuccess; ++l) {
             layer_now = l;
-            e = timed(P, [&] { return fast(mphip::kStore, h->x, hd, h->qkv[l], nullptr, qw, h->qkv_out, h->input_norm[l]); });
+            if (fast_decode) {
+                // q|k|v with RoPE and the KV append in the epilogue.
+                e = timed(P, [&] {
+                    mphip::FastGemmArgs a{};
+                    a.x = h->x;
+                    a.w = h->qkv[l];
+                    a.out = h->qkv_out;
+                    a.rows = R;
+                    a.inner = hd;
+                    a.columns = qw;
+                    a.norm = h->input_norm[l];
+                    a.eps = eps;
+                    a.ssq_in = h->ssq;
+                    a.ssq_parts = parts;
+                    a.ssq_stride = ssq_stride;
+                    a.meta = meta;
+                    a.kv = kv;
+                    a.layer = l;
+                    a.heads = c.heads;
+                    a.row_block = h->row_block;
+                    a.row_rope = h->row_rope;
+                    return mphip::launch_fast_gemm(s, mphip::kRope, a);
+                });
+            } else {
+                e = timed(P, [&] { return fast(mphip::kStore, h->x, hd, h->qkv[l], nullptr, qw, h->qkv_out, h->input_norm[l]); });
+            }
             if (e == hipSuccess) {
                 if (fast_decode) {
                     e = timed(MP_TIME_ATTENTION, [&] {
-                        hipError_t r = mphip::launch_rope_append(s, h->qkv_out, qw, R, c.heads, c.kv_heads, dim,
-                                                                 h->cos_table, h->sin_table, meta, kv, l);
-                        if (r == hipSuccess)
-                            r = mphip::launch_fast_attention(s, h->qkv_out, qw, R, c.heads, c.kv_heads, meta, kv, l,
-                                                             h->ctx, hd, fw);
-                        return r;
+                        return mphip::launch_fast_attention(s, h->qkv_out, qw, R, c.heads, c.kv_heads, meta, kv, l,
+                                                            h->ctx, hd, fw);
                     });
                 } else {
                     e = mphip::launch_attention(s, h->qkv_out, qw, R, c.heads, c.kv_heads, dim, meta, kv, l, h->ctx, hd,
@@ -860,12 +893,12 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
             a.ssq_in = h->ssq;
             a.ssq_parts = parts;
             a.ssq_stride = ssq_stride;
-            a.row_map = meta.seq_last_row;
+            a.row_map = decode ? nullptr : meta.seq_last_row;  // decode: row s is sequence s's last
             a.logits = logits ? h->logits : nullptr;
             a.best_value = h->best_value;
             a.best_index = h->best_index;
             a.bad = h->best_bad;
-            a.groups = c.vocabulary / 16;
+            a.groups = c.vocabulary / mphip::fast_head_group_columns(c.vocabulary);
             hipError_t r = mphip::launch_fast_gemm(s, mphip::kHead, a);
             mphip::GemmArgs g{};
             g.rows = nseq;

@@ -1,26 +1,42 @@
 // Decode attention of the fast arithmetic mode: flash-decoding over the
 // paged pools. The reference computes each (row, head) with an explicit
 // two-pass softmax and sequential sums (llama_runner.cpp:85-93); here the
-// context is cut into page-aligned splits, each split keeps a running
-// maximum, denominator and weighted sum (the order of the floating-point
-// sums differs; the result matches the reference within 1e-4 absolute on
-// the reference's scale of inputs).
+// context is cut into page-aligned splits of 128 tokens, each split keeps
+// a running maximum, denominator and weighted sum per query head, and the
+// splits are combined at the end (the order of the floating-point sums
+// differs; the result matches the reference within 1e-4 absolute on the
+// reference's scale of inputs). The splits depend on nothing but the row,
+// so a row's result does not depend on the rest of the batch.
 //
-// One wavefront per work item (row, KV head, split): it serves the G query
-// heads of the KV head, so each K and V byte is read once. Per page (16
-// tokens of one layer and KV head, 4 KB of K then 4 KB of V, device page
-// order of layout.h):
+// One wavefront per work item (row, KV head, split: the item carries the
+// row's table slot beside the KV head), four items per work-group; the
+// wavefront serves the G query heads of the KV head, so each K and V byte
+// is read once. It walks the split's (up to 8) pages with three pages in
+// flight in a ring of registers: the loads of page k+3 are issued as soon
+// as page k has been used. Per page (16 tokens of one layer and KV head,
+// 4 KB of K then 4 KB of V, device page order of layout.h):
 //  - scores: lane = (token t = lane/4, quarter dq = lane%4 of the 64 dims);
 //    a lane reads 4 float4 of K (dims 16dq..16dq+15 of token t, the 16 lanes
 //    of one float4 index forming a 256-byte run) and the four quarters are
 //    summed across lanes;
 //  - output: lane = dim d; a lane reads 4 float4 of V (4 tokens each for
-//    its d, a 1 KB run per float4 index) and the page's probabilities from
-//    LDS.
-// The next page's K and V loads are issued before the current page is used.
-// A merge kernel then combines the splits of every (row, head).
+//    its d, a 1 KB run per float4 index) and takes each token's probability
+//    from the token's lane (a lane read, as are the page's maximum and sum:
+//    cross-lane steps stay on the vector ALU, see lanes.h).
+// Loads past the split's last page re-read that page (a cache hit) so that
+// every load is unconditional and the waits stay exact. A row whose
+// context is one split writes its output directly; otherwise every split
+// writes its partial and a merge kernel combines them in split order.
+// (Combining in the last split to finish costs each split a store
+// completion and an atomic round trip at its end, more than the extra
+// launch; with a device-scope release fence it would also write back the
+// whole L2 on this chip.)
 #include "kernels.h"
+#include "lanes.h"
 #include "layout.h"
+
+// The fast mode's own summation order: multiply-adds may be fused.
+#pragma clang fp contract(fast)
 
 namespace mphip {
 namespace {
@@ -30,19 +46,47 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 constexpr int kDim = 64;
 constexpr int kPage = 16;
 constexpr int kMaxGroup = 4;
+constexpr int kSplitPages = 8;
+constexpr int kSplitTokens = kSplitPages * kPage;  // 128
+constexpr int kRing = 3;                           // pages in flight per wavefront
+constexpr int kItemsPerGroup = 4;
+constexpr int kMergeHeld = 16;  // splits whose partial outputs the merge loads up front
+constexpr float kScale = 0.125f;  // 1/sqrt(64)
+
 
 template <int G>
-__global__ __launch_bounds__(64) void fast_attention_split_kernel(const float* __restrict__ qkv, int ldq, int heads,
-                                                                  RowMeta meta, PagedKv kv, int layer,
-                                                                  FastAttentionWork w) {
-    __shared__ float p_s[G][kPage];
-    const int lane = threadIdx.x;
-    const int4 item = reinterpret_cast<const int4*>(w.items)[blockIdx.x];
-    const int row = item.x, kvh = item.y, t0 = item.z, n = item.w;
-    const int length = meta.row_pos[row] + 1;
-    const int32_t* table = kv.tables + (size_t)meta.seq_slot[meta.row_seq[row]] * kv.table_stride;
+__global__ __launch_bounds__(kItemsPerGroup * 64) void fast_attention_kernel(const float* __restrict__ qkv, int ldq,
+                                                                             RowMeta meta, PagedKv kv, int layer,
+                                                                             FastAttentionWork w,
+                                                                             float* __restrict__ out, int ldo) {
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int index = blockIdx.x * kItemsPerGroup + wave;
+    if (index >= w.items_count) return;
+    const int4 item = reinterpret_cast<const int4*>(w.items)[index];
+    const int row = item.x, kvh = item.y % w.kv_heads, t0 = item.z, n = item.w;
+    const int32_t* table = kv.tables + (size_t)(item.y / w.kv_heads) * kv.table_stride;
     const int t = lane >> 2, dq = lane & 3;
-    // q of the group's heads, dims 16dq..16dq+15 (rotated, quad layout).
+    const int end = t0 + n;           // tokens t0..end-1 (t0 page-aligned)
+    const int first = t0 / kPage;     // the split's first page
+    const int np = (end + kPage - 1) / kPage - first;  // 1..kSplitPages
+    int page_id[kSplitPages];
+#pragma unroll
+    for (int k = 0; k < kSplitPages; ++k) page_id[k] = table[first + min(k, np - 1)];
+    const size_t head_base = (size_t)kvh * kPage * kDim;  // floats into a page-layer span
+    f4 kb[kRing][4], vb[kRing][4];
+    auto load = [&](int k, f4 (&kk)[4], f4 (&vv)[4]) {
+        const size_t base = kv_page_base(page_id[k], layer, kv.layers, kPage, kv.kv_width) + head_base;
+        const f4* kp = reinterpret_cast<const f4*>(kv.keys + base);
+        const f4* vp = reinterpret_cast<const f4*>(kv.values + base);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            kk[j] = __builtin_nontemporal_load(kp + (dq * 4 + j) * kPage + t);
+            vv[j] = __builtin_nontemporal_load(vp + j * kDim + lane);
+        }
+    };
+    // q of the group's heads, dims 16dq..16dq+15 (rotated, quad layout);
+    // loaded before the pages, as loads complete in order.
     f4 q[G][4];
 #pragma unroll
     for (int h = 0; h < G; ++h)
@@ -51,19 +95,12 @@ __global__ __launch_bounds__(64) void fast_attention_split_kernel(const float* _
             const int c = (kvh * G + h) * kDim + dq * 16 + j * 4;
             q[h][j] = *reinterpret_cast<const f4*>(qkv + quad_index(row, c, ldq));
         }
-    const size_t head_base = (size_t)kvh * kPage * kDim;  // floats into a page-layer span
-    auto page_ptr = [&](const float* pool, int page) {
-        return pool + kv_page_base(table[page], layer, kv.layers, kPage, kv.kv_width) + head_base;
-    };
-    auto load = [&](int page, f4 (&kk)[4], f4 (&vv)[4]) {
-        const f4* kp = reinterpret_cast<const f4*>(page_ptr(kv.keys, page));
-        const f4* vp = reinterpret_cast<const f4*>(page_ptr(kv.values, page));
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            kk[j] = __builtin_nontemporal_load(kp + (dq * 4 + j) * kPage + t);
-            vv[j] = __builtin_nontemporal_load(vp + j * kDim + lane);
-        }
-    };
+    for (int k = 0; k < kRing; ++k) load(k, kb[k], vb[k]);
+    // Keep the loads where they are: the scheduler would otherwise sink
+    // them to their first use and take the pages out of flight.
+    __builtin_amdgcn_sched_barrier(0);
     float m[G], l[G], acc[G];
 #pragma unroll
     for (int h = 0; h < G; ++h) {
@@ -71,124 +108,149 @@ __global__ __launch_bounds__(64) void fast_attention_split_kernel(const float* _
         l[h] = 0.0f;
         acc[h] = 0.0f;
     }
-    const float scale = 0.125f;  // 1/sqrt(64)
-    const int first = t0 / kPage, last = (t0 + n - 1) / kPage;
-    f4 kc[4], vc[4], kn[4], vn[4];
-    load(first, kc, vc);
-    for (int page = first; page <= last; ++page) {
-        if (page < last) load(page + 1, kn, vn);
-        const int tok = page * kPage + t;
-        const bool valid = tok < length && tok >= t0 && tok < t0 + n;
-        float p[G];
+#pragma unroll
+    for (int k = 0; k < kSplitPages; ++k) {
+        if (k > 0 && k >= np) break;  // np >= 1
+        f4(&kc)[4] = kb[k % kRing];
+        f4(&vc)[4] = vb[k % kRing];
+        const int tok0 = (first + k) * kPage;
+        const bool valid = tok0 + t < end;
+        // Slots past the context (last page only) hold stale values: they
+        // take no part, whatever they are.
+        f4 v[4];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            v[g] = vc[g];
+            const int tok = tok0 + 4 * g;
+            if (tok + 0 >= end) v[g].x = 0.0f;
+            if (tok + 1 >= end) v[g].y = 0.0f;
+            if (tok + 2 >= end) v[g].z = 0.0f;
+            if (tok + 3 >= end) v[g].w = 0.0f;
+        }
 #pragma unroll
         for (int h = 0; h < G; ++h) {
-            f4 prod = q[h][0] * kc[0];
-            prod += q[h][1] * kc[1];
-            prod += q[h][2] * kc[2];
-            prod += q[h][3] * kc[3];
-            float s = (prod.x + prod.y) + (prod.z + prod.w);
-            s += __shfl_xor(s, 1);
-            s += __shfl_xor(s, 2);
-            s = valid ? s * scale : -__builtin_inff();
-            float mx = s;
-            mx = fmaxf(mx, __shfl_xor(mx, 4));
-            mx = fmaxf(mx, __shfl_xor(mx, 8));
-            mx = fmaxf(mx, __shfl_xor(mx, 16));
-            mx = fmaxf(mx, __shfl_xor(mx, 32));
-            const float m_new = fmaxf(m[h], mx);  // finite: every page holds a valid token
-            const float keep = __expf(m[h] - m_new);
-            p[h] = valid ? __expf(s - m_new) : 0.0f;
-            float ps = p[h];
-            ps += __shfl_xor(ps, 4);
-            ps += __shfl_xor(ps, 8);
-            ps += __shfl_xor(ps, 16);
-            ps += __shfl_xor(ps, 32);
-            l[h] = l[h] * keep + ps;
-            acc[h] *= keep;
-            m[h] = m_new;
-        }
-        if (dq == 0)
-#pragma unroll
-            for (int h = 0; h < G; ++h) p_s[h][t] = p[h];
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-        for (int h = 0; h < G; ++h) {
-            const f4* pp = reinterpret_cast<const f4*>(p_s[h]);
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const f4 pv = pp[g];
-                acc[h] += pv.x * vc[g].x + pv.y * vc[g].y + pv.z * vc[g].z + pv.w * vc[g].w;
-            }
-        }
-        __builtin_amdgcn_wave_barrier();
-        if (page < last) {
+            float s = 0.0f;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                kc[j] = kn[j];
-                vc[j] = vn[j];
+                s += q[h][j].x * kc[j].x;
+                s += q[h][j].y * kc[j].y;
+                s += q[h][j].z * kc[j].z;
+                s += q[h][j].w * kc[j].w;
             }
+            s = quad_sum(s);  // token t's score in its four lanes
+            s = valid ? s * kScale : -__builtin_inff();
+            const float m_new = fmaxf(m[h], rows_max(row_quads_max(s)));  // finite: the page holds a valid token
+            const float keep = __expf(m[h] - m_new);
+            const float p = valid ? __expf(s - m_new) : 0.0f;
+            l[h] = l[h] * keep + rows_sum(row_quads_sum(p));
+            float a = acc[h] * keep;
+            // Lane d: sum over the page's tokens of p_t * V[t][d], p_t read from lane 4t.
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                a += lane_value(p, 16 * g + 0) * v[g].x;
+                a += lane_value(p, 16 * g + 4) * v[g].y;
+                a += lane_value(p, 16 * g + 8) * v[g].z;
+                a += lane_value(p, 16 * g + 12) * v[g].w;
+            }
+            acc[h] = a;
+            m[h] = m_new;
         }
+        __builtin_amdgcn_sched_barrier(0);
+        if (k + kRing < kSplitPages) load(k + kRing, kb[k % kRing], vb[k % kRing]);
+        __builtin_amdgcn_sched_barrier(0);
     }
-    const size_t it = blockIdx.x;
+    if (t0 == 0 && n == meta.row_pos[row] + 1) {
+        // The row's only split: the output itself.
+#pragma unroll
+        for (int h = 0; h < G; ++h) out[quad_index(row, (kvh * G + h) * kDim + lane, ldo)] = acc[h] / l[h];
+        return;
+    }
 #pragma unroll
     for (int h = 0; h < G; ++h) {
-        w.partial_out[(it * G + h) * kDim + lane] = acc[h];
+        const size_t at = (size_t)index * G + h;
+        w.partial_out[at * kDim + lane] = acc[h];
         if (lane == 0) {
-            w.partial_ml[(it * G + h) * 2] = m[h];
-            w.partial_ml[(it * G + h) * 2 + 1] = l[h];
+            w.partial_ml[at * 2] = m[h];
+            w.partial_ml[at * 2 + 1] = l[h];
         }
     }
 }
 
-// out[row][h*64 + d] for every head: the splits of (row, h/G) combined.
-__global__ void fast_attention_merge_kernel(int heads, int kv_heads, FastAttentionWork w, float* __restrict__ out,
-                                            int ldo) {
-    const int row = blockIdx.x;
-    const int G = heads / kv_heads;
+// out[row][h*64 + d] for rows of more than one split: the splits of
+// (row, h/G) combined in split order. One wavefront per (row, head): lane
+// sp holds split sp's (max, denominator) and weight exp(m_sp - max); lane d
+// sums its dimension over the splits, the first kMergeHeld partial outputs
+// loaded together with the (max, denominator) pairs.
+__global__ __launch_bounds__(256) void fast_attention_merge_kernel(int rows, int heads, int kv_heads,
+                                                                   FastAttentionWork w, float* __restrict__ out,
+                                                                   int ldo) {
+    const int lane = threadIdx.x & 63;
+    const int pair = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (pair >= rows * heads) return;
+    const int row = pair / heads, h = pair % heads;
+    const int G = heads / kv_heads, kvh = h / G, hg = h % G;
     const int2 ri = reinterpret_cast<const int2*>(w.row_items)[row];
-    for (int i = threadIdx.x; i < heads * kDim; i += blockDim.x) {
-        const int h = i / kDim, d = i % kDim;
-        const int kvh = h / G, hg = h % G;
-        const int base = ri.x + kvh * ri.y;
-        float mx = -__builtin_inff();
-        for (int s = 0; s < ri.y; ++s) mx = fmaxf(mx, w.partial_ml[((size_t)(base + s) * G + hg) * 2]);
-        float den = 0.0f, num = 0.0f;
-        for (int s = 0; s < ri.y; ++s) {
-            const size_t at = (size_t)(base + s) * G + hg;
-            const float f = __expf(w.partial_ml[at * 2] - mx);
-            den += w.partial_ml[at * 2 + 1] * f;
-            num += w.partial_out[at * kDim + d] * f;
-        }
-        out[quad_index(row, i, ldo)] = num / den;
+    const int splits = ri.y;
+    if (splits == 1) return;  // written by the split kernel
+    const size_t item0 = (size_t)ri.x + (size_t)kvh * splits;  // items of (row, kvh) in split order
+    auto at = [&](int sp) { return (item0 + sp) * G + hg; };
+    float num = 0.0f, den = 0.0f, cm = 0.0f;
+    for (int s0 = 0; s0 < splits; s0 += 64) {
+        const int sp = s0 + lane;
+        const int count = min(64, splits - s0);
+        const float mv = w.partial_ml[at(s0 + min(lane, count - 1)) * 2];
+        const float lv = w.partial_ml[at(s0 + min(lane, count - 1)) * 2 + 1];
+        float ov[kMergeHeld];
+#pragma unroll
+        for (int j = 0; j < kMergeHeld; ++j) ov[j] = w.partial_out[at(s0 + min(j, count - 1)) * kDim + lane];
+        const bool mine = sp < splits;
+        float hm = mine ? mv : -__builtin_inff();
+        hm = fmaxf(hm, dpp<kDppQuadXor1>(hm));
+        hm = fmaxf(hm, dpp<kDppQuadXor2>(hm));
+        hm = rows_max(row_quads_max(hm));
+        // A later chunk of 64 splits rescales what the earlier ones summed.
+        const float m_new = s0 == 0 ? hm : fmaxf(cm, hm);
+        const float keep = s0 == 0 ? 0.0f : __expf(cm - m_new);
+        const float f = mine ? __expf(mv - m_new) : 0.0f;
+        den = den * keep + rows_sum(row_sum(lv * f));
+        num *= keep;
+#pragma unroll
+        for (int j = 0; j < kMergeHeld; ++j)
+            if (j < count) num += ov[j] * lane_value(f, j);
+        for (int j = kMergeHeld; j < count; ++j) num += w.partial_out[at(s0 + j) * kDim + lane] * lane_value(f, j);
+        cm = m_new;
     }
+    out[quad_index(row, h * kDim + lane, ldo)] = num / den;
 }
 
 template <int G>
-void launch_split(hipStream_t s, const float* qkv, int ldq, int heads, const RowMeta& meta, const PagedKv& kv,
-                  int layer, const FastAttentionWork& w) {
-    fast_attention_split_kernel<G><<<w.items_count, 64, 0, s>>>(qkv, ldq, heads, meta, kv, layer, w);
+void launch_items(hipStream_t s, const float* qkv, int ldq, const RowMeta& meta, const PagedKv& kv, int layer,
+                  const FastAttentionWork& w, float* out, int ldo) {
+    fast_attention_kernel<G><<<(w.items_count + kItemsPerGroup - 1) / kItemsPerGroup, kItemsPerGroup * 64, 0, s>>>(
+        qkv, ldq, meta, kv, layer, w, out, ldo);
 }
 
 }  // namespace
+
+int fast_attention_split_tokens() { return kSplitTokens; }
 
 hipError_t launch_fast_attention(hipStream_t s, const float* qkv, int ldq, int rows, int heads, int kv_heads,
                                  const RowMeta& meta, const PagedKv& kv, int layer, float* out, int ldo,
                                  const FastAttentionWork& w) {
     const int G = heads / kv_heads;
     if (rows <= 0) return hipSuccess;
-    if (kv.block_tokens != kPage || kv.kv_width != kv_heads * kDim || G > kMaxGroup || G < 1)
+    if (kv.block_tokens != kPage || kv.kv_width != kv_heads * kDim || G > kMaxGroup || G < 1 ||
+        G * kv_heads != heads || w.kv_heads != kv_heads)
         return hipErrorInvalidValue;
     switch (G) {
-    case 1: launch_split<1>(s, qkv, ldq, heads, meta, kv, layer, w); break;
-    case 2: launch_split<2>(s, qkv, ldq, heads, meta, kv, layer, w); break;
-    case 3: launch_split<3>(s, qkv, ldq, heads, meta, kv, layer, w); break;
-    default: launch_split<4>(s, qkv, ldq, heads, meta, kv, layer, w); break;
+    case 1: launch_items<1>(s, qkv, ldq, meta, kv, layer, w, out, ldo); break;
+    case 2: launch_items<2>(s, qkv, ldq, meta, kv, layer, w, out, ldo); break;
+    case 3: launch_items<3>(s, qkv, ldq, meta, kv, layer, w, out, ldo); break;
+    default: launch_items<4>(s, qkv, ldq, meta, kv, layer, w, out, ldo); break;
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    fast_attention_merge_kernel<<<rows, 256, 0, s>>>(heads, kv_heads, w, out, ldo);
+    fast_attention_merge_kernel<<<(rows * heads + 3) / 4, 256, 0, s>>>(rows, heads, kv_heads, w, out, ldo);
     return hipGetLastError();
 }
 

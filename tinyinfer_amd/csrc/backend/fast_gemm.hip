@@ -10,168 +10,355 @@
 // row (A) and its column (B); MFMA j of a 16-k step takes component j of
 // both, so the four lane groups l/16 cover k, k+4, k+8, k+12 of the step.
 //
-// A work-group of four wavefronts computes 16 rows x 16 columns: the
-// wavefronts take the 16-k steps of K in turn (step s to wavefront s % 4)
-// and sum their 16x16 partials through LDS in wavefront order. Activations
-// are in the row-tile quad layout (layout.h), projection weights [n][k].
-// Work-groups are laid out so that those sharing a column block (one per
-// 16-row block) are dispatched to the same XCD and share its L2 for the
+// A work-group of eight wavefronts computes RB 16-row blocks x CB 16-column
+// blocks. The 16-k steps of K are dealt to the wavefronts in turn (step s to
+// wavefront s % 8) and a wavefront issues the loads of all its steps (up to
+// CH at a time) before its first multiply: at decode sizes a projection is
+// bound by memory latency, not bandwidth, so the loads of a launch must be
+// in flight together, and so are everything the epilogue reads (RMSNorm
+// partials, the residual's old values, the RoPE rows). The partial tiles
+// are then summed through LDS in a fixed order: wavefronts 4-7 into 0-3,
+// then the final sum of each tile ((p0 + p1) + (p2 + p3)) by the wavefront
+// that owns its row block (row block rb to wavefront rb % min(RB, 4)), which
+// runs the epilogue for it. A row's result depends on nothing but the row.
+//
+// Work-groups are laid out so that those sharing a column group (one per
+// row group) are dispatched to the same XCD and share its L2 for the
 // weights: work-group b runs on XCD b % 8, and the 8-strided sequence of one
-// XCD walks the row blocks of a column block first.
+// XCD walks the row groups of a column group first.
 //
 // Epilogues: store; residual (x += result) writing, for the next RMSNorm,
-// the sum of squares of the updated x over the block's 16 columns; SwiGLU
-// (gate and up accumulated side by side); LM head (per row and block, the
-// first maximum and a non-finite flag, logits row-major on request).
+// the sum of squares of the updated x over each 16-column block; SwiGLU
+// (gate and up accumulated side by side); LM head (per row and column group
+// of 16*CB columns, the first maximum and a non-finite flag, logits
+// row-major on request); RoPE (the q|k|v projection of a decode step:
+// column blocks j and j+2 of a 64-wide head are computed together, so each
+// split-half pair (d, d+32) is in one lane; q is rotated in place, the
+// rotated k and the v go to the paged pools at the row's position).
 // RMSNorm on the input (NORM): a[r][k] = x[r][k] * g[k], and the result is
 // scaled by 1/sqrt(sum_k x[r][k]^2 / K + eps), the sum assembled from the
 // producer's per-block partials.
 #include "kernels.h"
+#include "lanes.h"
 #include "layout.h"
+
+// The fast mode's own summation order: multiply-adds may be fused.
+#pragma clang fp contract(fast)
 
 namespace mphip {
 namespace {
 
 typedef float f4 __attribute__((ext_vector_type(4)));
 
-constexpr int kWaves = 4;
+constexpr int kWaves = 8;
 constexpr int kXcds = 8;
+constexpr int kRopeDim = 64;
+constexpr int kSsqSlots = 8;  // threads per row summing the RMSNorm partials
+constexpr int kSsqHeld = 8;   // partials per thread loaded up front (hidden <= 1024)
 
 __device__ __forceinline__ f4 ld4(const float* p) { return *reinterpret_cast<const f4*>(p); }
 
-template <int EPI, bool NORM, bool GATHER>
+// Order-preserving key of a finite float (larger value -> larger key; -0 is
+// taken as +0) with the column in the low half (smaller column -> larger
+// key), so that the maximum key is the first maximum. 0 means no finite
+// value.
+__device__ __forceinline__ uint64_t argmax_key(float v, int col) {
+    const uint32_t u = __float_as_uint(v == 0.0f ? 0.0f : v);
+    const uint32_t k = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((uint64_t)k << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)col);
+}
+__device__ __forceinline__ float key_value(uint64_t key) {
+    const uint32_t k = (uint32_t)(key >> 32);
+    return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
+}
+
+// The larger of this lane's key and the key of the lane DPP control kCtrl
+// names (the reduction steps of a 16-lane row).
+template <int kCtrl>
+__device__ __forceinline__ uint64_t max_key(uint64_t key) {
+    const uint64_t k = ((uint64_t)dpp_u<kCtrl>((uint32_t)(key >> 32)) << 32) | dpp_u<kCtrl>((uint32_t)key);
+    return k > key ? k : key;
+}
+
+template <int EPI, bool NORM, bool GATHER, int RB, int CB, int CH>
 __global__ __launch_bounds__(kWaves * 64) void fast_gemm_kernel(FastGemmArgs a) {
     constexpr int M = EPI == kSwiglu ? 2 : 1;
-    __shared__ f4 part_s[kWaves - 1][M][64];
-    __shared__ float inv_s[16];
+    constexpr int NB = CB * M;  // B operands per step
+    constexpr int T = RB * NB;  // accumulator tiles
+    constexpr int OW = RB < 4 ? RB : 4;  // wavefronts that own row blocks
+    __shared__ f4 part_s[kWaves / 2][T][64];
+    __shared__ float ssq_s[NORM ? RB * 16 : 1][kSsqSlots];
+    __shared__ float inv_s[RB * 16];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    // Work-group -> (row block, column block), XCD-grouped.
-    const int nrb = (a.rows + 15) >> 4;
-    const int ncb = a.columns >> 4;
+    // Work-group -> (row group, column group), XCD-grouped.
+    const int nrg = (((a.rows + 15) >> 4) + RB - 1) / RB;
+    const int ncg = (a.columns >> 4) / CB;
     const int b = blockIdx.x;
     const int g = b / kXcds, xcd = b % kXcds;
-    const int rb = g % nrb;
-    const int cb = (g / nrb) * kXcds + xcd;
-    if (cb >= ncb) return;
+    const int rg = g % nrg;
+    const int cg = (g / nrg) * kXcds + xcd;
+    if (cg >= ncg) return;
+    int cblock[CB];
+#pragma unroll
+    for (int j = 0; j < CB; ++j) cblock[j] = EPI == kRope ? 4 * (cg >> 1) + (cg & 1) + 2 * j : cg * CB + j;
+    const int row0 = rg * RB * 16;
     const int K = a.inner, Q = K >> 2, steps = K >> 4;
-    // A: row rb*16 + l%16 (gathered), quads 4s + l/16.
-    const int row_a = min(rb * 16 + (lane & 15), a.rows - 1);
-    const int xrow = GATHER ? a.row_map[row_a] : row_a;
-    const float* xa = a.x + ((size_t)(xrow >> 6) * Q * 64 + (xrow & 63)) * 4 + (size_t)(lane >> 4) * 256;
-    // B: column cb*16 + l%16, k 16s + 4(l/16).
-    const size_t wcol = (size_t)(cb * 16 + (lane & 15)) * K + (size_t)(lane >> 4) * 4;
-    const float* wb = a.w + wcol;
-    const float* wb2 = M == 2 ? a.w2 + wcol : nullptr;
+    // A: row row0 + 16rb + l%16 (gathered), quads 4s + l/16.
+    const float* xa[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+        const int r = min(row0 + rb * 16 + (lane & 15), a.rows - 1);
+        const int xrow = GATHER && a.row_map ? a.row_map[r] : r;
+        xa[rb] = a.x + ((size_t)(xrow >> 6) * Q * 64 + (xrow & 63)) * 4 + (size_t)(lane >> 4) * 256;
+    }
+    // B: column 16cblock + l%16, k 16s + 4(l/16).
+    const float* wb[NB];
+#pragma unroll
+    for (int j = 0; j < CB; ++j) {
+        const size_t off = (size_t)(cblock[j] * 16 + (lane & 15)) * K + (size_t)(lane >> 4) * 4;
+        wb[j * M] = a.w + off;
+        if (M == 2) wb[j * M + M - 1] = a.w2 + off;
+    }
     const float* gn = NORM ? a.norm + (lane >> 4) * 4 : nullptr;
-    if (NORM && threadIdx.x < 16) {
-        // 1/sqrt(mean square + eps) of the block's rows from the producer's partials.
-        const int r = min(rb * 16 + (int)threadIdx.x, a.rows - 1);
-        const int pr = GATHER ? a.row_map[r] : r;
-        float ss = 0.0f;
-        for (int p = 0; p < a.ssq_parts; ++p) ss += a.ssq_in[(size_t)p * a.ssq_stride + pr];
-        inv_s[threadIdx.x] = 1.0f / sqrtf(ss / (float)K + a.eps);
-    }
-
-    f4 acc[M];
+    // RMSNorm: the producer's per-16-column partial sums of squares of each
+    // row, summed by 8 threads per row (slot u takes partials u, u+8, ...).
+    // The order of the sums is fixed per row (slots in order), whatever RB is.
+    const int ssq_row = threadIdx.x / kSsqSlots, ssq_slot = threadIdx.x % kSsqSlots;
+    float ssv[kSsqHeld];
+    if (NORM) {
+        const int r = min(row0 + ssq_row, a.rows - 1);
+        const int pr = GATHER && a.row_map ? a.row_map[r] : r;
 #pragma unroll
-    for (int m = 0; m < M; ++m) acc[m] = f4{0.f, 0.f, 0.f, 0.f};
-    // Two steps in flight: this wavefront's next step loads while one multiplies.
-    auto load = [&](int s, f4& av, f4 (&bv)[M]) {
-        av = ld4(xa + (size_t)s * 1024);  // 4 quads of 64 rows x 4 floats
-        if (NORM) av = av * ld4(gn + (size_t)s * 16);
-        bv[0] = __builtin_nontemporal_load(reinterpret_cast<const f4*>(wb + (size_t)s * 16));
-        if (M == 2) bv[M - 1] = __builtin_nontemporal_load(reinterpret_cast<const f4*>(wb2 + (size_t)s * 16));
-    };
-    auto mma = [&](const f4& av, const f4 (&bv)[M]) {
-#pragma unroll
-        for (int m = 0; m < M; ++m) {
-            acc[m] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.x, bv[m].x, acc[m], 0, 0, 0);
-            acc[m] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.y, bv[m].y, acc[m], 0, 0, 0);
-            acc[m] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.z, bv[m].z, acc[m], 0, 0, 0);
-            acc[m] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.w, bv[m].w, acc[m], 0, 0, 0);
-        }
-    };
-    int s = wave;
-    if (s < steps) {
-        f4 a0, a1, b0[M], b1[M];
-        load(s, a0, b0);
-        for (;;) {
-            const int s1 = s + kWaves;
-            if (s1 < steps) load(s1, a1, b1);
-            mma(a0, b0);
-            if (s1 >= steps) break;
-            const int s2 = s1 + kWaves;
-            if (s2 < steps) load(s2, a0, b0);
-            mma(a1, b1);
-            if (s2 >= steps) break;
-            s = s2;
+        for (int u = 0; u < kSsqHeld; ++u) {
+            const int p = ssq_slot + u * kSsqSlots;
+            ssv[u] = ssq_row < RB * 16 && p < a.ssq_parts ? a.ssq_in[(size_t)p * a.ssq_stride + pr] : 0.0f;
         }
     }
-    // Partials of wavefronts 1..3 to LDS; wavefront 0 adds them in order.
-    if (wave > 0)
+    // The residual's old values (small tiles: wavefront 0 owns the only row block).
+    constexpr bool kEarly = EPI == kResidual && RB * CB == 1;
+    float old[4];
+    if (kEarly && wave == 0) {
 #pragma unroll
-        for (int m = 0; m < M; ++m) part_s[wave - 1][m][lane] = acc[m];
-    __syncthreads();
-    if (wave > 0) return;
+        for (int i = 0; i < 4; ++i) {
+            const int row = min(row0 + 4 * (lane >> 4) + i, a.rows - 1);
+            old[i] = a.out[quad_index(row, cblock[0] * 16 + (lane & 15), a.columns)];
+        }
+    }
+    // RoPE rows of the owned row block: position, page and rotation
+    // (cos, sin of dim d = 16(cg&1) + l%16 at the row's position).
+    int rope_pos[4], rope_block[4];
+    float rope_cs[4], rope_sn[4];
+    if (EPI == kRope && wave < OW) {
+        const int d = (cg & 1) * 16 + (lane & 15);
 #pragma unroll
-    for (int w = 0; w < kWaves - 1; ++w)
-#pragma unroll
-        for (int m = 0; m < M; ++m) acc[m] += part_s[w][m][lane];
+        for (int i = 0; i < 4; ++i) {
+            const int row = min(row0 + wave * 16 + 4 * (lane >> 4) + i, a.rows - 1);
+            rope_pos[i] = a.meta.row_pos[row];
+            rope_block[i] = a.row_block[row];
+            rope_cs[i] = a.row_rope[(size_t)row * kRopeDim + d];
+            rope_sn[i] = a.row_rope[(size_t)row * kRopeDim + kRopeDim / 2 + d];
+        }
+    }
 
-    // Lane l, register i: row rb*16 + 4(l/16) + i, column cb*16 + l%16.
-    const int col = cb * 16 + (lane & 15);
-    const int N = a.columns;
+    f4 acc[T];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int rl = 4 * (lane >> 4) + i;
-        const int row = rb * 16 + rl;
-        const bool live = row < a.rows;
-        float v[M];
+    for (int t = 0; t < T; ++t) acc[t] = f4{0.f, 0.f, 0.f, 0.f};
+    const int mine = steps > wave ? (steps - wave + kWaves - 1) / kWaves : 0;  // this wavefront's steps
+    for (int i0 = 0; i0 < mine; i0 += CH) {
+        f4 av[CH][RB], bv[CH][NB], gv[CH];
 #pragma unroll
-        for (int m = 0; m < M; ++m) v[m] = NORM ? acc[m][i] * inv_s[rl] : acc[m][i];
-        if (EPI == kStore) {
-            if (live) a.out[quad_index(row, col, N)] = v[0];
-        } else if (EPI == kResidual) {
-            float nx = 0.0f;
-            if (live) {
-                float* o = a.out + quad_index(row, col, N);
-                nx = *o + v[0];
-                *o = nx;
+        for (int c = 0; c < CH; ++c) {
+            if (i0 + c < mine) {
+                const size_t s = wave + (size_t)kWaves * (i0 + c);
+                if (NORM) gv[c] = ld4(gn + s * 16);
+#pragma unroll
+                for (int rb = 0; rb < RB; ++rb) av[c][rb] = ld4(xa[rb] + s * 1024);  // 4 quads x 64 rows x 4
+#pragma unroll
+                for (int j = 0; j < NB; ++j)
+                    bv[c][j] = __builtin_nontemporal_load(reinterpret_cast<const f4*>(wb[j] + s * 16));
             }
-            // The row's 16 columns sit in the 16 lanes of this lane's group.
-            float sq = nx * nx;
-            sq += __shfl_xor(sq, 1);
-            sq += __shfl_xor(sq, 2);
-            sq += __shfl_xor(sq, 4);
-            sq += __shfl_xor(sq, 8);
-            if (live && (lane & 15) == 0) a.ssq_out[(size_t)cb * a.ssq_stride + row] = sq;
-        } else if (EPI == kSwiglu) {
-            const float gt = v[0];
-            if (live) a.out[quad_index(row, col, N)] = (gt / (1.0f + __expf(-gt))) * v[M - 1];
-        } else {  // kHead
-            const float x = v[0];
-            const bool finite = __builtin_isfinite(x);
-            if (live && a.logits) a.logits[(size_t)row * N + col] = x;
-            // First maximum of the row's 16 columns (finite values only).
-            float bv = finite ? x : -__builtin_inff();
-            int bi = finite ? col : -1;
-            int bad = finite ? 0 : 1;
+        }
 #pragma unroll
-            for (int o = 1; o < 16; o <<= 1) {
-                const float ov = __shfl_xor(bv, o);
-                const int oi = __shfl_xor(bi, o);
-                bad |= __shfl_xor(bad, o);
-                if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) {
-                    bv = ov;
-                    bi = oi;
+        for (int c = 0; c < CH; ++c) {
+            if (i0 + c < mine) {
+#pragma unroll
+                for (int rb = 0; rb < RB; ++rb) {
+                    const f4 x = NORM ? av[c][rb] * gv[c] : av[c][rb];
+#pragma unroll
+                    for (int j = 0; j < NB; ++j) {
+                        f4& d = acc[rb * NB + j];
+                        d = __builtin_amdgcn_mfma_f32_16x16x4f32(x.x, bv[c][j].x, d, 0, 0, 0);
+                        d = __builtin_amdgcn_mfma_f32_16x16x4f32(x.y, bv[c][j].y, d, 0, 0, 0);
+                        d = __builtin_amdgcn_mfma_f32_16x16x4f32(x.z, bv[c][j].z, d, 0, 0, 0);
+                        d = __builtin_amdgcn_mfma_f32_16x16x4f32(x.w, bv[c][j].w, d, 0, 0, 0);
+                    }
                 }
             }
-            if (live && (lane & 15) == 0) {
-                const size_t at = (size_t)row * a.groups + cb;
-                a.best_value[at] = bv;
-                a.best_index[at] = bi;
-                a.bad[at] = bad;
+        }
+    }
+    if (NORM) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int u = 0; u < kSsqHeld; ++u) ss += ssv[u];
+        if (ssq_row < RB * 16) {
+            const int r = min(row0 + ssq_row, a.rows - 1);
+            const int pr = GATHER && a.row_map ? a.row_map[r] : r;
+            for (int p = ssq_slot + kSsqHeld * kSsqSlots; p < a.ssq_parts; p += kSsqSlots)
+                ss += a.ssq_in[(size_t)p * a.ssq_stride + pr];
+            ssq_s[ssq_row][ssq_slot] = ss;
+        }
+    }
+    // Wavefronts 4-7 into 0-3.
+    if (wave >= kWaves / 2)
+#pragma unroll
+        for (int t = 0; t < T; ++t) part_s[wave - kWaves / 2][t][lane] = acc[t];
+    __syncthreads();
+    if (wave < kWaves / 2)
+#pragma unroll
+        for (int t = 0; t < T; ++t) acc[t] += part_s[wave][t][lane];
+    if (NORM && threadIdx.x < RB * 16) {
+        // 1/sqrt(mean square + eps) of the group's rows.
+        float ss = 0.0f;
+#pragma unroll
+        for (int u = 0; u < kSsqSlots; ++u) ss += ssq_s[threadIdx.x][u];
+        inv_s[threadIdx.x] = 1.0f / sqrtf(ss / (float)K + a.eps);
+    }
+    __syncthreads();
+    // Then each tile's four partials to its owner.
+    if (wave < kWaves / 2)
+#pragma unroll
+        for (int t = 0; t < T; ++t) part_s[wave][t][lane] = acc[t];
+    __syncthreads();
+    if (wave >= OW) return;
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+        if (rb % OW != wave) continue;
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            const int t = rb * NB + j;
+            acc[t] = (part_s[0][t][lane] + part_s[1][t][lane]) + (part_s[2][t][lane] + part_s[3][t][lane]);
+        }
+    }
+
+    const int N = a.columns;
+    if (EPI == kRope) {
+        // acc[2rb] holds dims d = 16(cg&1) + l%16 of head cg>>1, acc[2rb+1]
+        // dims d + 32 (head dim 64, split-half rotation). RB <= 4 here, so
+        // wavefront w owns row block w.
+        const int rb = wave;
+        const int hcol = (cg >> 1) * kRopeDim;
+        const int d = (cg & 1) * 16 + (lane & 15);
+        const int hidden = a.heads * kRopeDim, kvw = a.kv.kv_width;
+        const int bt = a.kv.block_tokens;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int rl = 4 * (lane >> 4) + i;
+            const int row = row0 + rb * 16 + rl;
+            if (row >= a.rows) continue;
+            const float inv = inv_s[rb * 16 + rl];
+            float x0 = 0.0f, x1 = 0.0f;
+#pragma unroll
+            for (int r2 = 0; r2 < RB; ++r2)
+                if (r2 == rb) {
+                    x0 = acc[2 * r2][i] * inv;
+                    x1 = acc[2 * r2 + 1][i] * inv;
+                }
+            const float cs = rope_cs[i], sn = rope_sn[i];
+            const float y0 = x0 * cs - x1 * sn, y1 = x1 * cs + x0 * sn;
+            if (hcol < hidden) {
+                a.out[quad_index(row, hcol + d, N)] = y0;
+                a.out[quad_index(row, hcol + d + kRopeDim / 2, N)] = y1;
+                continue;
+            }
+            const size_t base = kv_page_base(rope_block[i], a.layer, a.kv.layers, bt, kvw);
+            const int slot = rope_pos[i] % bt;
+            if (hcol < hidden + kvw) {
+                const int kvh = (hcol - hidden) / kRopeDim;
+                a.kv.keys[base + key_offset(slot, kvh, d, bt, kRopeDim)] = y0;
+                a.kv.keys[base + key_offset(slot, kvh, d + kRopeDim / 2, bt, kRopeDim)] = y1;
+            } else {
+                const int kvh = (hcol - hidden - kvw) / kRopeDim;
+                a.kv.values[base + value_offset(slot, kvh, d, bt, kRopeDim)] = x0;
+                a.kv.values[base + value_offset(slot, kvh, d + kRopeDim / 2, bt, kRopeDim)] = x1;
+            }
+        }
+        return;
+    }
+    if (EPI == kHead) {
+        // Per row of the owned row blocks: the first maximum over the column
+        // group's 16*CB columns (lane: columns cblock[j]*16 + l%16, j in
+        // order), then across the 16 lanes of the row's lane group.
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+            if (rb % OW != wave) continue;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int rl = 4 * (lane >> 4) + i;
+                const int row = row0 + rb * 16 + rl;
+                const bool live = row < a.rows;
+                const float inv = NORM ? inv_s[rb * 16 + rl] : 1.0f;
+                uint64_t key = 0;
+                bool bad = false;
+#pragma unroll
+                for (int j = 0; j < CB; ++j) {
+                    const float x = acc[rb * NB + j][i] * inv;
+                    const int col = cblock[j] * 16 + (lane & 15);
+                    if (live && a.logits) a.logits[(size_t)row * N + col] = x;
+                    const bool finite = __builtin_isfinite(x);
+                    bad |= !finite;
+                    const uint64_t k = finite ? argmax_key(x, col) : 0;
+                    key = k > key ? k : key;
+                }
+                key = max_key<kDppQuadXor1>(key);
+                key = max_key<kDppQuadXor2>(key);
+                key = max_key<kDppRowRor4>(key);
+                key = max_key<kDppRowRor8>(key);
+                const uint64_t bads = __ballot(bad);
+                if (live && (lane & 15) == 0) {
+                    const size_t at = (size_t)row * a.groups + cg;
+                    a.best_value[at] = key ? key_value(key) : -__builtin_inff();
+                    a.best_index[at] = key ? (int)(0xFFFFFFFFu - (uint32_t)key) : -1;
+                    a.bad[at] = ((bads >> (lane & 48)) & 0xFFFFull) != 0;
+                }
+            }
+        }
+        return;
+    }
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+        if (rb % OW != wave) continue;
+#pragma unroll
+        for (int j = 0; j < CB; ++j) {
+            // Lane l, register i: row row0 + 16rb + 4(l/16) + i, column 16cblock + l%16.
+            const int col = cblock[j] * 16 + (lane & 15);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int rl = 4 * (lane >> 4) + i;
+                const int row = row0 + rb * 16 + rl;
+                const bool live = row < a.rows;
+                float v[M];
+#pragma unroll
+                for (int m = 0; m < M; ++m) {
+                    const float s = acc[rb * NB + j * M + m][i];
+                    v[m] = NORM ? s * inv_s[rb * 16 + rl] : s;
+                }
+                if (EPI == kStore) {
+                    if (live) a.out[quad_index(row, col, N)] = v[0];
+                } else if (EPI == kResidual) {
+                    float nx = 0.0f;
+                    if (live) {
+                        float* o = a.out + quad_index(row, col, N);
+                        nx = (kEarly ? old[i] : *o) + v[0];
+                        *o = nx;
+                    }
+                    // The row's 16 columns sit in the 16 lanes of this lane's group.
+                    const float sq = row_sum(nx * nx);
+                    if (live && (lane & 15) == 0) a.ssq_out[(size_t)cblock[j] * a.ssq_stride + row] = sq;
+                } else {  // kSwiglu
+                    const float gt = v[0];
+                    if (live) a.out[quad_index(row, col, N)] = (gt / (1.0f + __expf(-gt))) * v[M - 1];
+                }
             }
         }
     }
@@ -194,17 +381,38 @@ __global__ __launch_bounds__(256) void fast_ssq_kernel(const float* __restrict__
     ssq[(size_t)p * stride + r] = s;
 }
 
-template <int EPI, bool NORM, bool GATHER>
+template <int EPI, bool NORM, bool GATHER, int RB, int CB, int CH>
 hipError_t launch_fast(hipStream_t s, const FastGemmArgs& a) {
-    const int nrb = (a.rows + 15) / 16;
-    const int ncb = a.columns / 16;
-    const int per_xcd = (ncb + kXcds - 1) / kXcds;  // column blocks per XCD
-    const int blocks = per_xcd * nrb * kXcds;
-    fast_gemm_kernel<EPI, NORM, GATHER><<<blocks, kWaves * 64, 0, s>>>(a);
+    const int nrg = ((a.rows + 15) / 16 + RB - 1) / RB;
+    const int ncg = a.columns / 16 / CB;
+    const int blocks = (ncg + kXcds - 1) / kXcds * nrg * kXcds;
+    fast_gemm_kernel<EPI, NORM, GATHER, RB, CB, CH><<<blocks, kWaves * 64, 0, s>>>(a);
     return hipGetLastError();
 }
 
+// Tile shape by size. At decode sizes (one row tile) the tiles are small,
+// for many work-groups (SwiGLU takes two row blocks: its two weight
+// matrices make its column blocks the heaviest); the LM head and any
+// projection of more than one row tile take 64-row x 64-column tiles, which
+// read each weight and each activation a quarter as often.
+bool head_wide(int columns) { return columns % 64 == 0; }
+
+template <int EPI, bool NORM, bool GATHER>
+hipError_t launch_sized(hipStream_t s, const FastGemmArgs& a) {
+    constexpr int M = EPI == kSwiglu ? 2 : 1;
+    if constexpr (EPI == kHead) {
+        if (head_wide(a.columns)) return launch_fast<EPI, NORM, GATHER, 4, 4, 3>(s, a);
+        return launch_fast<EPI, NORM, GATHER, 1, 1, 6>(s, a);
+    } else {
+        if (a.rows > 64 && a.columns % 64 == 0) return launch_fast<EPI, NORM, GATHER, 4, 4 / M, 3>(s, a);
+        if constexpr (M == 2) return launch_fast<EPI, NORM, GATHER, 2, 1, 6>(s, a);
+        return launch_fast<EPI, NORM, GATHER, 1, 1, 12>(s, a);
+    }
+}
+
 }  // namespace
+
+int fast_head_group_columns(int columns) { return head_wide(columns) ? 64 : 16; }
 
 bool fast_gemm_fits(const FastGemmArgs& a) {
     return a.rows > 0 && a.inner > 0 && a.inner % 16 == 0 && a.columns > 0 && a.columns % 16 == 0;
@@ -214,10 +422,19 @@ hipError_t launch_fast_gemm(hipStream_t s, Epilogue epilogue, const FastGemmArgs
     if (!fast_gemm_fits(a)) return hipErrorInvalidValue;
     const bool norm = a.norm != nullptr;
     switch (epilogue) {
-    case kStore: return norm ? launch_fast<kStore, true, false>(s, a) : launch_fast<kStore, false, false>(s, a);
-    case kResidual: return launch_fast<kResidual, false, false>(s, a);
-    case kSwiglu: return norm ? launch_fast<kSwiglu, true, false>(s, a) : launch_fast<kSwiglu, false, false>(s, a);
-    case kHead: return launch_fast<kHead, true, true>(s, a);
+    case kStore: return norm ? launch_sized<kStore, true, false>(s, a) : launch_sized<kStore, false, false>(s, a);
+    case kResidual: return launch_sized<kResidual, false, false>(s, a);
+    case kSwiglu: return norm ? launch_sized<kSwiglu, true, false>(s, a) : launch_sized<kSwiglu, false, false>(s, a);
+    case kHead:
+        if (a.groups != a.columns / fast_head_group_columns(a.columns)) return hipErrorInvalidValue;
+        return launch_sized<kHead, true, true>(s, a);
+    case kRope:
+        // q|k|v of 64-wide heads: column groups pair blocks j and j+2 of a head.
+        if (a.columns % kRopeDim || a.heads * kRopeDim + 2 * a.kv.kv_width != a.columns || !norm ||
+            a.kv.block_tokens <= 0 || !a.row_block || !a.row_rope)
+            return hipErrorInvalidValue;
+        if (a.rows > 64) return launch_fast<kRope, true, false, 4, 2, 3>(s, a);
+        return launch_fast<kRope, true, false, 1, 2, 6>(s, a);
     }
     return hipErrorInvalidValue;
 }

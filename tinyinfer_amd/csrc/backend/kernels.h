@@ -29,7 +29,8 @@ struct PagedKv {
     int32_t layers, block_tokens, kv_width;
 };
 
-enum Epilogue { kStore = 0, kResidual = 1, kSwiglu = 2, kHead = 3 };
+// kRope is of the fast mode only (launch_fast_gemm).
+enum Epilogue { kStore = 0, kResidual = 1, kSwiglu = 2, kHead = 3, kRope = 4 };
 
 // out[r][n] = epilogue(sum_k x[r][k] * w[n][k]) with k accumulated in order
 // from 0, multiply and add rounded separately. x is `rows` x `inner` (quad
@@ -75,9 +76,17 @@ hipError_t launch_head_argmax(hipStream_t s, const GemmArgs& args, int32_t* argm
 //   ssq_in[p*ssq_stride + row] (written by the producer of x).
 // - kResidual: out += result, and ssq_out[c*ssq_stride + row] = sum of
 //   squares of the updated row over columns 16c..16c+15.
-// - kHead: row i of the result reads x row row_map[i]; per row and 16-column
-//   block, the first maximum into best_value/best_index/bad [rows][groups]
-//   (groups = columns/16), logits written when `logits` is non-null.
+// - kHead: row i of the result reads x row row_map[i] (row i when row_map is
+//   null); per row and column group, the first maximum into
+//   best_value/best_index/bad [rows][groups], logits written when `logits`
+//   is non-null
+//   (groups = columns/fast_head_group_columns(columns)).
+// - kRope (norm required; head dim 64; columns = q|k|v of `heads` query and
+//   kv.kv_width/64 KV heads): split-half RoPE at meta.row_pos with the
+//   per-row rotation row_rope[row][64] (cos of dims 0..31, then sin) and
+//   page row_block[row] (launch_embed writes both); rotated q into out (quad
+//   layout), rotated k and v into the pools of `kv` at `layer` and the
+//   row's position.
 struct FastGemmArgs {
     const float* x;
     const float* w;
@@ -95,8 +104,15 @@ struct FastGemmArgs {
     int32_t* best_index;
     int32_t* bad;
     int groups;
+    RowMeta meta;
+    PagedKv kv;
+    int layer, heads;
+    const int32_t* row_block;
+    const float* row_rope;
 };
 bool fast_gemm_fits(const FastGemmArgs& args);
+// Columns per LM-head argmax group of the fast head.
+int fast_head_group_columns(int columns);
 hipError_t launch_fast_gemm(hipStream_t s, Epilogue epilogue, const FastGemmArgs& args);
 // Per-16-column sums of squares of x's rows (quad layout, `width` columns)
 // into ssq[p*stride + row], for the first RMSNorm after the embedding.
@@ -104,25 +120,44 @@ hipError_t launch_fast_ssq(hipStream_t s, const float* x, int rows, int width, f
 
 // Fast-mode decode attention (fast_attention.hip): every row is one new
 // token (already rotated q, its K/V already in the pools). Flash-decoding
-// split over the context: work item (row, KV head, split of `split` tokens)
-// keeps a running maximum, denominator and output per query head; then one
-// merge per (row, head). Scratch: partial outputs [items][group][dim] and
-// (max, denominator) pairs [items][group][2]. head dim 64, page 16.
+// split over the context: work item (row, KV head, split of
+// fast_attention_split_tokens() tokens, page-aligned) computes a maximum,
+// denominator and output per query head; a merge kernel combines the splits
+// of every (row, head). Scratch: partial outputs [items][group][dim] and
+// (max, denominator) pairs [items][group][2]. Head dim 64, page 16.
 struct FastAttentionWork {
-    const int32_t* items;  // per work item: row, kv head, first token, token count (int4)
+    // per work item (int4): row, table slot * kv_heads + KV head, first token, token count;
+    // the items of a row are KV head major, then split order
+    const int32_t* items;
     int items_count;
-    const int32_t* row_items;  // per row: first work item of kv head 0 and splits per kv head (int2)
+    const int32_t* row_items;  // per row: first work item and splits per KV head (int2)
     float* partial_out;
     float* partial_ml;
+    int kv_heads;
 };
+int fast_attention_split_tokens();
 hipError_t launch_fast_attention(hipStream_t s, const float* qkv, int ldq, int rows, int heads, int kv_heads,
                                  const RowMeta& meta, const PagedKv& kv, int layer, float* out, int ldo,
                                  const FastAttentionWork& work);
 
+// Per-row RoPE inputs of a forward for the fast q|k|v projection: for row r
+// at position p = meta.row_pos[r], block[r] = the page holding p (from the
+// row's sequence table) and rope[r][0..half) = cos_table[p][..],
+// rope[r][half..2half) = sin_table[p][..].
+struct RowRope {
+    RowMeta meta;
+    const int32_t* tables;
+    int32_t table_stride, block_tokens, half;
+    const float* cos_table;
+    const float* sin_table;
+    int32_t* block;
+    float* rope;
+};
+
 // x = embedding rows of `tokens`; also clears the forward's device error
-// word `error` (may be null).
+// word `error` (may be null) and fills `rope` when it is non-null.
 hipError_t launch_embed(hipStream_t s, const float* embedding, const int32_t* tokens, float* x, int rows,
-                        int hidden, int32_t* error);
+                        int hidden, int32_t* error, const RowRope* rope = nullptr);
 
 // out[r] = (x[r']*scale_r')*w with scale = 1/sqrt(sequential sum of squares/width + eps);
 // r' = row_map[r] when row_map is non-null, else r.

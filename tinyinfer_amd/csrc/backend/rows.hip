@@ -16,8 +16,23 @@ namespace {
 __global__ __launch_bounds__(256) void embed_kernel(const float* __restrict__ embedding,
                                                     const int32_t* __restrict__ tokens,
                                                     float* __restrict__ x, int rows, int hidden,
-                                                    int32_t* __restrict__ error) {
+                                                    int32_t* __restrict__ error, RowRope rope) {
     if (error && blockIdx.x == 0 && threadIdx.x == 0) *error = 0;
+    if (rope.rope) {
+        const int per = 2 * rope.half + 1;  // cos, sin, then the page
+        for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < rows * per; i += gridDim.x * blockDim.x) {
+            const int r = i / per, c = i % per;
+            const int pos = rope.meta.row_pos[r];
+            if (c < 2 * rope.half) {
+                const float* src = c < rope.half ? rope.cos_table : rope.sin_table;
+                rope.rope[(size_t)r * 2 * rope.half + c] = src[(size_t)pos * rope.half + c % rope.half];
+            } else {
+                const int32_t* table =
+                    rope.tables + (size_t)rope.meta.seq_slot[rope.meta.row_seq[r]] * rope.table_stride;
+                rope.block[r] = table[pos / rope.block_tokens];
+            }
+        }
+    }
     const int quads = hidden >> 2;
     const size_t total = (size_t)((rows + 63) >> 6) * quads * 64;
     float4* x4 = reinterpret_cast<float4*>(x);
@@ -261,11 +276,13 @@ __global__ void transpose_kernel(const float* __restrict__ src, float* __restric
 }  // namespace
 
 hipError_t launch_embed(hipStream_t s, const float* embedding, const int32_t* tokens, float* x, int rows,
-                        int hidden, int32_t* error) {
+                        int hidden, int32_t* error, const RowRope* rope) {
     if (rows <= 0) return hipSuccess;
     const size_t total = quad_floats(rows, hidden) / 4;
     const int blocks = (int)std::min<size_t>((total + 255) / 256, 4096);
-    embed_kernel<<<blocks, 256, 0, s>>>(embedding, tokens, x, rows, hidden, error);
+    RowRope rr{};
+    if (rope) rr = *rope;
+    embed_kernel<<<blocks, 256, 0, s>>>(embedding, tokens, x, rows, hidden, error, rr);
     return hipGetLastError();
 }
 
