@@ -1,12 +1,22 @@
-"""Batch-64 FP32 decode throughput of a SmolLM2-135M-shaped model through the
-MiniPrefix engine on one MI355X (HIP runner), with the paged-attention
-roofline and the CPU baseline.
+"""FP32 decode throughput of a SmolLM2-135M-shaped model through the
+MiniPrefix engine on one MI355X (HIP runner), with the roofline of the
+paged attention and of the projections, and the reference CPU path timed on
+the host beside it.
 
-Workload (one step = one engine step in which all 64 requests decode one
-token): 64 requests, prompt lengths uniform in [256, 2048], token ids uniform
-in [0, 49152), chunked prefill of 256, greedy decode, page 16, physical pool
-ceil(1.25 * sum ceil((p + 127) / 16)) pages, no prefix cache, EOS disabled.
-Weights are synthetic N(0, 0.02) (RMSNorm weights 1.0), seeded.
+Workloads (tinyinfer_amd/workloads.py; one step = one engine step in which
+every request decodes one token):
+- config3 (default, the headline): 64 requests, prompts uniform in
+  [256, 2048], chunked prefill of 256, 128 greedy tokens each, page 16, pool
+  1.25x the reserved pages, no prefix cache, EOS disabled;
+- config2: 1 request, 128-token prompt, 128 greedy tokens;
+- config4: a 1000-token prefix published once, then 32 requests of prefix +
+  64 unique tokens with the prefix cache on (copy-on-write of the shared
+  8-token tail), 64 greedy tokens each.
+Weights are synthetic N(0, 0.02) (RMSNorm weights 1.0), seeded. The runner
+computes in the fast arithmetic by default (FP32 matrix cores, flash-decoding
+attention; logits within 1e-3 of the reference, greedy tokens checked
+against the reference's in the GPU tests); --arithmetic exact selects the
+bit-exact one.
 
 Prefill runs first (untimed); `--warmup` pure-decode steps follow, then
 exactly `--steps` timed steps between two device synchronisations. Each
@@ -14,29 +24,38 @@ forward call ends with a device synchronisation of its own (the runner
 returns argmax results to the host), so host time over the steps is the
 whole job's time.
 
-roofline: the dominant kernel is paged attention (score, softmax and value
-kernels of one layer = one launch), timed live with HIP events over the
-timed steps: one layer per step (rotating through the layers), the events
-carried by the kernel dispatches on the runner's stream, so the timing adds
-nothing between kernels. Algorithmic bytes per launch =
-sum over sequences of T*kv_width*4*2 (K and V of every attended token, read
-once) + rows*hidden*4*2 (q in, context out). `traffic` is this run's
-algorithmic bytes times the measured/algorithmic ratio recorded in
-profiles/attention_b64_decode_traffic.json (two rocprofv3 --pmc passes,
-FETCH_SIZE and WRITE_SIZE, calibrated with a copy of known size).
+roofline: one layer per step (rotating through the layers) has its
+attention and its four projections timed with HIP events on the runner's
+stream. Attention algorithmic bytes per launch = sum over sequences of
+T*kv_width*4*2 (K and V of every attended token, read once) +
+rows*hidden*4*2 (q in, context out). Projection algorithmic bytes per layer
+= the layer's weights (q|k|v, o, gate, up, down) + the activations they read
+and write; FLOPs per layer = 2*rows*(weights/4); the projections' line
+carries both the HBM fraction and the fraction of the FP32 matrix peak. The
+one the metric names (attention; the projections at B=1) is `roofline`, the
+other `roofline_other`. `traffic` is this run's algorithmic bytes times the
+measured/algorithmic ratio of the committed counter record
+(profiles/*_traffic.json, written by --summarise-counters from two
+rocprofv3 --pmc passes, FETCH_SIZE and WRITE_SIZE, calibrated with the copy
+of known size that --traffic-probe runs).
 
-cpu_baseline: the oracle (a C restatement of the reference CPU path,
-bit-identical to it) on one host core, decoding single tokens at contexts
-drawn from the same prompt distribution, for about --cpu-seconds.
+cpu_baseline: the reference CPU runner (the reference's own CpuRunner,
+Engine and KVManager compiled from its sources into oracle/_ref) on one
+pinned host core: the prefill of one request's first prompt chunk, then
+single-token decode steps for about --cpu-seconds; prefill and decode rates
+are reported separately. Without oracle/_ref the oracle (a C restatement of
+the reference CPU path, bit-identical to it) stands in, labelled "port".
 """
 from __future__ import annotations
 
 import argparse
+import csv
 import json
-import math
 import os
+import platform
 import sys
 import time
+from collections import defaultdict
 from pathlib import Path
 
 import numpy as np
@@ -45,31 +64,35 @@ ROOT = Path(__file__).resolve().parent
 if str(ROOT) not in sys.path:
     sys.path.insert(0, str(ROOT))
 
-METRIC = "decode tok/s (B=64, SmolLM2-135M-shape FP32); paged-attn HBM GB/s % peak"
+METRICS = {
+    "config3": "decode tok/s (B=64, SmolLM2-135M-shape FP32); paged-attn HBM GB/s % peak",
+    "config2": "decode tok/s (B=1, SmolLM2-135M-shape FP32); projections HBM GB/s % peak",
+    "config4": "decode tok/s (32 prefix-sharing requests with COW, SmolLM2-135M-shape FP32); paged-attn HBM GB/s % peak",
+}
+DEFAULT_STEPS = {"config3": (96, 8), "config2": (96, 8), "config4": (48, 8)}
 HBM_PEAK_GBS = 8000.0
-BATCH, PAGE, CHUNK, BUDGET, MAX_NEW = 64, 16, 256, 8192, 128
-PROMPT_MIN, PROMPT_MAX = 256, 2048
-TRAFFIC_FILE = ROOT / "profiles" / "attention_b64_decode_traffic.json"
-
-
-def model_config() -> dict:
-    return dict(layers=30, hidden=576, intermediate=1536, heads=9, kv_heads=3, vocabulary=49152, context=4096,
-                eos=0, rms_epsilon=1e-5, rope_theta=100000.0, tied=1)
-
-
-def workload(seed: int):
-    rng = np.random.default_rng(seed)
-    lengths = rng.integers(PROMPT_MIN, PROMPT_MAX + 1, size=BATCH)
-    prompts = [rng.integers(0, 49152, size=int(p), dtype=np.int64).astype(np.int32) for p in lengths]
-    pages = sum(-(-(int(p) + MAX_NEW - 1) // PAGE) for p in lengths)
-    return prompts, int(math.ceil(1.25 * pages))
+FP32_MATRIX_PEAK_TFLOPS = 157.3
+PROBE_BYTES = 128 << 20  # --traffic-probe: one copy of 128 MiB (read and written)
 
 
 def log(msg: str):
     print(msg, file=sys.stderr, flush=True)
 
 
-def gpu_leg(args):
+def traffic_file(workload: str) -> Path:
+    return ROOT / "profiles" / f"decode_{workload}_traffic.json"
+
+
+def layer_shape(cfg: dict):
+    hd, inter = cfg["hidden"], cfg["intermediate"]
+    kvw = cfg["kv_heads"] * (hd // cfg["heads"])
+    qw = hd + 2 * kvw
+    weights = hd * qw + hd * hd + 2 * hd * inter + inter * hd  # floats
+    acts = 8 * hd + 2 * kvw + 2 * inter  # floats read or written per row
+    return kvw, weights, acts
+
+
+def gpu_leg(args, wl):
     import torch
 
     from tinyinfer_amd.backend import TIME_ATTENTION, TIME_HEAD, TIME_PROJECTION, TIME_SAMPLED, kernel_times, set_timing
@@ -77,21 +100,18 @@ def gpu_leg(args):
 
     if not torch.cuda.is_available():
         raise SystemExit("bench.py needs a GPU (no HIP device visible)")
-    cfg = model_config()
-    prompts, max_blocks = workload(args.seed)
+    cfg = wl.config()
     t = time.perf_counter()
-    weights = Weights.synthetic(cfg, seed=args.seed, stddev=0.02)
-    runner = Runner(weights, context=cfg["context"], block_tokens=PAGE, max_blocks=max_blocks,
-                    prefix_cache_blocks=0, kind=2 if args.arithmetic == "fast" else 0)
+    weights = Weights.synthetic(cfg, seed=wl.weight_seed, stddev=0.02)
+    runner = Runner(weights, context=cfg["context"], kind=2 if args.arithmetic == "fast" else 0, **wl.kv_args())
     device = runner.device()
-    engine = Engine(runner, max_batch_size=BATCH, token_budget=BUDGET, prefill_chunk=CHUNK, context=cfg["context"])
+    engine = Engine(runner, **wl.engine_args())
     engine.set_batching(True)
-    ids = [f"r{i}" for i in range(BATCH)]
-    for rid, p in zip(ids, prompts):
-        engine.submit(rid, p, max_new_tokens=MAX_NEW, eos_token_id=None)
-    log(f"setup {time.perf_counter() - t:.1f}s: pool {max_blocks} pages, prompts sum {sum(map(len, prompts))}")
+    log(f"setup {time.perf_counter() - t:.1f}s: {wl.name}, pool {wl.max_blocks} pages, "
+        f"prompts sum {sum(len(r.prompt) for r in wl.requests)}")
 
-    generated = {rid: 0 for rid in ids}
+    generated = defaultdict(int)
+    finished = set()
 
     def step():
         engine.step()
@@ -100,138 +120,309 @@ def gpu_leg(args):
                 raise RuntimeError(f"request {ev['id']} failed: {ev['error']}")
             if ev.get("token") is not None:
                 generated[ev["id"]] += 1
+            if ev.get("finish") is not None:
+                finished.add(ev["id"])
         if engine.failed():
             raise RuntimeError("engine failed")
         return engine.last_step_stats()
 
     t = time.perf_counter()
+    setup_steps = 0
+    phases = sorted({r.phase for r in wl.requests})
+    for ph in phases[:-1]:  # earlier phases run to completion (config4's published prefix)
+        for r in wl.requests:
+            if r.phase == ph:
+                engine.submit(r.id, r.prompt, max_new_tokens=r.max_new_tokens, eos_token_id=None)
+        while not engine.idle():
+            step()
+            setup_steps += 1
+    active = [r for r in wl.requests if r.phase == phases[-1]]
+    for r in active:
+        engine.submit(r.id, r.prompt, max_new_tokens=r.max_new_tokens, eos_token_id=None)
+    ids = [r.id for r in active]
     prefill_steps = 0
-    while min(generated.values()) == 0:
+    while min(generated[i] for i in ids) == 0:
         step()
         prefill_steps += 1
-        if prefill_steps > 200:
+        if prefill_steps > 400:
             raise RuntimeError("prefill did not finish")
-    log(f"prefill: {prefill_steps} steps, {time.perf_counter() - t:.1f}s")
-    if max(generated.values()) + args.warmup + args.steps > MAX_NEW:
-        raise SystemExit(f"--warmup + --steps must leave every request decoding: at most "
-                         f"{MAX_NEW - max(generated.values())} steps remain")
+    log(f"prefill: {setup_steps} + {prefill_steps} steps, {time.perf_counter() - t:.1f}s")
+    remaining = min(r.max_new_tokens for r in active) - max(generated[i] for i in ids)
+    if args.warmup + args.steps > remaining:
+        raise SystemExit(f"--warmup + --steps must leave every request decoding: at most {remaining} steps remain")
+    batch = len(ids)
     for _ in range(args.warmup):
         s = step()
-        assert s["decode_tokens"] == BATCH and s["prefill_tokens"] == 0, s
+        assert s["decode_tokens"] == batch and s["prefill_tokens"] == 0, s
     used = {rid: engine.runner.sequence(rid)[1] for rid in ids}
-    # Attention is timed on one layer per step (rotating through the layers,
-    # events carried by the kernel dispatches) so that timing costs the
-    # measured throughput nothing; --all-kernels times every launch.
-    set_timing(device, TIME_ATTENTION | (TIME_PROJECTION | TIME_HEAD if args.all_kernels else TIME_SAMPLED))
+    # One layer per step (rotating) has its attention and projections timed,
+    # so that timing costs the measured throughput almost nothing;
+    # --all-kernels times every launch and the LM head.
+    classes = TIME_ATTENTION | TIME_PROJECTION | (TIME_HEAD if args.all_kernels else TIME_SAMPLED)
+    set_timing(device, classes)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
         s = step()
-        assert s["decode_tokens"] == BATCH and s["prefill_tokens"] == 0, s
+        assert s["decode_tokens"] == batch and s["prefill_tokens"] == 0, s
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     times = kernel_times(device)
     for rid in ids:
         assert engine.runner.sequence(rid)[1] == used[rid] + args.steps
-    K = args.steps
-    sum_t = sum(K * u + K * (K + 1) // 2 for u in used.values())  # attended tokens over the timed steps
-    kv_width = cfg["kv_heads"] * (cfg["hidden"] // cfg["heads"])
-    launches = times["attention_launches"]
-    timed_layers = cfg["layers"] if args.all_kernels else 1  # per step
-    assert launches == K * timed_layers, times
-    att_bytes = timed_layers * (sum_t * kv_width * 4 * 2) + launches * BATCH * cfg["hidden"] * 4 * 2
-    att_s = times["attention_ns"] * 1e-9
-    achieved = att_bytes / att_s / 1e9
-    mean_context = sum_t / (K * BATCH)
-    result = dict(
-        value=BATCH * K / elapsed, ms_per_step=elapsed / K * 1e3, prefill_steps=prefill_steps,
-        mean_context=mean_context, attention_us_per_launch=att_s / launches * 1e6,
-        attention_bytes_per_launch=att_bytes / launches, achieved=achieved, times=times)
+    if args.traffic_probe:
+        # A copy of known size for the counter calibration (--summarise-counters).
+        src = torch.ones(PROBE_BYTES // 4, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(2):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+    costs = runner.cost_stats()
     engine.shutdown()
     engine.close()
-    return result
+
+    K = args.steps
+    sum_t = sum(K * u + K * (K + 1) // 2 for u in used.values())  # attended tokens over the timed steps
+    kvw, layer_floats, act_floats = layer_shape(cfg)
+    timed_layers = cfg["layers"] if args.all_kernels else 1  # per step
+    att_launches = times["attention_launches"]
+    assert att_launches == K * timed_layers, times
+    att_bytes = timed_layers * (sum_t * kvw * 4 * 2) + att_launches * batch * cfg["hidden"] * 4 * 2
+    att_s = times["attention_ns"] * 1e-9
+    proj_layers = times["projection_launches"] // 4
+    assert proj_layers == K * timed_layers, times
+    proj_bytes_layer = 4 * (layer_floats + batch * act_floats)
+    proj_flops_layer = 2 * batch * layer_floats
+    proj_s = times["projection_ns"] * 1e-9
+    return dict(
+        value=batch * K / elapsed, ms_per_step=elapsed / K * 1e3, batch=batch, prefill_steps=setup_steps + prefill_steps,
+        mean_context=sum_t / (K * batch), times=times, cow=costs,
+        attention=dict(us=att_s / att_launches * 1e6, bytes=att_bytes / att_launches, gbs=att_bytes / att_s / 1e9),
+        projections=dict(us=proj_s / proj_layers * 1e6, bytes=proj_bytes_layer, flops=proj_flops_layer,
+                         gbs=proj_bytes_layer * proj_layers / proj_s / 1e9,
+                         tflops=proj_flops_layer * proj_layers / proj_s / 1e12))
 
 
-def cpu_leg(args):
-    """Oracle decode tokens on one core (single requests, as the reference CPU
-    runner serves them)."""
-    from oracle import OracleModel
+def host_info():
+    model = platform.processor() or ""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        avail = os.cpu_count()
+    return dict(host_nproc=os.cpu_count(), host_cpus_available=avail, cpu_model=model)
 
+
+def cpu_leg(args, wl):
+    """The reference CPU path on one pinned core: one request's first prompt
+    chunk, then single-token decode steps (the reference CPU runner serves
+    one sequence per call, so this is its throughput)."""
+    from oracle import ref_library
+
+    info = host_info()
     try:
         os.sched_setaffinity(0, {sorted(os.sched_getaffinity(0))[0]})
     except (AttributeError, OSError):
         pass
-    cfg = model_config()
-    model = OracleModel(cfg, seed=args.seed, stddev=0.02)
-    rng = np.random.default_rng(args.seed + 1)
-    kv_width = cfg["kv_heads"] * (cfg["hidden"] // cfg["heads"])
-    pages = -(-(PROMPT_MAX + MAX_NEW) // PAGE)
-    floats = pages * cfg["layers"] * PAGE * kv_width
-    keys = rng.standard_normal(floats, dtype=np.float32)
-    values = rng.standard_normal(floats, dtype=np.float32)
-    table = np.arange(pages, dtype=np.int32)
-    tokens, contexts, spent = 0, [], 0.0
-    while spent < args.cpu_seconds or tokens < 2:
-        used = int(rng.integers(PROMPT_MIN, PROMPT_MAX + 1)) + MAX_NEW // 2
-        token = int(rng.integers(0, cfg["vocabulary"]))
+    cfg = wl.config()
+    prompt = np.asarray(wl.requests[-1].prompt[:wl.prefill_chunk], dtype=np.int32)
+    ref = ref_library()
+    if ref is None:
+        return oracle_cpu_leg(args, wl, cfg, prompt, info)
+    from tinyinfer_amd.host import Engine, Runner, Weights
+
+    w = Weights.synthetic(cfg, seed=wl.weight_seed, stddev=0.02, library=ref)
+    pages = -(-(len(prompt) + 256) // 16)
+    runner = Runner(w, context=cfg["context"], kind=0, block_tokens=16, max_blocks=pages, prefix_cache_blocks=0)
+    engine = Engine(runner, max_batch_size=1, token_budget=len(prompt), prefill_chunk=len(prompt),
+                    context=cfg["context"])
+    engine.submit("cpu", prompt, max_new_tokens=256, eos_token_id=None)
+    t = time.perf_counter()
+    engine.step()  # the whole prompt in one chunk, and its first token
+    prefill_s = time.perf_counter() - t
+    decoded, spent = 0, 0.0
+    while spent < args.cpu_seconds or decoded < 2:
         t = time.perf_counter()
-        model.append(keys, values, PAGE, table, used, [token])
+        engine.step()
         spent += time.perf_counter() - t
-        tokens += 1
-        contexts.append(used + 1)
-    return dict(value=tokens / spent, unit="tok/s", cores=1, kind="port",
-                sample=f"{tokens} single-request decode tokens of the same model at contexts "
-                       f"{min(contexts)}..{max(contexts)} (mean {np.mean(contexts):.0f}; prompt U[256,2048] + 64), "
-                       f"{spent:.1f}s on 1 host core (oracle: C restatement of the reference CPU runner, "
-                       f"bit-identical to it)")
+        decoded += 1
+        if decoded >= 200:
+            break
+    events = engine.poll_events()
+    assert not any(e.get("error") for e in events), events
+    engine.shutdown()
+    engine.close()
+    return dict(value=round(decoded / spent, 3), unit="tok/s", cores=1, kind="reference",
+                prefill_tok_s=round(len(prompt) / prefill_s, 2), prefill_s=round(prefill_s, 2),
+                sample=f"reference CpuRunner + Engine (oracle/_ref, built from the reference sources), 1 pinned core: "
+                       f"prefill of a {len(prompt)}-token prompt chunk of the same workload ({prefill_s:.1f}s), then "
+                       f"{decoded} single-token decode steps at contexts {len(prompt) + 1}..{len(prompt) + decoded} "
+                       f"({spent:.1f}s)", **info)
+
+
+def oracle_cpu_leg(args, wl, cfg, prompt, info):
+    from oracle import OracleModel
+
+    model = OracleModel(cfg, seed=wl.weight_seed, stddev=0.02)
+    kvw = cfg["kv_heads"] * (cfg["hidden"] // cfg["heads"])
+    pages = -(-(len(prompt) + 256) // 16)
+    keys = np.zeros(pages * cfg["layers"] * 16 * kvw, dtype=np.float32)
+    values = np.zeros_like(keys)
+    table = np.arange(pages, dtype=np.int32)
+    t = time.perf_counter()
+    logits = model.append(keys, values, 16, table, 0, [int(x) for x in prompt])
+    prefill_s = time.perf_counter() - t
+    used, decoded, spent = len(prompt), 0, 0.0
+    token = int(np.argmax(logits))
+    while spent < args.cpu_seconds or decoded < 2:
+        t = time.perf_counter()
+        logits = model.append(keys, values, 16, table, used, [token])
+        spent += time.perf_counter() - t
+        used += 1
+        decoded += 1
+        token = int(np.argmax(logits))
+    return dict(value=round(decoded / spent, 3), unit="tok/s", cores=1, kind="port",
+                prefill_tok_s=round(len(prompt) / prefill_s, 2), prefill_s=round(prefill_s, 2),
+                sample=f"oracle (C restatement of the reference CPU runner, bit-identical to it), 1 pinned core: "
+                       f"{len(prompt)}-token prefill ({prefill_s:.1f}s), {decoded} decode steps ({spent:.1f}s)", **info)
+
+
+def roofline(kind: str, g: dict, rec: dict | None):
+    if kind == "attention":
+        a = g["attention"]
+        ratio = rec.get("attention_ratio") if rec else None
+        return {"bound": "hbm", "kernel": "paged attention (one layer: split kernel + merge kernel)",
+                "achieved": round(a["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(a["gbs"] / HBM_PEAK_GBS, 4),
+                "traffic": int(round(ratio * a["bytes"])) if ratio else None, "traffic_ratio": ratio,
+                "algorithmic_bytes_per_launch": int(a["bytes"]), "us_per_launch": round(a["us"], 2)}
+    p = g["projections"]
+    ratio = rec.get("projection_ratio") if rec else None
+    return {"bound": "hbm", "kernel": "projections (one layer: q|k|v+RoPE, o, gate/up+SwiGLU, down)",
+            "achieved": round(p["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(p["gbs"] / HBM_PEAK_GBS, 4),
+            "traffic": int(round(ratio * p["bytes"])) if ratio else None, "traffic_ratio": ratio,
+            "algorithmic_bytes_per_launch": int(p["bytes"]), "us_per_launch": round(p["us"], 2),
+            "mfma": {"achieved": round(p["tflops"], 2), "peak": FP32_MATRIX_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(p["tflops"] / FP32_MATRIX_PEAK_TFLOPS, 4), "flops_per_launch": int(p["flops"])}}
+
+
+def summarise_counters(fetch_csv: str, write_csv: str, bench_json: str, out: str):
+    """Per-launch HBM bytes of the decode attention and projections from two
+    rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE; KiB per dispatch) of
+    `bench.py --traffic-probe`, each counter scaled by what it reads for the
+    probe's copy of known size."""
+    line = json.loads(Path(bench_json).read_text().strip().splitlines()[-1])
+    fast = line["config"].get("arithmetic") == "fast"
+    # The decode kernels (prefill runs other instantiations).
+    att_kernels = (("fast_attention_kernel<", "fast_attention_merge_kernel") if fast else
+                   ("attn_scores_kernel<16, 64, true>", "attn_decode_kernel<"))
+    proj_kernels = (("fast_gemm_kernel<4, true, false, 1, 2, 6>", "fast_gemm_kernel<1, false, false, 1, 1, 12>",
+                     "fast_gemm_kernel<2, true, false, 2, 1, 6>") if fast else ("gemm_column",))
+
+    def read(path):
+        per = defaultdict(list)
+        probe = []
+        for r in csv.DictReader(open(path)):
+            name = r["Kernel_Name"].replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0]
+            kib = float(r["Counter_Value"])
+            if name.startswith("__amd_rocclr_copyBuffer") and kib * 1024 > PROBE_BYTES / 4:
+                probe.append(kib)
+            per[name].append(kib)
+        return per, probe
+
+    result = {"workload": line["config"]["workload"], "seed": line["config"]["seed"],
+              "arithmetic": line["config"].get("arithmetic"), "mean_context": line["config"]["mean_context"],
+              "steps": line["steps"], "warmup": line["warmup"]}
+    for counter, path in (("fetch", fetch_csv), ("write", write_csv)):
+        per, probe = read(path)
+        if not probe:
+            raise SystemExit(f"{path}: no probe copy found (run bench.py with --traffic-probe)")
+        factor = float(np.mean(probe)) * 1024 / PROBE_BYTES
+        result[f"{counter}_factor"] = round(factor, 6)
+        att = {k: float(np.mean(v)) * 1024 / factor for k, v in per.items() if any(a in k for a in att_kernels)}
+        proj = {k: float(np.mean(v)) * 1024 / factor for k, v in per.items() if any(p in k for p in proj_kernels)}
+        result[f"attention_{counter}_bytes"] = {k: int(v) for k, v in att.items()}
+        result[f"projection_{counter}_bytes"] = {k: int(v) for k, v in proj.items()}
+    att_total = sum(result["attention_fetch_bytes"].values()) + sum(result["attention_write_bytes"].values())
+    # One layer runs the residual projection twice (o and down): its mean counts twice.
+    proj_total = sum(v * (2 if "<1, false, false" in k else 1) for k, v in result["projection_fetch_bytes"].items())
+    proj_total += sum(v * (2 if "<1, false, false" in k else 1) for k, v in result["projection_write_bytes"].items())
+    att_alg = line["roofline" if "attention" in line["roofline"]["kernel"] else "roofline_other"]
+    proj_alg = line["roofline" if "projections" in line["roofline"]["kernel"] else "roofline_other"]
+    result["attention_bytes_per_launch"] = int(att_total)
+    result["attention_algorithmic_bytes"] = att_alg["algorithmic_bytes_per_launch"]
+    result["attention_ratio"] = round(att_total / att_alg["algorithmic_bytes_per_launch"], 4)
+    result["projection_bytes_per_layer"] = int(proj_total)
+    result["projection_algorithmic_bytes"] = proj_alg["algorithmic_bytes_per_launch"]
+    result["projection_ratio"] = round(proj_total / proj_alg["algorithmic_bytes_per_launch"], 4)
+    Path(out).write_text(json.dumps(result, indent=1) + "\n")
+    print(json.dumps(result, indent=1))
 
 
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=96)
-    ap.add_argument("--warmup", type=int, default=8)
-    ap.add_argument("--seed", type=int, default=20250)
-    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--workload", choices=sorted(METRICS), default="config3")
+    ap.add_argument("--steps", type=int, default=None)
+    ap.add_argument("--warmup", type=int, default=None)
+    ap.add_argument("--cpu-seconds", type=float, default=8.0, help="decode time of the CPU baseline")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--all-kernels", action="store_true", help="also time projections and the LM head")
+    ap.add_argument("--all-kernels", action="store_true", help="time every layer and the LM head")
     ap.add_argument("--arithmetic", choices=["fast", "exact"], default="fast")
+    ap.add_argument("--traffic-probe", action="store_true", help="run a copy of known size after the timed steps")
+    ap.add_argument("--summarise-counters", nargs=4, metavar=("FETCH_CSV", "WRITE_CSV", "BENCH_JSON", "OUT"))
     args = ap.parse_args()
+    if args.summarise_counters:
+        summarise_counters(*args.summarise_counters)
+        return
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (decode would shard by request, "
               "one engine per GPU); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
+    from tinyinfer_amd import workloads
+
+    wl = getattr(workloads, args.workload)()
+    steps, warmup = DEFAULT_STEPS[args.workload]
+    args.steps = steps if args.steps is None else args.steps
+    args.warmup = warmup if args.warmup is None else args.warmup
     if args.steps < 1 or args.warmup < 0:
         raise SystemExit("--steps must be >= 1 and --warmup >= 0")
-    g = gpu_leg(args)
-    cpu = None if args.no_cpu_baseline else cpu_leg(args)
-    # HBM bytes per attention launch: the counter-measured bytes / algorithmic
-    # bytes ratio of the committed two-pass FETCH_SIZE/WRITE_SIZE record (same
-    # workload and seed, fewer steps), applied to this run's algorithmic bytes.
-    traffic, traffic_ratio = None, None
-    if TRAFFIC_FILE.exists():
-        rec = json.loads(TRAFFIC_FILE.read_text())
-        if rec.get("seed") == args.seed and rec.get("traffic_ratio"):
-            traffic_ratio = rec["traffic_ratio"]
-            traffic = int(round(traffic_ratio * g["attention_bytes_per_launch"]))
-    frac = g["achieved"] / HBM_PEAK_GBS
+    g = gpu_leg(args, wl)
+    cpu = None if args.no_cpu_baseline else cpu_leg(args, wl)
+    rec = None
+    tf = traffic_file(args.workload)
+    if tf.exists():
+        r = json.loads(tf.read_text())
+        if r.get("seed") == wl.weight_seed and r.get("arithmetic") == args.arithmetic:
+            rec = r
+    # The kernel the metric names: paged attention, except at B=1 where the
+    # projections' weight stream dominates the step.
+    dominant = "projections" if args.workload == "config2" else "attention"
+    other = "projections" if dominant == "attention" else "attention"
     line = {
-        "metric": METRIC, "value": round(g["value"], 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(g["ms_per_step"], 4), "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "metric": METRICS[args.workload], "value": round(g["value"], 2), "unit": "tok/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(g["ms_per_step"], 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
         "data": "synthetic: random-init N(0,0.02) weights, seeded uniform prompt ids",
-        "config": {"workload": "B=64 batched greedy decode, SmolLM2-135M shape (30 layers, hidden 576, "
-                               "9/3 heads, head_dim 64, SwiGLU 1536, vocab 49152, tied), prompts U[256,2048], "
-                               "prefill chunk 256, page 16, pool 1.25x",
-                   "batch": BATCH, "page_tokens": PAGE, "prefill_chunk": CHUNK, "token_budget": BUDGET,
-                   "seed": args.seed, "mean_context": round(g["mean_context"], 1)},
-        "roofline": {"bound": "hbm", "kernel": "paged attention (score+softmax+value kernels, one layer)",
-                     "achieved": round(g["achieved"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(frac, 4), "traffic": traffic, "traffic_ratio": traffic_ratio,
-                     "algorithmic_bytes_per_launch": int(g["attention_bytes_per_launch"]),
-                     "us_per_launch": round(g["attention_us_per_launch"], 2)},
+        "config": {"workload": f"{wl.name}: {wl.description}; SmolLM2-135M shape (30 layers, hidden 576, 9/3 heads, "
+                               f"head_dim 64, SwiGLU 1536, vocab 49152, tied), page 16",
+                   "batch": g["batch"], "page_tokens": 16, "prefill_chunk": wl.prefill_chunk,
+                   "token_budget": wl.token_budget, "seed": wl.weight_seed, "arithmetic": args.arithmetic,
+                   "mean_context": round(g["mean_context"], 1),
+                   "timed_window": f"decode steps {args.warmup + 1}..{args.warmup + args.steps} after prefill "
+                                   f"({g['prefill_steps']} prefill steps untimed)"},
+        "roofline": roofline(dominant, g, rec),
+        "roofline_other": roofline(other, g, rec),
         "cpu_baseline": cpu,
         "kernel_times_ns": g["times"],
+        "cow": {k: g["cow"][k] for k in ("cow_pages", "cow_bytes") if k in g["cow"]},
     }
     print(json.dumps(line), flush=True)
 

@@ -834,6 +834,18 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
         fw.partial_out = h->fast_partials;
         fw.partial_ml = h->fast_partials + fast_items * group_ * 64;
         fw.kv_heads = c.kv_heads;
+        auto set_prefetch = [&](int l) {
+            // This layer's remaining projections, then the next layer's q|k|v.
+            const float* ranges[] = {h->o[l], h->gate[l], h->up[l], h->down[l],
+                                     l + 1 < c.layers ? h->qkv[l + 1] : nullptr};
+            const uint64_t bytes[] = {sizeof(float) * hd * hd, sizeof(float) * hd * in, sizeof(float) * hd * in,
+                                      sizeof(float) * hd * in,
+                                      l + 1 < c.layers ? sizeof(float) * hd * (uint64_t)qw : 0};
+            for (int r = 0; r < mphip::FastAttentionWork::kPrefetchRanges; ++r) {
+                fw.prefetch[r] = r < 5 ? ranges[r] : nullptr;
+                fw.prefetch_bytes[r] = r < 5 && ranges[r] ? bytes[r] : 0;
+            }
+        };
         if (e == hipSuccess) e = mphip::launch_fast_ssq(s, h->x, R, hd, h->ssq, ssq_stride);
         for (int l = 0; l < c.layers && e == hipSuccess; ++l) {
             layer_now = l;
@@ -865,6 +877,7 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
             }
             if (e == hipSuccess) {
                 if (fast_decode) {
+                    set_prefetch(l);
                     e = timed(MP_TIME_ATTENTION, [&] {
                         return mphip::launch_fast_attention(s, h->qkv_out, qw, R, c.heads, c.kv_heads, meta, kv, l,
                                                             h->ctx, hd, fw);

@@ -20,9 +20,12 @@
 //    of one float4 index forming a 256-byte run) and the four quarters are
 //    summed across lanes;
 //  - output: lane = dim d; a lane reads 4 float4 of V (4 tokens each for
-//    its d, a 1 KB run per float4 index) and takes each token's probability
-//    from the token's lane (a lane read, as are the page's maximum and sum:
-//    cross-lane steps stay on the vector ALU, see lanes.h).
+//    its d, a 1 KB run per float4 index) and the page's probabilities from
+//    LDS (written by one lane per token, read back as a broadcast).
+// Cross-lane sums and maxima use DPP and lane reads (lanes.h). The softmax
+// keeps a reference maximum per head that is raised only when a score
+// exceeds it by more than 16 (probabilities then stay below e^16 and the
+// sums are rescaled), so most pages need no cross-lane maximum.
 // Loads past the split's last page re-read that page (a cache hit) so that
 // every load is unconditional and the waits stay exact. A row whose
 // context is one split writes its output directly; otherwise every split
@@ -52,6 +55,7 @@ constexpr int kRing = 3;                           // pages in flight per wavefr
 constexpr int kItemsPerGroup = 4;
 constexpr int kMergeHeld = 16;  // splits whose partial outputs the merge loads up front
 constexpr float kScale = 0.125f;  // 1/sqrt(64)
+constexpr float kRescale = 16.0f;  // probabilities stay below e^16 before a rescale
 
 
 template <int G>
@@ -60,6 +64,7 @@ __global__ __launch_bounds__(kItemsPerGroup * 64) void fast_attention_kernel(con
                                                                              FastAttentionWork w,
                                                                              float* __restrict__ out, int ldo) {
     const int lane = threadIdx.x & 63;
+    __shared__ float p_s[kItemsPerGroup][G][kPage];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int index = blockIdx.x * kItemsPerGroup + wave;
     if (index >= w.items_count) return;
@@ -96,16 +101,33 @@ __global__ __launch_bounds__(kItemsPerGroup * 64) void fast_attention_kernel(con
             q[h][j] = *reinterpret_cast<const f4*>(qkv + quad_index(row, c, ldq));
         }
     __builtin_amdgcn_sched_barrier(0);
+    // This wavefront's 8 KB of the weights to prefetch: lane i touches line
+    // i (128 bytes) of the slice.
+    float touched = 0.0f;
+    {
+        uint64_t at = ((uint64_t)index * 64 + lane) * 128;
+        const char* line = nullptr;
+#pragma unroll
+        for (int r = 0; r < FastAttentionWork::kPrefetchRanges; ++r) {
+            if (!line && at < w.prefetch_bytes[r]) line = reinterpret_cast<const char*>(w.prefetch[r]) + at;
+            if (!line) at -= w.prefetch_bytes[r];
+        }
+        if (line) touched = *reinterpret_cast<const float*>(line);
+    }
 #pragma unroll
     for (int k = 0; k < kRing; ++k) load(k, kb[k], vb[k]);
     // Keep the loads where they are: the scheduler would otherwise sink
     // them to their first use and take the pages out of flight.
     __builtin_amdgcn_sched_barrier(0);
-    float m[G], l[G], acc[G];
+    // Per head: the reference maximum m (uniform), this lane's share of the
+    // denominator (the probabilities of its token; quad-uniform) and lane
+    // d's output. Probabilities are exp(s - m) with m raised only when a
+    // score exceeds it by more than kRescale (then the sums are rescaled),
+    // so a page costs no cross-lane maximum unless the scores climb.
+    float m[G], lp[G], acc[G];
 #pragma unroll
     for (int h = 0; h < G; ++h) {
-        m[h] = -__builtin_inff();
-        l[h] = 0.0f;
+        lp[h] = 0.0f;
         acc[h] = 0.0f;
     }
 #pragma unroll
@@ -115,50 +137,76 @@ __global__ __launch_bounds__(kItemsPerGroup * 64) void fast_attention_kernel(con
         f4(&vc)[4] = vb[k % kRing];
         const int tok0 = (first + k) * kPage;
         const bool valid = tok0 + t < end;
+        float s[G];
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+            // Four independent chains (one per float4), then their sum.
+            float dj[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                dj[j] = q[h][j].x * kc[j].x;
+                dj[j] += q[h][j].y * kc[j].y;
+                dj[j] += q[h][j].z * kc[j].z;
+                dj[j] += q[h][j].w * kc[j].w;
+            }
+            const float d = quad_sum((dj[0] + dj[1]) + (dj[2] + dj[3]));  // token t's score in its four lanes
+            s[h] = valid ? d * kScale : -__builtin_inff();
+        }
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+            if (k == 0) {
+                m[h] = rows_max(row_quads_max(s[h]));  // finite: the first page holds a valid token
+            } else if (__builtin_amdgcn_ballot_w64(s[h] > m[h] + kRescale)) {
+                const float m_new = fmaxf(m[h], rows_max(row_quads_max(s[h])));
+                const float keep = __expf(m[h] - m_new);
+                lp[h] *= keep;
+                acc[h] *= keep;
+                m[h] = m_new;
+            }
+            const float p = valid ? __expf(s[h] - m[h]) : 0.0f;
+            lp[h] += p;
+            if (dq == 0) p_s[wave][h][t] = p;
+        }
         // Slots past the context (last page only) hold stale values: they
         // take no part, whatever they are.
         f4 v[4];
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            v[g] = vc[g];
-            const int tok = tok0 + 4 * g;
-            if (tok + 0 >= end) v[g].x = 0.0f;
-            if (tok + 1 >= end) v[g].y = 0.0f;
-            if (tok + 2 >= end) v[g].z = 0.0f;
-            if (tok + 3 >= end) v[g].w = 0.0f;
-        }
-#pragma unroll
-        for (int h = 0; h < G; ++h) {
-            float s = 0.0f;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                s += q[h][j].x * kc[j].x;
-                s += q[h][j].y * kc[j].y;
-                s += q[h][j].z * kc[j].z;
-                s += q[h][j].w * kc[j].w;
-            }
-            s = quad_sum(s);  // token t's score in its four lanes
-            s = valid ? s * kScale : -__builtin_inff();
-            const float m_new = fmaxf(m[h], rows_max(row_quads_max(s)));  // finite: the page holds a valid token
-            const float keep = __expf(m[h] - m_new);
-            const float p = valid ? __expf(s - m_new) : 0.0f;
-            l[h] = l[h] * keep + rows_sum(row_quads_sum(p));
-            float a = acc[h] * keep;
-            // Lane d: sum over the page's tokens of p_t * V[t][d], p_t read from lane 4t.
+        for (int g = 0; g < 4; ++g) v[g] = vc[g];
+        if (tok0 + kPage > end) {
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-                a += lane_value(p, 16 * g + 0) * v[g].x;
-                a += lane_value(p, 16 * g + 4) * v[g].y;
-                a += lane_value(p, 16 * g + 8) * v[g].z;
-                a += lane_value(p, 16 * g + 12) * v[g].w;
+                const int tok = tok0 + 4 * g;
+                if (tok + 0 >= end) v[g].x = 0.0f;
+                if (tok + 1 >= end) v[g].y = 0.0f;
+                if (tok + 2 >= end) v[g].z = 0.0f;
+                if (tok + 3 >= end) v[g].w = 0.0f;
             }
-            acc[h] = a;
-            m[h] = m_new;
         }
+        __builtin_amdgcn_wave_barrier();
+        // Lane d: sum over the page's tokens of p_t * V[t][d], p read back
+        // from LDS as four float4 (the same address in every lane).
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+            float ag[4];
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const f4 pv = reinterpret_cast<const f4*>(p_s[wave][h])[g];
+                ag[g] = pv.x * v[g].x;
+                ag[g] += pv.y * v[g].y;
+                ag[g] += pv.z * v[g].z;
+                ag[g] += pv.w * v[g].w;
+            }
+            acc[h] += (ag[0] + ag[1]) + (ag[2] + ag[3]);
+        }
+        __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_sched_barrier(0);
         if (k + kRing < kSplitPages) load(k + kRing, kb[k % kRing], vb[k % kRing]);
         __builtin_amdgcn_sched_barrier(0);
     }
+    asm volatile("" ::"v"(touched));  // the prefetch's value is not used
+    float l[G];
+#pragma unroll
+    for (int h = 0; h < G; ++h) l[h] = rows_sum(row_quads_sum(lp[h]));  // each token once
     if (t0 == 0 && n == meta.row_pos[row] + 1) {
         // The row's only split: the output itself.
 #pragma unroll

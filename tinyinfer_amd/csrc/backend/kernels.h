@@ -134,6 +134,13 @@ struct FastAttentionWork {
     float* partial_out;
     float* partial_ml;
     int kv_heads;
+    // Weights the next projections read, touched by the attention's
+    // wavefronts (one dword per 128-byte line, 8 KB per wavefront, results
+    // unused) so that they are in the memory-side cache when those
+    // projections run: up to kPrefetchRanges ranges of `bytes` each.
+    static constexpr int kPrefetchRanges = 6;
+    const float* prefetch[kPrefetchRanges];
+    uint64_t prefetch_bytes[kPrefetchRanges];
 };
 int fast_attention_split_tokens();
 hipError_t launch_fast_attention(hipStream_t s, const float* qkv, int ldq, int rows, int heads, int kv_heads,
