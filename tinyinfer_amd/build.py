@@ -1,8 +1,9 @@
 """Builds the native library of the package in-tree.
 
 `build()` compiles every HIP source for gfx950 and the host C++ runtime into
-tinyinfer_amd/lib/libminiprefix_hip.so with hipcc. There is no CPU fallback:
-the Python side refuses to run without this library.
+tinyinfer_amd/lib/libminiprefix_hip.so with hipcc, then the protocol-v3
+worker executable tinyinfer_amd/lib/miniprefix_worker against it. There is
+no CPU fallback: the Python side refuses to run without this library.
 """
 from __future__ import annotations
 
@@ -16,6 +17,7 @@ ROOT = PACKAGE.parent
 CSRC = PACKAGE / "csrc"
 LIB_DIR = PACKAGE / "lib"
 LIBRARY = LIB_DIR / "libminiprefix_hip.so"
+WORKER = LIB_DIR / "miniprefix_worker"
 
 ARCH = os.environ.get("MP_HIP_ARCH", "gfx950")
 
@@ -55,7 +57,24 @@ def build(verbose: bool = False) -> Path:
     if verbose and err.strip():
         print(err, file=sys.stderr)
     os.replace(tmp, LIBRARY)
+    build_worker(verbose)
     return LIBRARY
+
+
+def build_worker(verbose: bool = False) -> Path:
+    """The worker executable (csrc/worker), linked to the library beside it."""
+    worker = CSRC / "worker"
+    tmp = WORKER.with_suffix(".tmp")
+    cmd = [os.environ.get("CXX", "g++"), "-std=c++17", "-O2", "-Wall", f"-I{ROOT / 'include'}",
+           f"-I{CSRC / 'host'}", f"-I{worker}", str(worker / "worker.cpp"), str(worker / "protocol.cpp"),
+           f"-L{LIB_DIR}", "-lminiprefix_hip", "-Wl,-rpath,$ORIGIN", "-o", str(tmp)]
+    if verbose:
+        print(" ".join(cmd), file=sys.stderr)
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"worker build failed ({proc.returncode}):\n{proc.stderr[-4000:]}")
+    os.replace(tmp, WORKER)
+    return WORKER
 
 
 if __name__ == "__main__":
