@@ -130,12 +130,16 @@ int mp_hip_table_write(mp_hip* h, int32_t slot, int32_t first, const int32_t* bl
  * Inside a page the pools use the device order, and the copy moves the
  * valid tokens' K and V in that order (the same bytes the reference's 2-D
  * copy moves, counted the same way in the COW statistics). Other regions
- * are MP_INVALID_ARGUMENT. Asynchronous on the context's stream; ordered
- * before the next forward. */
+ * are MP_INVALID_ARGUMENT. Queued: the copies queued since the last
+ * forward run as one launch at the start of the next forward (or at
+ * mp_hip_sync), before any kernel touches the pools; a copy that would read
+ * or write a page a queued copy writes (or write a page one reads) first
+ * flushes the queue, so the result is that of the calls in order. */
 int mp_hip_copy_tail(mp_hip* h, const mp_tail_region* region);
 
 /* Same copy, timed with device events around it (the reference's opt-in
- * COW timing, llama_runner.cu:129-138,171-172). Synchronous. */
+ * COW timing, llama_runner.cu:129-138,171-172): flushes the queue first
+ * (untimed), then launches and times this copy alone. Synchronous. */
 int mp_hip_copy_tail_timed(mp_hip* h, const mp_tail_region* region, uint64_t* nanoseconds);
 
 /* Chunk forward of `nseq` sequences (CpuRunner::append's device half,
@@ -174,11 +178,13 @@ int mp_hip_paged_attention_decode_noalloc(const float* q, const float* keys, con
                                           int32_t layers, int32_t block_tokens, int32_t heads,
                                           int32_t kv_heads, int32_t dim, float* out, void* stream);
 
-/* Waits for all work on the context's stream (StreamBlas::synchronize). */
+/* Applies queued table entries and copies, then waits for all work on the
+ * context's stream (StreamBlas::synchronize). */
 int mp_hip_sync(mp_hip* h);
 int mp_hip_stats(const mp_hip* h, mp_hip_counters* out);
 
-/* Device pointers of the K and V pools (for tests and profiling). */
+/* Device pointers of the K and V pools (for tests and profiling); their
+ * contents include queued copies after mp_hip_sync. */
 int mp_hip_kv_pools(const mp_hip* h, float** keys, float** values, size_t* elements);
 
 /* The context's stream (hipStream_t), e.g. for recording events around calls. */

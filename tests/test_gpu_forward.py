@@ -221,3 +221,65 @@ def test_long_context_softmax_windows(torch_cuda, shape):
         split.append(tokens[at:at + n])
         at += n
     _run_sequence(model, backend, bt, split, table)
+
+
+def test_queued_tail_copies(torch_cuda):
+    """Copies-on-write are queued and run as one launch before the next
+    forward: three copies of one shared tail page into fresh pages, and a
+    chain (tail -> X, then X -> Y: the second reads a page the first
+    writes, which flushes the queue first). Each fork then appends a token
+    through its own table in one batched forward; logits equal the oracle's
+    over pools where the same regions were copied on the CPU, bit for bit."""
+    cfg = smollm_config(layers=2, context=128)
+    model = OracleModel(cfg, seed=31)
+    bt, max_blocks = 16, 32
+    backend = HipBackend(cfg, block_tokens=bt, max_blocks=max_blocks, max_sequences=8)
+    upload_model(backend, model)
+    o = Oracle()
+    n = pool_elements(cfg, bt, max_blocks)
+    keys = np.zeros(n, dtype=np.float32)
+    values = np.zeros(n, dtype=np.float32)
+    kvw = cfg["kv_heads"] * (cfg["hidden"] // cfg["heads"])
+    page, layers = bt * kvw, cfg["layers"]
+    block = page * layers
+    source = np.array([3, 11, 20], dtype=np.int32)
+    prompt = [int(t) for t in o.fill_tokens(37, 31, 8000, cfg["vocabulary"])]
+    backend.table_write(0, 0, source)
+    want = model.append(keys, values, bt, source, 0, prompt)
+    _, got = backend.forward([(0, 0, len(prompt))], prompt)
+    _logits_match(got[0], want)
+    valid = len(prompt) % bt
+
+    def cow(dst, src):
+        backend.copy_tail(dst * block, src * block, page, valid * kvw, layers)
+        for layer in range(layers):
+            d, s = dst * block + layer * page, src * block + layer * page
+            keys[d:d + valid * kvw] = keys[s:s + valid * kvw]
+            values[d:d + valid * kvw] = values[s:s + valid * kvw]
+
+    forks = {1: 5, 2: 6, 3: 7}  # table slot -> fresh tail page
+    for slot, fresh in forks.items():
+        cow(fresh, 20)
+    cow(9, 20)
+    cow(12, 9)  # reads the page the previous copy writes
+    forks[4] = 12
+    tables = {slot: np.array([3, 11, fresh], dtype=np.int32) for slot, fresh in forks.items()}
+    for slot, t in tables.items():
+        backend.table_write(slot, 0, t)
+    tokens = [int(t) for t in o.fill_tokens(len(tables), 31, 8001, cfg["vocabulary"])]
+    expect = [model.append(keys, values, bt, tables[slot], len(prompt), [tok])
+              for slot, tok in zip(tables, tokens)]
+    before = backend.stats()["cow_copies"]
+    am, got = backend.forward([(slot, len(prompt), 1) for slot in tables], tokens)
+    for i, w in enumerate(expect):
+        _logits_match(got[i], w)
+        assert am[i] == int(np.argmax(w))
+    assert backend.stats()["cow_copies"] == before
+    # A copy queued and flushed by sync alone.
+    cow(13, 12)
+    backend.sync()
+    backend.table_write(5, 0, np.array([3, 11, 13], dtype=np.int32))
+    tok = tokens[0]
+    w = model.append(keys, values, bt, np.array([3, 11, 13], dtype=np.int32), len(prompt), [tok])
+    _, got = backend.forward([(5, len(prompt), 1)], [tok])
+    _logits_match(got[0], w)

@@ -83,6 +83,11 @@ struct mp_hip {
     // block id): applied on the device at the start of the next forward
     // (or sync), uploaded with that call's metadata.
     std::unordered_map<int32_t, int32_t> pending_tables;
+    // Copies-on-write queued since the last flush, in call order; launched
+    // as one kernel at the start of the next forward (or sync), before any
+    // kernel reads or writes the pools. No queued copy touches a page
+    // another queued copy writes (a conflicting copy flushes the queue).
+    std::vector<mphip::TailCopy> pending_copies;
     // Pinned host staging of the metadata upload and of the results, reused
     // across calls; `staged` marks the last upload out of the meta staging.
     int32_t* host_meta = nullptr;
@@ -322,19 +327,41 @@ size_t take_pending_tables(mp_hip* h, int32_t* dst) {
     return n;
 }
 
-// Uploads and applies pending block-table entries on the context's stream.
-int flush_tables(mp_hip* h) {
-    if (h->pending_tables.empty()) return MP_OK;
-    const size_t n = h->pending_tables.size();
-    int status = ensure_call_buffers(h, 2 * n);
+// Appends the queued copies-on-write to `dst` (three int32 each) and clears
+// them; returns the number of copies.
+size_t take_pending_copies(mp_hip* h, int32_t* dst) {
+    const size_t n = h->pending_copies.size();
+    if (n) std::memcpy(dst, h->pending_copies.data(), sizeof(mphip::TailCopy) * n);
+    h->pending_copies.clear();
+    return n;
+}
+
+// Launches `count` copies from the device metadata at `at`.
+int launch_copies(mp_hip* h, const int32_t* at, size_t count) {
+    const mp_model_desc& c = h->model;
+    return check(h, mphip::launch_copy_tails(h->stream, h->keys, h->values,
+                                             reinterpret_cast<const mphip::TailCopy*>(at), (int)count, c.layers,
+                                             h->kv.block_tokens, c.kv_heads, c.hidden / c.heads),
+                 "COW copy");
+}
+
+// Uploads and applies the queued block-table entries and copies-on-write on
+// the context's stream.
+int flush_pending(mp_hip* h) {
+    static_assert(sizeof(mphip::TailCopy) == 3 * sizeof(int32_t), "copies travel as three int32");
+    if (h->pending_tables.empty() && h->pending_copies.empty()) return MP_OK;
+    const size_t n = h->pending_tables.size(), copies = h->pending_copies.size();
+    int status = ensure_call_buffers(h, 2 * n + 3 * copies);
     if (status) return status;
     take_pending_tables(h, h->host_meta);
-    status = check(h, hipMemcpyAsync(h->meta, h->host_meta, sizeof(int32_t) * 2 * n, hipMemcpyHostToDevice,
-                                      h->stream), "upload block table entries");
+    take_pending_copies(h, h->host_meta + 2 * n);
+    status = check(h, hipMemcpyAsync(h->meta, h->host_meta, sizeof(int32_t) * (2 * n + 3 * copies),
+                                      hipMemcpyHostToDevice, h->stream), "upload block table entries");
     if (!status) status = check(h, hipEventRecord(h->staged, h->stream), "metadata upload event");
-    if (!status)
+    if (!status && n)
         status = check(h, mphip::launch_table_update(h->stream, h->tables, reinterpret_cast<const int2*>(h->meta),
                                                      (int)n), "apply block table entries");
+    if (!status && copies) status = launch_copies(h, h->meta + 2 * n, copies);
     return status;
 }
 
@@ -553,7 +580,7 @@ int mp_hip_copy_tail(mp_hip* h, const mp_tail_region* r) {
     // every layer, pitch = one page-layer span, width = valid tokens x
     // kv_width, page-aligned source and destination. The pools keep the
     // reference's page bases but their own order inside a page, so the copy
-    // moves the valid slots in that order (launch_copy_tail).
+    // moves the valid slots in that order (launch_copy_tails).
     const mp_model_desc& c = h->model;
     const uint64_t kvw = (uint64_t)kv_width(c);
     const uint64_t page = (uint64_t)h->kv.block_tokens * kvw;
@@ -562,24 +589,34 @@ int mp_hip_copy_tail(mp_hip* h, const mp_tail_region* r) {
         r->destination % block || r->source % block || r->destination / block >= (uint64_t)h->kv.max_blocks ||
         r->source / block >= (uint64_t)h->kv.max_blocks)
         return fail(h, MP_INVALID_ARGUMENT, "tail copy region is not a page region of the pools");
-    const int status = check(h, mphip::launch_copy_tail(h->stream, h->keys, h->values, r->destination, r->source,
-                                                        c.layers, (int)(r->width / kvw), h->kv.block_tokens,
-                                                        c.kv_heads, c.hidden / c.heads),
-                             "COW copy");
-    if (!status) {
-        ++h->stats.cow_copies;
-        h->stats.cow_bytes += 2 * r->width * r->rows * sizeof(float);
-    }
-    return status;
+    const mphip::TailCopy copy{(int32_t)(r->destination / block), (int32_t)(r->source / block),
+                               (int32_t)(r->width / kvw)};
+    // Queued copies run side by side; one that reads or writes a page a
+    // queued copy writes, or writes a page a queued copy reads, waits for
+    // them (the queue is flushed first).
+    for (const mphip::TailCopy& q : h->pending_copies)
+        if (q.destination == copy.source || q.destination == copy.destination || q.source == copy.destination) {
+            const int status = flush_pending(h);
+            if (status) return status;
+            break;
+        }
+    h->pending_copies.push_back(copy);
+    ++h->stats.cow_copies;
+    h->stats.cow_bytes += 2 * r->width * r->rows * sizeof(float);
+    return MP_OK;
 }
 
 int mp_hip_copy_tail_timed(mp_hip* h, const mp_tail_region* region, uint64_t* nanoseconds) {
     if (!h || !nanoseconds) return MP_INVALID_ARGUMENT;
+    // Earlier queued work goes first, outside the timed span.
+    int status = flush_pending(h);
+    if (status) return status;
     hipEvent_t begin = nullptr, end = nullptr;
-    int status = check(h, hipEventCreate(&begin), "COW event begin");
+    status = check(h, hipEventCreate(&begin), "COW event begin");
     if (!status) status = check(h, hipEventCreate(&end), "COW event end");
-    if (!status) status = check(h, hipEventRecord(begin, h->stream), "COW timing begin");
     if (!status) status = mp_hip_copy_tail(h, region);
+    if (!status) status = check(h, hipEventRecord(begin, h->stream), "COW timing begin");
+    if (!status) status = flush_pending(h);
     if (!status) status = check(h, hipEventRecord(end, h->stream), "COW timing end");
     if (!status) status = check(h, hipEventSynchronize(end), "COW completion");
     float ms = 0.0f;
@@ -635,6 +672,7 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
     for (const Block& b : blocks) items += (size_t)(b.length + 255) / 256;
     const size_t nblocks = blocks.size();
     const size_t table_pairs = h->pending_tables.size();
+    const size_t copies = h->pending_copies.size();
     // Fast-mode decode attention: work items (row, KV head, first token,
     // tokens) over 128-token splits, and per row (first item, splits per KV
     // head). The split depends on nothing but the row, so a row's result
@@ -645,7 +683,8 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
     size_t fast_items = 0;
     if (fast_decode)
         for (int q = 0; q < nseq; ++q) fast_items += (size_t)c.kv_heads * ((steps[q].used + 1 + split - 1) / split);
-    const size_t base_entries = 3 * (size_t)R + 2 * (size_t)nseq + 2 * nblocks + 2 * items + 2 * table_pairs;
+    const size_t base_entries =
+        3 * (size_t)R + 2 * (size_t)nseq + 2 * nblocks + 2 * items + 2 * table_pairs + 3 * copies;
     const size_t fast_at = (base_entries + 3) / 4 * 4;  // int4 items need 16-byte alignment
     const size_t entries = fast_decode ? fast_at + 4 * fast_items + 2 * (size_t)R : base_entries;
     if ((status = ensure_call_buffers(h, entries))) return status;
@@ -671,7 +710,9 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
     int32_t* m_blocks = m_last + nseq;
     int32_t* m_items = m_blocks + 2 * nblocks;
     int32_t* m_tables = m_items + 2 * items;
+    int32_t* m_copies = m_tables + 2 * table_pairs;
     take_pending_tables(h, m_tables);
+    take_pending_copies(h, m_copies);
     int r = 0;
     for (int s = 0; s < nseq; ++s) {
         for (int i = 0; i < steps[s].count; ++i, ++r) {
@@ -716,6 +757,7 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
         status = check(h, mphip::launch_table_update(h->stream, h->tables,
                                                      reinterpret_cast<const int2*>(h->meta + (m_tables - m0)),
                                                      (int)table_pairs), "apply block table entries");
+    if (!status && copies) status = launch_copies(h, h->meta + (m_copies - m0), copies);
     if (status) return status;
     h->stats.token_uploaded_bytes += sizeof(int32_t) * R;
     mphip::RowMeta meta{h->meta, h->meta + R, h->meta + 2 * (size_t)R, h->meta + 3 * (size_t)R,
@@ -1019,7 +1061,7 @@ int mp_hip_paged_attention_decode(const float* q, const float* keys, const float
 
 int mp_hip_sync(mp_hip* h) {
     if (!h) return MP_INVALID_ARGUMENT;
-    const int status = flush_tables(h);
+    const int status = flush_pending(h);
     if (status) return status;
     return check(h, hipStreamSynchronize(h->stream), "model completion");
 }

@@ -226,11 +226,16 @@ hipError_t launch_attention_single(hipStream_t s, const float* q, const float* k
 // Score floats per row that fit in LDS.
 constexpr int kAttentionLdsScores = 10240;
 
-// Copy-on-write of a page's first `valid` token slots, layers 0..layers-1,
-// in both pools, in the device page order of layout.h. destination and
-// source are float offsets of (page, layer 0), multiples of a page-layer span.
-hipError_t launch_copy_tail(hipStream_t s, float* keys, float* values, uint64_t destination, uint64_t source,
-                            int layers, int valid, int block_tokens, int kv_heads, int dim);
+// One copy-on-write: the first `valid` token slots of page `source` into
+// page `destination` (block ids), every layer, both pools.
+struct TailCopy {
+    int32_t destination, source, valid;
+};
+
+// `count` copies-on-write (device array), in the device page order of
+// layout.h, as one launch; no copy reads or writes a page another one writes.
+hipError_t launch_copy_tails(hipStream_t s, float* keys, float* values, const TailCopy* copies, int count,
+                             int layers, int block_tokens, int kv_heads, int dim);
 
 // tables[updates[i].x] = updates[i].y for i < count (queued block-table
 // entries; the indices are distinct).

@@ -221,15 +221,19 @@ __global__ void rope_append_kernel(float* __restrict__ qkv, int width, int heads
 }
 
 // Copy-on-write of the first `valid` token slots of a page, every layer, in
-// both pools (block x = layer, block y = pool). In the device page order the
-// valid slots of a key page are, per (KV head, group of 4 dims), a run of
-// `valid` float4 (key_offset); those of a value page are, per KV head, the
-// first ceil(valid/4) groups of dim float4 (value_offset; the last group may
-// carry slots past the tail, which later appends overwrite before any read).
-// Offsets are float4 indices of the (page, layer 0) spans; `page4` is one
-// page-layer span in float4.
-__global__ void copy_tail_kernel(float4* keys, float4* values, uint64_t destination, uint64_t source,
-                                 uint32_t page4, int valid, int block_tokens, int kv_heads, int dim) {
+// both pools (block x = layer, block y = pool, block z = copy). In the device
+// page order the valid slots of a key page are, per (KV head, group of 4
+// dims), a run of `valid` float4 (key_offset); those of a value page are, per
+// KV head, the first ceil(valid/4) groups of dim float4 (value_offset; the
+// last group may carry slots past the tail, which later appends overwrite
+// before any read). `page4` is one page-layer span in float4; a block id
+// times `layers` page-layer spans is the (page, layer 0) span.
+__global__ void copy_tails_kernel(float4* keys, float4* values, const TailCopy* __restrict__ copies,
+                                  uint32_t page4, int layers, int block_tokens, int kv_heads, int dim) {
+    const TailCopy c = copies[blockIdx.z];
+    const int valid = c.valid;
+    const uint64_t destination = (uint64_t)c.destination * layers * page4;
+    const uint64_t source = (uint64_t)c.source * layers * page4;
     const bool is_key = blockIdx.y == 0;
     float4* pool = is_key ? keys : values;
     const uint64_t layer = blockIdx.x;
@@ -303,13 +307,13 @@ hipError_t launch_rope_append(hipStream_t s, float* qkv, int width, int rows, in
     return hipGetLastError();
 }
 
-hipError_t launch_copy_tail(hipStream_t s, float* keys, float* values, uint64_t destination, uint64_t source,
-                            int layers, int valid, int block_tokens, int kv_heads, int dim) {
-    if (layers <= 0 || valid <= 0) return hipSuccess;
+hipError_t launch_copy_tails(hipStream_t s, float* keys, float* values, const TailCopy* copies, int count,
+                             int layers, int block_tokens, int kv_heads, int dim) {
+    if (layers <= 0 || count <= 0) return hipSuccess;
     const uint32_t page4 = (uint32_t)(block_tokens * kv_heads * dim / 4);
-    copy_tail_kernel<<<dim3((unsigned)layers, 2), 256, 0, s>>>(
-        reinterpret_cast<float4*>(keys), reinterpret_cast<float4*>(values), destination / 4, source / 4, page4,
-        valid, block_tokens, kv_heads, dim);
+    copy_tails_kernel<<<dim3((unsigned)layers, 2, (unsigned)count), 256, 0, s>>>(
+        reinterpret_cast<float4*>(keys), reinterpret_cast<float4*>(values), copies, page4, layers, block_tokens,
+        kv_heads, dim);
     return hipGetLastError();
 }
 

@@ -4,8 +4,12 @@
 // Storage: nodes live in one vector and refer to each other by index. A
 // node's children are a vector sorted by edge (lexicographic token order),
 // and the children that hold a lease form a second sorted vector. Recency
-// is a use counter per leased node plus an ordered index from counter to
-// node, so the least recently used lease is the first entry of the index.
+// is a doubly linked list through the leased nodes, oldest first (a use
+// moves a node to the newest end; nothing allocates). Publishing keeps the
+// node path of the previous publication as a hint: a hinted node is taken
+// when it is still the child of the expected parent with the page's tokens
+// (a pruned node has no parent), so consecutive publications of one history,
+// or of histories sharing a prefix, find their pages without a search.
 //
 // The choices that decide which physical blocks a sequence receives, and
 // therefore must match the reference exactly:
@@ -23,7 +27,6 @@
 #include "miniprefix/prefix_cache.h"
 
 #include <algorithm>
-#include <map>
 
 namespace miniprefix {
 namespace {
@@ -55,7 +58,7 @@ private:
         std::vector<int> children;  // sorted by edge
         std::vector<int> leased;    // the children holding a lease, sorted by edge
         int block = kNone;
-        std::uint64_t last_use = 0;
+        int older = kNone, newer = kNone;  // recency list of leased nodes
     };
 
     Node& at(int id) { return nodes_[static_cast<std::size_t>(id)]; }
@@ -142,23 +145,30 @@ public:
         return {best, length};
     }
 
+    // `id` when it is the child of `parent` whose edge is the run.
+    bool is_child(int id, int parent, const std::int32_t* run, std::size_t n) const {
+        if (id < 0 || static_cast<std::size_t>(id) >= nodes_.size()) return false;
+        const Node& node = at(id);
+        return node.parent == parent && node.edge.size() == n && std::equal(node.edge.begin(), node.edge.end(), run);
+    }
+
     void lease(int id, int block) {
         Node& node = at(id);
         std::vector<int>& list = at(node.parent).leased;
         list.insert(first_not_less(list, node.edge.data(), node.edge.size()), id);
         node.block = block;
-        node.last_use = ++clock_;
-        recency_.emplace(node.last_use, id);
+        link_newest(id);
         ++leases_per_block_[static_cast<std::size_t>(block)];
         ++leases_;
     }
 
     void touch(int id) {
-        Node& node = at(id);
-        recency_.erase(node.last_use);
-        node.last_use = ++clock_;
-        recency_.emplace(node.last_use, id);
+        if (newest_ == id) return;
+        unlink(id);
+        link_newest(id);
     }
+
+    std::vector<int>& hint() { return hint_; }
 
     // Drops the lease of `id` (one block reference) and removes the
     // unleased leaves this leaves behind, never `keep`.
@@ -166,7 +176,7 @@ public:
         Node& node = at(id);
         std::vector<int>& list = at(node.parent).leased;
         list.erase(first_not_less(list, node.edge.data(), node.edge.size()));
-        recency_.erase(node.last_use);
+        unlink(id);
         const int block = node.block;
         node.block = kNone;
         --leases_per_block_[static_cast<std::size_t>(block)];
@@ -175,7 +185,7 @@ public:
         prune(id, keep);
     }
 
-    void evict_oldest(KvBlockPool& pool, int keep = kNone) noexcept { unlease(pool, recency_.begin()->second, keep); }
+    void evict_oldest(KvBlockPool& pool, int keep = kNone) noexcept { unlease(pool, oldest_, keep); }
 
     // Removes `id` and then its ancestors while they are unleased leaves.
     void prune(int id, int keep = kNone) noexcept {
@@ -210,11 +220,28 @@ public:
     }
 
 private:
+    void link_newest(int id) {
+        Node& node = at(id);
+        node.older = newest_;
+        node.newer = kNone;
+        if (newest_ != kNone) at(newest_).newer = id;
+        else oldest_ = id;
+        newest_ = id;
+    }
+    void unlink(int id) {
+        Node& node = at(id);
+        if (node.older != kNone) at(node.older).newer = node.newer;
+        else oldest_ = node.newer;
+        if (node.newer != kNone) at(node.newer).older = node.older;
+        else newest_ = node.older;
+        node.older = node.newer = kNone;
+    }
+
     std::vector<Node> nodes_;  // nodes_[kRoot] is the empty root
     std::vector<int> free_;
     std::vector<int> stack_;
-    std::map<std::uint64_t, int> recency_;  // last use -> leased node, oldest first
-    std::uint64_t clock_ = 0;
+    std::vector<int> hint_;  // node path of the previous publication
+    int oldest_ = kNone, newest_ = kNone;  // recency list ends
     std::vector<std::size_t> leases_per_block_;
     std::size_t leases_ = 0, live_nodes_ = 0, key_tokens_ = 0;
 };
@@ -280,10 +307,13 @@ void ExactPrefixCache::publish(const PagedSequence& sequence) {
     const std::size_t capacity = static_cast<std::size_t>(pool_.config().prefix_cache_blocks);
     const std::size_t pages = std::min({sequence.blocks.size(), (used + page - 1) / page, capacity});
     int parent = Tree::kRoot;
+    std::vector<int>& hint = tree_->hint();
+    if (hint.capacity() < pages) hint.reserve(pages);
     for (std::size_t i = 0; i < pages; ++i) {
         const std::int32_t* run = sequence.tokens.data() + i * page;
         const std::size_t length = std::min(page, used - i * page);
-        int node = tree_->child(parent, run, length);
+        int node = i < hint.size() && tree_->is_child(hint[i], parent, run, length) ? hint[i]
+                                                                                    : tree_->child(parent, run, length);
         if (node == Tree::kNone) node = tree_->add_child(parent, run, length);
         if (tree_->leased(node)) {
             tree_->touch(node);
@@ -301,8 +331,11 @@ void ExactPrefixCache::publish(const PagedSequence& sequence) {
             }
             tree_->lease(node, block);
         }
+        if (i < hint.size()) hint[i] = node;
+        else hint.push_back(node);
         parent = node;
     }
+    hint.resize(pages);
 }
 
 }  // namespace miniprefix
