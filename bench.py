@@ -369,6 +369,115 @@ def summarise_counters(fetch_csv: str, write_csv: str, bench_json: str, out: str
     print(json.dumps(result, indent=1))
 
 
+def summarise_trace(trace_csv: str, steps: str, out: str, command: str):
+    """Markdown table of a rocprofv3 --kernel-trace run of bench.py: every
+    kernel of the last `steps` engine steps (a step ends with the LM head's
+    argmax kernel), its launches, average and minimum duration and time per
+    step, then the kernels of one layer in launch order."""
+    steps = int(steps)
+    rows = sorted(csv.DictReader(open(trace_csv)), key=lambda r: int(r["Start_Timestamp"]))
+    name = lambda r: r["Kernel_Name"].replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0]
+    dur = lambda r: int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+    ends = [i for i, r in enumerate(rows) if "head_argmax_kernel" in name(r)]
+    if len(ends) < steps + 1:
+        raise SystemExit(f"{trace_csv}: {len(ends) - 1} complete steps, {steps} asked for")
+    window = rows[ends[-steps - 1] + 1:ends[-1] + 1]
+    span = int(window[-1]["End_Timestamp"]) - int(window[0]["Start_Timestamp"])
+    busy = sum(dur(r) for r in window)
+    per = defaultdict(list)
+    for r in window:
+        per[(name(r), r["Grid_Size_X"], r["Workgroup_Size_X"])].append(dur(r))
+    lines = [f"# Kernel trace: last {steps} steps", "", f"Command: `{command}`", "",
+             f"Trace: {steps} steps in {span / 1e6:.3f} ms on the GPU clock ({span / 1e3 / steps:.1f} us per step "
+             f"under the profiler); kernels busy {busy / 1e6:.3f} ms ({busy / 1e3 / steps:.1f} us per step).", "",
+             "| kernel | grid (threads) | work-group | launches | avg us | min us | us per step | % of busy |",
+             "|---|---|---|---|---|---|---|---|"]
+    for (k, grid, wg), v in sorted(per.items(), key=lambda kv: -sum(kv[1])):
+        lines.append(f"| `{k}` | {grid} | {wg} | {len(v)} | {np.mean(v) / 1e3:.2f} | {min(v) / 1e3:.2f} | "
+                     f"{sum(v) / 1e3 / steps:.2f} | {100 * sum(v) / busy:.1f} |")
+    # One layer in launch order: the kernels from one launch of the layer's
+    # first projection (the step's first matrix kernel) to the next.
+    starter = next(name(r) for r in window if "gemm" in name(r))
+    order, layer, instances = defaultdict(list), [], 0
+    for r in window:
+        if name(r) == starter and layer:
+            for i, (k, d) in enumerate(layer):
+                order[(i, k)].append(d)
+            instances += 1
+            layer = []
+        if name(r) == starter or layer:
+            layer.append((name(r), dur(r)))
+    lines += ["", f"One layer in launch order (averages over the {steps} steps' layers):", "",
+              "| # | kernel | avg us |", "|---|---|---|"]
+    total = 0.0
+    for (i, k), v in sorted(order.items()):
+        if len(v) * 2 >= instances:
+            lines.append(f"| {i} | `{k}` | {np.mean(v) / 1e3:.2f} |")
+            total += np.mean(v) / 1e3
+    lines += [f"| | sum | {total:.2f} |", ""]
+    Path(out).write_text("\n".join(lines))
+    print("\n".join(lines))
+
+
+def summarise_sq(counter_csv: str, trace_csv: str, out: str, command: str):
+    """Markdown table of a rocprofv3 --pmc run of bench.py with the SQ
+    counters SQ_WAVE_CYCLES SQ_BUSY_CYCLES SQ_ACTIVE_INST_VALU SQ_INSTS_VALU
+    SQ_INSTS_MFMA SQ_VALU_MFMA_BUSY_CYCLES SQ_INSTS_VALU_MFMA_MOPS_F32
+    SQ_WAIT_INST_ANY GRBM_GUI_ACTIVE, for the decode step's kernels. The
+    matrix-core utilisation divides a launch's SQ_VALU_MFMA_BUSY_CYCLES
+    (summed over SIMDs) by all 1,024 SIMDs over the kernel's average
+    duration in a --kernel-trace run of the same workload (`trace_csv`; the
+    counter run serialises dispatches, so its own cycle counts include the
+    profiler's gaps) at the 2.4 GHz peak engine clock."""
+    clean = lambda n: n.replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0]
+    decode = ("fast_attention_kernel<", "fast_attention_merge_kernel", "fast_gemm_kernel<4, true, false, 1, 2, 6>",
+              "fast_gemm_kernel<1, false, false, 1, 1, 12>", "fast_gemm_kernel<2, true, false, 2, 1, 6>",
+              "fast_gemm_kernel<3, true, true, 4, 4, 3>")
+    pick = lambda n: next((k for k in decode if k in n), None)
+    per, meta = defaultdict(dict), {}
+    for r in csv.DictReader(open(counter_csv)):
+        k = pick(clean(r["Kernel_Name"]))
+        if k is None:
+            continue
+        # prefill runs the same residual instantiation on other shapes
+        if "<1, false, false, 1, 1, 12>" in k and int(r["Grid_Size"]) != 81920:
+            continue
+        d = int(r["Dispatch_Id"])
+        per[d][r["Counter_Name"]] = float(r["Counter_Value"])
+        meta[d] = k
+    durations = defaultdict(list)
+    for r in csv.DictReader(open(trace_csv)):
+        k = pick(clean(r["Kernel_Name"]))
+        if k and not ("<1, false, false, 1, 1, 12>" in k and int(r["Grid_Size_X"]) != 81920):
+            durations[k].append(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
+    agg, n = defaultdict(lambda: defaultdict(float)), defaultdict(int)
+    for d, c in per.items():
+        n[meta[d]] += 1
+        for k, v in c.items():
+            agg[meta[d]][k] += v
+    simds, clock = 256 * 4, 2.4e9
+    lines = ["# SQ counters of the decode kernels (fast arithmetic)", "", f"Counters: `{command}`", "",
+             "Durations: the --kernel-trace summary of the same workload (decode_config3_fast_kernels.md). "
+             "Matrix-core utilisation = SQ_VALU_MFMA_BUSY_CYCLES per launch / (1,024 SIMDs x average duration x "
+             "2.4 GHz); VALU active and waiting = SQ_ACTIVE_INST_VALU and SQ_WAIT_INST_ANY over SQ_WAVE_CYCLES.", "",
+             "| kernel | launches | avg us | MFMA instr per launch | MFMA busy cycles per launch | matrix-core "
+             "utilisation % | VALU instr per launch | VALU active % of wave cycles | waiting % of wave cycles |",
+             "|---|---|---|---|---|---|---|---|---|"]
+    for k in decode:
+        if k not in agg:
+            continue
+        a, c = agg[k], n[k]
+        us = float(np.mean(durations[k])) / 1e3 if durations[k] else float("nan")
+        busy = a.get("SQ_VALU_MFMA_BUSY_CYCLES", 0) / c
+        wave = a.get("SQ_WAVE_CYCLES", 0) / c
+        lines.append(f"| `{k}` | {c} | {us:.2f} | {a.get('SQ_INSTS_MFMA', 0) / c:.0f} | {busy:.0f} | "
+                     f"{100 * busy / (simds * us * 1e-6 * clock):.1f} | {a.get('SQ_INSTS_VALU', 0) / c:.0f} | "
+                     f"{100 * a.get('SQ_ACTIVE_INST_VALU', 0) / c / wave:.1f} | "
+                     f"{100 * a.get('SQ_WAIT_INST_ANY', 0) / c / wave:.1f} |")
+    Path(out).write_text("\n".join(lines) + "\n")
+    print("\n".join(lines))
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -383,7 +492,17 @@ def main():
     ap.add_argument("--cost-timing", action="store_true",
                     help="time the host prefix-cache lookups/publications and the COW copies of the timed steps")
     ap.add_argument("--summarise-counters", nargs=4, metavar=("FETCH_CSV", "WRITE_CSV", "BENCH_JSON", "OUT"))
+    ap.add_argument("--summarise-sq", nargs=4, metavar=("COUNTER_CSV", "TRACE_CSV", "OUT", "COMMAND"),
+                    help="markdown summary of a rocprofv3 --pmc run of this script with the SQ counters")
+    ap.add_argument("--summarise-trace", nargs=4, metavar=("TRACE_CSV", "STEPS", "OUT", "COMMAND"),
+                    help="markdown summary of a rocprofv3 --kernel-trace run of this script")
     args = ap.parse_args()
+    if args.summarise_sq:
+        summarise_sq(*args.summarise_sq)
+        return
+    if args.summarise_trace:
+        summarise_trace(*args.summarise_trace)
+        return
     if args.summarise_counters:
         summarise_counters(*args.summarise_counters)
         return
