@@ -681,15 +681,21 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
     const bool fast_decode = h->fast && decode && h->kv.block_tokens == 16 && dim_ == 64 && group_ <= 4;
     const int split = mphip::fast_attention_split_tokens();
     size_t fast_items = 0;
+    int max_splits = 0;
     if (fast_decode)
-        for (int q = 0; q < nseq; ++q) fast_items += (size_t)c.kv_heads * ((steps[q].used + 1 + split - 1) / split);
+        for (int q = 0; q < nseq; ++q) {
+            const int splits = (steps[q].used + 1 + split - 1) / split;
+            fast_items += (size_t)c.kv_heads * splits;
+            max_splits = std::max(max_splits, splits);
+        }
     const size_t base_entries =
         3 * (size_t)R + 2 * (size_t)nseq + 2 * nblocks + 2 * items + 2 * table_pairs + 3 * copies;
     const size_t fast_at = (base_entries + 3) / 4 * 4;  // int4 items need 16-byte alignment
-    const size_t entries = fast_decode ? fast_at + 4 * fast_items + 2 * (size_t)R : base_entries;
+    const size_t entries = fast_decode ? fast_at + 4 * fast_items : base_entries;
     if ((status = ensure_call_buffers(h, entries))) return status;
     if (fast_decode) {
-        const size_t need = fast_items * group_ * (64 + 2);
+        // Partials of (row, KV head, split) at a fixed stride of max_splits.
+        const size_t need = (size_t)R * c.kv_heads * max_splits * group_ * (64 + 2);
         if (need > h->fast_partial_floats) {
             if ((status = stream_sync(h))) return status;
             device_free(h, h->fast_partials);
@@ -733,14 +739,11 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
         }
     }
     int32_t* const m_fast = m0 + fast_at;
-    int32_t* const m_row_items = m_fast + 4 * fast_items;
     if (fast_decode) {
         // Decode: row q is sequence q's only row.
         size_t f = 0;
         for (int q = 0; q < nseq; ++q) {
             const int length = steps[q].used + 1, splits = (length + split - 1) / split;
-            m_row_items[2 * q] = (int32_t)f;
-            m_row_items[2 * q + 1] = splits;
             for (int kvh = 0; kvh < c.kv_heads; ++kvh)
                 for (int sp = 0; sp < splits; ++sp, ++f) {
                     m_fast[4 * f] = q;
@@ -872,9 +875,9 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
         mphip::FastAttentionWork fw{};
         fw.items = h->meta + (m_fast - m0);
         fw.items_count = (int)fast_items;
-        fw.row_items = h->meta + (m_row_items - m0);
+        fw.max_splits = max_splits;
         fw.partial_out = h->fast_partials;
-        fw.partial_ml = h->fast_partials + fast_items * group_ * 64;
+        fw.partial_ml = h->fast_partials + (size_t)R * c.kv_heads * max_splits * group_ * 64;
         fw.kv_heads = c.kv_heads;
         auto set_prefetch = [&](int l) {
             // This layer's remaining projections, then the next layer's q|k|v.

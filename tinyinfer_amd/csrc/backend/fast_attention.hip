@@ -213,9 +213,10 @@ __global__ __launch_bounds__(kItemsPerGroup * 64) void fast_attention_kernel(con
         for (int h = 0; h < G; ++h) out[quad_index(row, (kvh * G + h) * kDim + lane, ldo)] = acc[h] / l[h];
         return;
     }
+    const size_t slot = ((size_t)row * w.kv_heads + kvh) * w.max_splits + t0 / kSplitTokens;
 #pragma unroll
     for (int h = 0; h < G; ++h) {
-        const size_t at = (size_t)index * G + h;
+        const size_t at = slot * G + h;
         w.partial_out[at * kDim + lane] = acc[h];
         if (lane == 0) {
             w.partial_ml[at * 2] = m[h];
@@ -227,9 +228,11 @@ __global__ __launch_bounds__(kItemsPerGroup * 64) void fast_attention_kernel(con
 // out[row][h*64 + d] for rows of more than one split: the splits of
 // (row, h/G) combined in split order. One wavefront per (row, head): lane
 // sp holds split sp's (max, denominator) and weight exp(m_sp - max); lane d
-// sums its dimension over the splits, the first kMergeHeld partial outputs
-// loaded together with the (max, denominator) pairs.
-__global__ __launch_bounds__(256) void fast_attention_merge_kernel(int rows, int heads, int kv_heads,
+// sums its dimension over the splits. The partials sit at a fixed stride
+// per (row, KV head), so the first 64 (max, denominator) pairs and the
+// first kMergeHeld partial outputs are loaded together with the row's
+// position, in one round.
+__global__ __launch_bounds__(256) void fast_attention_merge_kernel(int rows, int heads, int kv_heads, RowMeta meta,
                                                                    FastAttentionWork w, float* __restrict__ out,
                                                                    int ldo) {
     const int lane = threadIdx.x & 63;
@@ -237,21 +240,23 @@ __global__ __launch_bounds__(256) void fast_attention_merge_kernel(int rows, int
     if (pair >= rows * heads) return;
     const int row = pair / heads, h = pair % heads;
     const int G = heads / kv_heads, kvh = h / G, hg = h % G;
-    const int2 ri = reinterpret_cast<const int2*>(w.row_items)[row];
-    const int splits = ri.y;
-    if (splits == 1) return;  // written by the split kernel
-    const size_t item0 = (size_t)ri.x + (size_t)kvh * splits;  // items of (row, kvh) in split order
-    auto at = [&](int sp) { return (item0 + sp) * G + hg; };
+    const int S = w.max_splits;
+    const size_t slot0 = ((size_t)row * kv_heads + kvh) * S;  // split 0 of (row, kvh)
+    auto at = [&](int sp) { return (slot0 + sp) * G + hg; };
+    int pos = meta.row_pos[row];
     float num = 0.0f, den = 0.0f, cm = 0.0f;
-    for (int s0 = 0; s0 < splits; s0 += 64) {
-        const int sp = s0 + lane;
-        const int count = min(64, splits - s0);
-        const float mv = w.partial_ml[at(s0 + min(lane, count - 1)) * 2];
-        const float lv = w.partial_ml[at(s0 + min(lane, count - 1)) * 2 + 1];
-        float ov[kMergeHeld];
+    // Splits s0.. s0+63 (loaded up to the longest row's splits, in bounds),
+    // used up to this row's.
+    float mv, lv, ov[kMergeHeld];
+    auto load = [&](int s0) {
+        const int loaded = min(64, S - s0);
+        mv = w.partial_ml[at(s0 + min(lane, loaded - 1)) * 2];
+        lv = w.partial_ml[at(s0 + min(lane, loaded - 1)) * 2 + 1];
 #pragma unroll
-        for (int j = 0; j < kMergeHeld; ++j) ov[j] = w.partial_out[at(s0 + min(j, count - 1)) * kDim + lane];
-        const bool mine = sp < splits;
+        for (int j = 0; j < kMergeHeld; ++j) ov[j] = w.partial_out[at(s0 + min(j, loaded - 1)) * kDim + lane];
+    };
+    auto combine = [&](int s0, int count) {
+        const bool mine = lane < count;
         float hm = mine ? mv : -__builtin_inff();
         hm = fmaxf(hm, dpp<kDppQuadXor1>(hm));
         hm = fmaxf(hm, dpp<kDppQuadXor2>(hm));
@@ -267,8 +272,19 @@ __global__ __launch_bounds__(256) void fast_attention_merge_kernel(int rows, int
             if (j < count) num += ov[j] * lane_value(f, j);
         for (int j = kMergeHeld; j < count; ++j) num += w.partial_out[at(s0 + j) * kDim + lane] * lane_value(f, j);
         cm = m_new;
+    };
+    load(0);
+    // The row's position is first needed here, after the loads above are in flight.
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("" : "+v"(pos));
+    const int splits = (pos + kSplitTokens) / kSplitTokens;  // ceil((pos + 1) / split)
+    combine(0, min(64, splits));
+    for (int s0 = 64; s0 < splits; s0 += 64) {
+        load(s0);
+        combine(s0, min(64, splits - s0));
     }
-    out[quad_index(row, h * kDim + lane, ldo)] = num / den;
+    // A row of one split was written by the split kernel.
+    if (splits > 1) out[quad_index(row, h * kDim + lane, ldo)] = num / den;
 }
 
 template <int G>
@@ -298,7 +314,7 @@ hipError_t launch_fast_attention(hipStream_t s, const float* qkv, int ldq, int r
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    fast_attention_merge_kernel<<<(rows * heads + 3) / 4, 256, 0, s>>>(rows, heads, kv_heads, w, out, ldo);
+    fast_attention_merge_kernel<<<(rows * heads + 3) / 4, 256, 0, s>>>(rows, heads, kv_heads, meta, w, out, ldo);
     return hipGetLastError();
 }
 

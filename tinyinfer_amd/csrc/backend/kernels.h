@@ -130,9 +130,11 @@ struct FastAttentionWork {
     // the items of a row are KV head major, then split order
     const int32_t* items;
     int items_count;
-    const int32_t* row_items;  // per row: first work item and splits per KV head (int2)
-    float* partial_out;
-    float* partial_ml;
+    // Splits of the longest row; the partial results of (row, KV head,
+    // split) sit at slot (row * kv_heads + KV head) * max_splits + split.
+    int max_splits;
+    float* partial_out;  // [slot][G][64]
+    float* partial_ml;   // [slot][G][2]: running maximum, denominator
     int kv_heads;
     // Weights the next projections read, touched by the attention's
     // wavefronts (one dword per 128-byte line, 8 KB per wavefront, results
