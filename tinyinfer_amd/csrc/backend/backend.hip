@@ -389,7 +389,7 @@ int mp_hip_create(const mp_model_desc* model, const mp_kv_desc* kv, mp_hip** out
         return MP_INVALID_ARGUMENT;
     }
     h->fast = c.arithmetic == MP_ARITHMETIC_FAST && c.hidden % 16 == 0 && c.intermediate % 16 == 0 &&
-              qkv_width(c) % 16 == 0 && c.vocabulary % 16 == 0;
+              kv_width(c) % 16 == 0 && c.vocabulary % 16 == 0;
     // Pages are streamed as float4 runs of tokens: the device path needs a
     // page size that is a multiple of 4 tokens, head_dim a multiple of 4 and
     // at most 64 (one output lane per d) and at most 8 query heads per KV
@@ -501,9 +501,11 @@ int mp_hip_upload_tensor(mp_hip* h, int32_t layer, int32_t slot, const float* da
     const int hd = c.hidden, kvw = kv_width(c), in = c.intermediate;
     hipError_t e = hipSuccess;
     const hipMemcpyKind h2d = hipMemcpyHostToDevice;
-    // Projections arrive [in][out] (model.cpp:33-37) and are stored [out][in]
-    // through a staging buffer; norms and the embedding are stored as given.
-    auto transposed = [&](float* dst, int rows, int cols) -> hipError_t {
+    // Projections arrive [in][out] (model.cpp:33-37). The exact arithmetic
+    // stores them [out][in], the fast one in the matrix-core fragment order
+    // of layout.h (the embedding too, which arrives [vocab][hidden] =
+    // [out][in]), through a staging buffer; norms are stored as given.
+    auto staged = [&]() -> hipError_t {
         if (h->staging_floats < count) {
             device_free(h, h->staging);
             h->staging = nullptr;
@@ -511,14 +513,28 @@ int mp_hip_upload_tensor(mp_hip* h, int32_t layer, int32_t slot, const float* da
             if (device_alloc(h, (void**)&h->staging, bytes, "allocate upload staging")) return hipErrorOutOfMemory;
             h->staging_floats = count;
         }
-        hipError_t r = hipMemcpyAsync(h->staging, data, bytes, h2d, h->stream);
-        if (r == hipSuccess) r = mphip::launch_transpose(h->stream, h->staging, dst, rows, cols, rows);
-        return r;
+        return hipMemcpyAsync(h->staging, data, bytes, h2d, h->stream);
+    };
+    auto transposed = [&](float* dst, int rows, int cols) -> hipError_t {
+        hipError_t r = staged();
+        if (r != hipSuccess) return r;
+        return h->fast ? mphip::launch_to_fragments(h->stream, h->staging, dst, cols, rows, true)
+                       : mphip::launch_transpose(h->stream, h->staging, dst, rows, cols, rows);
     };
     if (layer < 0) {
-        if (slot == MP_TENSOR_EMBEDDING) e = hipMemcpyAsync(h->embedding, data, bytes, h2d, h->stream);
-        else if (slot == MP_TENSOR_FINAL_NORM) e = hipMemcpyAsync(h->final_norm, data, bytes, h2d, h->stream);
-        else e = transposed(h->head, hd, c.vocabulary);
+        if (slot == MP_TENSOR_EMBEDDING) {
+            if (!h->fast) {
+                e = hipMemcpyAsync(h->embedding, data, bytes, h2d, h->stream);
+            } else {
+                e = staged();
+                if (e == hipSuccess)
+                    e = mphip::launch_to_fragments(h->stream, h->staging, h->embedding, c.vocabulary, hd, false);
+            }
+        } else if (slot == MP_TENSOR_FINAL_NORM) {
+            e = hipMemcpyAsync(h->final_norm, data, bytes, h2d, h->stream);
+        } else {
+            e = transposed(h->head, hd, c.vocabulary);
+        }
     } else {
         float* qkv = h->qkv[layer];
         switch (slot) {
@@ -849,7 +865,7 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
     mphip::RowRope row_rope{meta, h->tables, h->kv.max_sequence_blocks, h->kv.block_tokens, dim / 2,
                             h->cos_table, h->sin_table, h->row_block, h->row_rope};
     hipError_t e = mphip::launch_embed(s, h->embedding, meta.tokens, h->x, R, hd, device_error,
-                                       fast_decode ? &row_rope : nullptr);
+                                       fast_decode ? &row_rope : nullptr, h->fast);
     if (h->fast) {
         // Matrix-core projections; RMSNorm folded into the next projection
         // through per-16-column sums of squares of the residual stream.

@@ -9,6 +9,8 @@
 // D[4*(l/16)+i][l%16]. Each lane loads a float4 of 4 consecutive k for its
 // row (A) and its column (B); MFMA j of a 16-k step takes component j of
 // both, so the four lane groups l/16 cover k, k+4, k+8, k+12 of the step.
+// The weights are stored in that fragment order (layout.h), so a
+// wavefront's B operand of one step is one contiguous 1 KB load.
 //
 // A work-group of eight wavefronts computes RB 16-row blocks x CB 16-column
 // blocks. The 16-k steps of K are dealt to the wavefronts in turn (step s to
@@ -112,11 +114,13 @@ __global__ __launch_bounds__(kWaves * 64) void fast_gemm_kernel(FastGemmArgs a) 
         const int xrow = GATHER && a.row_map ? a.row_map[r] : r;
         xa[rb] = a.x + ((size_t)(xrow >> 6) * Q * 64 + (xrow & 63)) * 4 + (size_t)(lane >> 4) * 256;
     }
-    // B: column 16cblock + l%16, k 16s + 4(l/16).
+    // B: column 16cblock + l%16, k 16s + 4(l/16): lane l's float4 of the
+    // (cblock, s) fragment (weights in fragment order), one contiguous 1 KB
+    // per wavefront and step.
     const float* wb[NB];
 #pragma unroll
     for (int j = 0; j < CB; ++j) {
-        const size_t off = (size_t)(cblock[j] * 16 + (lane & 15)) * K + (size_t)(lane >> 4) * 4;
+        const size_t off = (size_t)cblock[j] * steps * 256 + (size_t)lane * 4;
         wb[j * M] = a.w + off;
         if (M == 2) wb[j * M + M - 1] = a.w2 + off;
     }
@@ -176,7 +180,7 @@ __global__ __launch_bounds__(kWaves * 64) void fast_gemm_kernel(FastGemmArgs a) 
                 for (int rb = 0; rb < RB; ++rb) av[c][rb] = ld4(xa[rb] + s * 1024);  // 4 quads x 64 rows x 4
 #pragma unroll
                 for (int j = 0; j < NB; ++j)
-                    bv[c][j] = __builtin_nontemporal_load(reinterpret_cast<const f4*>(wb[j] + s * 16));
+                    bv[c][j] = __builtin_nontemporal_load(reinterpret_cast<const f4*>(wb[j] + s * 256));
             }
         }
 #pragma unroll

@@ -163,10 +163,16 @@ struct RowRope {
     float* rope;
 };
 
-// x = embedding rows of `tokens`; also clears the forward's device error
-// word `error` (may be null) and fills `rope` when it is non-null.
+// x = embedding rows of `tokens` (the embedding [vocab][hidden] row-major,
+// or in the fragment order of layout.h when `fragments`); also clears the
+// forward's device error word `error` (may be null) and fills `rope` when it
+// is non-null.
 hipError_t launch_embed(hipStream_t s, const float* embedding, const int32_t* tokens, float* x, int rows,
-                        int hidden, int32_t* error, const RowRope* rope = nullptr);
+                        int hidden, int32_t* error, const RowRope* rope = nullptr, bool fragments = false);
+// dst = the n_out x k_in matrix W (W[n][k]: output n, input k) in the
+// fragment order of layout.h; src holds it [k_in][n_out] (in_out) or
+// [n_out][k_in]. n_out and k_in are multiples of 16.
+hipError_t launch_to_fragments(hipStream_t s, const float* src, float* dst, int n_out, int k_in, bool in_out);
 
 // out[r] = (x[r']*scale_r')*w with scale = 1/sqrt(sequential sum of squares/width + eps);
 // r' = row_map[r] when row_map is non-null, else r.

@@ -9,7 +9,12 @@
 //
 // Projection weights are stored transposed, [out][in] (each output column's
 // weights contiguous along k), so a wavefront that owns one output column
-// reads its weights as a broadcast.
+// reads its weights as a broadcast. The fast arithmetic stores them (and
+// the embedding, which is the tied LM head) in the matrix cores' fragment
+// order instead: for output block nb (16 outputs) and input step s (16
+// inputs), fragment nb * (in/16) + s is 64 float4, float4 l holding
+// W[16nb + l%16][16s + 4(l/16) .. 16s + 4(l/16) + 3], the B operand of lane
+// l for the four 16x16x4 MFMAs of the step.
 //
 // K/V pages: block b of layer l starts at float (b*layers + l)*bt*kv_width,
 // as in the reference pool (paged_kv.cpp:53-56), so page tables, block ids

@@ -16,7 +16,7 @@ namespace {
 __global__ __launch_bounds__(256) void embed_kernel(const float* __restrict__ embedding,
                                                     const int32_t* __restrict__ tokens,
                                                     float* __restrict__ x, int rows, int hidden,
-                                                    int32_t* __restrict__ error, RowRope rope) {
+                                                    int32_t* __restrict__ error, RowRope rope, bool fragments) {
     if (error && blockIdx.x == 0 && threadIdx.x == 0) *error = 0;
     if (rope.rope) {
         const int per = 2 * rope.half + 1;  // cos, sin, then the page
@@ -43,7 +43,15 @@ __global__ __launch_bounds__(256) void embed_kernel(const float* __restrict__ em
         const size_t tq = i >> 6;  // tile * quads + q
         const int q = (int)(tq % quads);
         const int row = (int)(tq / quads) * 64 + r_in;
-        x4[i] = row < rows ? e4[(size_t)tokens[row] * quads + q] : make_float4(0.f, 0.f, 0.f, 0.f);
+        if (row >= rows) {
+            x4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+            continue;
+        }
+        const int t = tokens[row];
+        // Fragment order: quad q of row t is the float4 of lane
+        // t%16 + 16(q%4) in the (t/16, q/4) fragment.
+        x4[i] = fragments ? e4[((size_t)(t >> 4) * (quads >> 2) + (q >> 2)) * 64 + (t & 15) + 16 * (q & 3)]
+                          : e4[(size_t)t * quads + q];
     }
 }
 
@@ -262,6 +270,23 @@ __global__ void table_update_kernel(int32_t* __restrict__ tables, const int2* __
         tables[updates[i].x] = updates[i].y;
 }
 
+// W[n][k] (n < n_out, k < k_in) to the fragment order of layout.h: float4
+// f of the destination is lane f%64 of fragment f/64 = (n/16) * (k_in/16) +
+// k/16, holding W[16(n/16) + lane%16][16(k/16) + 4(lane/16) .. +3].
+__global__ void to_fragments_kernel(const float* __restrict__ src, float* __restrict__ dst, int n_out, int k_in,
+                                    bool in_out) {
+    const size_t total = (size_t)n_out * k_in;
+    const int steps = k_in >> 4;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
+        const int c = (int)(i & 3);
+        const int lane = (int)((i >> 2) & 63);
+        const size_t fragment = i >> 8;
+        const int n = (int)(fragment / steps) * 16 + (lane & 15);
+        const int k = (int)(fragment % steps) * 16 + 4 * (lane >> 4) + c;
+        dst[i] = in_out ? src[(size_t)k * n_out + n] : src[(size_t)n * k_in + k];
+    }
+}
+
 __global__ void transpose_kernel(const float* __restrict__ src, float* __restrict__ dst, int rows, int cols,
                                  int ld_dst) {
     __shared__ float tile[32][33];
@@ -280,13 +305,20 @@ __global__ void transpose_kernel(const float* __restrict__ src, float* __restric
 }  // namespace
 
 hipError_t launch_embed(hipStream_t s, const float* embedding, const int32_t* tokens, float* x, int rows,
-                        int hidden, int32_t* error, const RowRope* rope) {
+                        int hidden, int32_t* error, const RowRope* rope, bool fragments) {
     if (rows <= 0) return hipSuccess;
+    if (fragments && hidden % 16) return hipErrorInvalidValue;
     const size_t total = quad_floats(rows, hidden) / 4;
     const int blocks = (int)std::min<size_t>((total + 255) / 256, 4096);
     RowRope rr{};
     if (rope) rr = *rope;
-    embed_kernel<<<blocks, 256, 0, s>>>(embedding, tokens, x, rows, hidden, error, rr);
+    embed_kernel<<<blocks, 256, 0, s>>>(embedding, tokens, x, rows, hidden, error, rr, fragments);
+    return hipGetLastError();
+}
+
+hipError_t launch_to_fragments(hipStream_t s, const float* src, float* dst, int n_out, int k_in, bool in_out) {
+    if (n_out % 16 || k_in % 16) return hipErrorInvalidValue;
+    to_fragments_kernel<<<4096, 256, 0, s>>>(src, dst, n_out, k_in, in_out);
     return hipGetLastError();
 }
 
