@@ -19,10 +19,12 @@
 // bound by memory latency, not bandwidth, so the loads of a launch must be
 // in flight together, and so are everything the epilogue reads (RMSNorm
 // partials, the residual's old values, the RoPE rows). The partial tiles
-// are then summed through LDS in a fixed order: wavefronts 4-7 into 0-3,
-// then the final sum of each tile ((p0 + p1) + (p2 + p3)) by the wavefront
-// that owns its row block (row block rb to wavefront rb % min(RB, 4)), which
-// runs the epilogue for it. A row's result depends on nothing but the row.
+// are then summed through LDS in a fixed order by the wavefront that owns
+// their row block (row block rb to wavefront rb % min(RB, 4)), which runs
+// the epilogue for it, as ((p0 + p4) + (p1 + p5)) + ((p2 + p6) + (p3 + p7)):
+// with up to 4 tiles from all eight partials after one barrier, with more
+// in two levels (wavefronts 4-7 into 0-3, then the four). A row's result
+// depends on nothing but the row.
 //
 // Work-groups are laid out so that those sharing a column group (one per
 // row group) are dispatched to the same XCD and share its L2 for the
@@ -88,7 +90,11 @@ __global__ __launch_bounds__(kWaves * 64) void fast_gemm_kernel(FastGemmArgs a) 
     constexpr int NB = CB * M;  // B operands per step
     constexpr int T = RB * NB;  // accumulator tiles
     constexpr int OW = RB < 4 ? RB : 4;  // wavefronts that own row blocks
-    __shared__ f4 part_s[kWaves / 2][T][64];
+    // Up to 4 tiles, every wavefront's partials go to LDS at once and one
+    // barrier precedes the owners' sums; more tiles are summed in two levels
+    // (wavefronts 4-7 into 0-3, then to the owners) to halve the LDS.
+    constexpr bool kOneSync = T <= 4;
+    __shared__ f4 part_s[kOneSync ? kWaves : kWaves / 2][T][64];
     __shared__ float ssq_s[NORM ? RB * 16 : 1][kSsqSlots];
     __shared__ float inv_s[RB * 16];
     const int lane = threadIdx.x & 63;
@@ -205,43 +211,73 @@ __global__ __launch_bounds__(kWaves * 64) void fast_gemm_kernel(FastGemmArgs a) 
         float ss = 0.0f;
 #pragma unroll
         for (int u = 0; u < kSsqHeld; ++u) ss += ssv[u];
-        if (ssq_row < RB * 16) {
-            const int r = min(row0 + ssq_row, a.rows - 1);
-            const int pr = GATHER && a.row_map ? a.row_map[r] : r;
-            for (int p = ssq_slot + kSsqHeld * kSsqSlots; p < a.ssq_parts; p += kSsqSlots)
-                ss += a.ssq_in[(size_t)p * a.ssq_stride + pr];
+        const int r = min(row0 + ssq_row, a.rows - 1);
+        const int pr = GATHER && a.row_map ? a.row_map[r] : r;
+        for (int p = ssq_slot + kSsqHeld * kSsqSlots; p < a.ssq_parts; p += kSsqSlots)
+            ss += a.ssq_in[(size_t)p * a.ssq_stride + pr];
+        if constexpr (kOneSync) {
+            // A row's kSsqSlots = 8 slots are 8 consecutive lanes: lane 8r
+            // gets their sum (quads, then the other quad of the eight).
+            ss += dpp<kDppQuadXor1>(ss);
+            ss += dpp<kDppQuadXor2>(ss);
+            ss += __shfl_xor(ss, 4);
+            // 1/sqrt(mean square + eps) of the group's rows.
+            if (ssq_slot == 0 && ssq_row < RB * 16) inv_s[ssq_row] = 1.0f / sqrtf(ss / (float)K + a.eps);
+        } else if (ssq_row < RB * 16) {
             ssq_s[ssq_row][ssq_slot] = ss;
         }
     }
-    // Wavefronts 4-7 into 0-3.
-    if (wave >= kWaves / 2)
-#pragma unroll
-        for (int t = 0; t < T; ++t) part_s[wave - kWaves / 2][t][lane] = acc[t];
-    __syncthreads();
-    if (wave < kWaves / 2)
-#pragma unroll
-        for (int t = 0; t < T; ++t) acc[t] += part_s[wave][t][lane];
-    if (NORM && threadIdx.x < RB * 16) {
-        // 1/sqrt(mean square + eps) of the group's rows.
-        float ss = 0.0f;
-#pragma unroll
-        for (int u = 0; u < kSsqSlots; ++u) ss += ssq_s[threadIdx.x][u];
-        inv_s[threadIdx.x] = 1.0f / sqrtf(ss / (float)K + a.eps);
-    }
-    __syncthreads();
-    // Then each tile's four partials to its owner.
-    if (wave < kWaves / 2)
+    if constexpr (kOneSync) {
+        // Every wavefront's partial tiles, one barrier, then each tile's
+        // eight partials to its owner.
 #pragma unroll
         for (int t = 0; t < T; ++t) part_s[wave][t][lane] = acc[t];
-    __syncthreads();
-    if (wave >= OW) return;
+        __syncthreads();
+        if (wave >= OW) return;
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb) {
-        if (rb % OW != wave) continue;
+        for (int rb = 0; rb < RB; ++rb) {
+            if (rb % OW != wave) continue;
 #pragma unroll
-        for (int j = 0; j < NB; ++j) {
-            const int t = rb * NB + j;
-            acc[t] = (part_s[0][t][lane] + part_s[1][t][lane]) + (part_s[2][t][lane] + part_s[3][t][lane]);
+            for (int j = 0; j < NB; ++j) {
+                const int t = rb * NB + j;
+                // The order of the two-level sums below (wavefront w with
+                // w + 4, then the four in order), whatever the tile count.
+                const f4 q0 = part_s[0][t][lane] + part_s[4][t][lane], q1 = part_s[1][t][lane] + part_s[5][t][lane];
+                const f4 q2 = part_s[2][t][lane] + part_s[6][t][lane], q3 = part_s[3][t][lane] + part_s[7][t][lane];
+                acc[t] = (q0 + q1) + (q2 + q3);
+            }
+        }
+    } else {
+        // Wavefronts 4-7 into 0-3.
+        if (wave >= kWaves / 2)
+#pragma unroll
+            for (int t = 0; t < T; ++t) part_s[wave - kWaves / 2][t][lane] = acc[t];
+        __syncthreads();
+        if (wave < kWaves / 2)
+#pragma unroll
+            for (int t = 0; t < T; ++t) acc[t] += part_s[wave][t][lane];
+        if (NORM && threadIdx.x < RB * 16) {
+            // 1/sqrt(mean square + eps) of the group's rows, the slots
+            // summed in the order of the lane sums above.
+            const float* u = ssq_s[threadIdx.x];
+            const float ss = ((u[0] + u[1]) + (u[2] + u[3])) + ((u[4] + u[5]) + (u[6] + u[7]));
+            inv_s[threadIdx.x] = 1.0f / sqrtf(ss / (float)K + a.eps);
+        }
+        __syncthreads();
+        // Then each tile's four partials to its owner.
+        if (wave < kWaves / 2)
+#pragma unroll
+            for (int t = 0; t < T; ++t) part_s[wave][t][lane] = acc[t];
+        __syncthreads();
+        if (wave >= OW) return;
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+            if (rb % OW != wave) continue;
+#pragma unroll
+            for (int j = 0; j < NB; ++j) {
+                const int t = rb * NB + j;
+                acc[t] = (part_s[0][t][lane] + part_s[1][t][lane]) + (part_s[2][t][lane] + part_s[3][t][lane]);
+            }
         }
     }
 
