@@ -175,8 +175,9 @@ __global__ __launch_bounds__(kWaves * 64) void fast_gemm_kernel(FastGemmArgs a) 
 #pragma unroll
     for (int t = 0; t < T; ++t) acc[t] = f4{0.f, 0.f, 0.f, 0.f};
     const int mine = steps > wave ? (steps - wave + kWaves - 1) / kWaves : 0;  // this wavefront's steps
-    for (int i0 = 0; i0 < mine; i0 += CH) {
-        f4 av[CH][RB], bv[CH][NB], gv[CH];
+    // Steps i0 .. i0+CH-1 of this wavefront: their operands, then their MFMAs
+    // (steps in order, whatever the chunking).
+    auto load = [&](int i0, f4 (&av)[CH][RB], f4 (&bv)[CH][NB], f4 (&gv)[CH]) {
 #pragma unroll
         for (int c = 0; c < CH; ++c) {
             if (i0 + c < mine) {
@@ -189,6 +190,8 @@ __global__ __launch_bounds__(kWaves * 64) void fast_gemm_kernel(FastGemmArgs a) 
                     bv[c][j] = __builtin_nontemporal_load(reinterpret_cast<const f4*>(wb[j] + s * 256));
             }
         }
+    };
+    auto multiply = [&](int i0, const f4 (&av)[CH][RB], const f4 (&bv)[CH][NB], const f4 (&gv)[CH]) {
 #pragma unroll
         for (int c = 0; c < CH; ++c) {
             if (i0 + c < mine) {
@@ -205,6 +208,28 @@ __global__ __launch_bounds__(kWaves * 64) void fast_gemm_kernel(FastGemmArgs a) 
                     }
                 }
             }
+        }
+    };
+    if constexpr (CH <= 2) {
+        // Short chunks (the many-step tiles of the LM head and of prefill):
+        // two operand buffers, the next chunk's loads in flight during this
+        // chunk's MFMAs.
+        f4 av0[CH][RB], bv0[CH][NB], gv0[CH], av1[CH][RB], bv1[CH][NB], gv1[CH];
+        load(0, av0, bv0, gv0);
+        for (int i0 = 0; i0 < mine; i0 += 2 * CH) {
+            if (i0 + CH < mine) load(i0 + CH, av1, bv1, gv1);
+            __builtin_amdgcn_sched_barrier(0);
+            multiply(i0, av0, bv0, gv0);
+            if (i0 + CH >= mine) break;
+            if (i0 + 2 * CH < mine) load(i0 + 2 * CH, av0, bv0, gv0);
+            __builtin_amdgcn_sched_barrier(0);
+            multiply(i0 + CH, av1, bv1, gv1);
+        }
+    } else {
+        for (int i0 = 0; i0 < mine; i0 += CH) {
+            f4 av[CH][RB], bv[CH][NB], gv[CH];
+            load(i0, av, bv, gv);
+            multiply(i0, av, bv, gv);
         }
     }
     if (NORM) {
@@ -441,10 +466,10 @@ template <int EPI, bool NORM, bool GATHER>
 hipError_t launch_sized(hipStream_t s, const FastGemmArgs& a) {
     constexpr int M = EPI == kSwiglu ? 2 : 1;
     if constexpr (EPI == kHead) {
-        if (head_wide(a.columns)) return launch_fast<EPI, NORM, GATHER, 4, 4, 3>(s, a);
+        if (head_wide(a.columns)) return launch_fast<EPI, NORM, GATHER, 4, 4, 2>(s, a);
         return launch_fast<EPI, NORM, GATHER, 1, 1, 6>(s, a);
     } else {
-        if (a.rows > 64 && a.columns % 64 == 0) return launch_fast<EPI, NORM, GATHER, 4, 4 / M, 3>(s, a);
+        if (a.rows > 64 && a.columns % 64 == 0) return launch_fast<EPI, NORM, GATHER, 4, 4 / M, 2>(s, a);
         if constexpr (M == 2) return launch_fast<EPI, NORM, GATHER, 2, 1, 6>(s, a);
         return launch_fast<EPI, NORM, GATHER, 1, 1, 12>(s, a);
     }
@@ -473,7 +498,7 @@ hipError_t launch_fast_gemm(hipStream_t s, Epilogue epilogue, const FastGemmArgs
         if (a.columns % kRopeDim || a.heads * kRopeDim + 2 * a.kv.kv_width != a.columns || !norm ||
             a.kv.block_tokens <= 0 || !a.row_block || !a.row_rope)
             return hipErrorInvalidValue;
-        if (a.rows > 64) return launch_fast<kRope, true, false, 4, 2, 3>(s, a);
+        if (a.rows > 64) return launch_fast<kRope, true, false, 4, 2, 2>(s, a);
         return launch_fast<kRope, true, false, 1, 2, 6>(s, a);
     }
     return hipErrorInvalidValue;
