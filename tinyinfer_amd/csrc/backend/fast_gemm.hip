@@ -85,7 +85,7 @@ __device__ __forceinline__ uint64_t max_key(uint64_t key) {
 }
 
 template <int EPI, bool NORM, bool GATHER, int RB, int CB, int CH>
-__global__ __launch_bounds__(kWaves * 64) void fast_gemm_kernel(FastGemmArgs a) {
+__global__ __launch_bounds__(kWaves * 64, CH == 1 ? 4 : 1) void fast_gemm_kernel(FastGemmArgs a) {
     constexpr int M = EPI == kSwiglu ? 2 : 1;
     constexpr int NB = CB * M;  // B operands per step
     constexpr int T = RB * NB;  // accumulator tiles
@@ -210,7 +210,7 @@ __global__ __launch_bounds__(kWaves * 64) void fast_gemm_kernel(FastGemmArgs a) 
             }
         }
     };
-    if constexpr (CH <= 2) {
+    if constexpr (CH == 2) {
         // Short chunks (the many-step tiles of the LM head and of prefill):
         // two operand buffers, the next chunk's loads in flight during this
         // chunk's MFMAs.
@@ -466,7 +466,7 @@ template <int EPI, bool NORM, bool GATHER>
 hipError_t launch_sized(hipStream_t s, const FastGemmArgs& a) {
     constexpr int M = EPI == kSwiglu ? 2 : 1;
     if constexpr (EPI == kHead) {
-        if (head_wide(a.columns)) return launch_fast<EPI, NORM, GATHER, 4, 4, 2>(s, a);
+        if (head_wide(a.columns)) return launch_fast<EPI, NORM, GATHER, 4, 4, 1>(s, a);
         return launch_fast<EPI, NORM, GATHER, 1, 1, 6>(s, a);
     } else {
         if (a.rows > 64 && a.columns % 64 == 0) return launch_fast<EPI, NORM, GATHER, 4, 4 / M, 2>(s, a);
