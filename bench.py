@@ -432,7 +432,7 @@ def summarise_sq(counter_csv: str, trace_csv: str, out: str, command: str):
     clean = lambda n: n.replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0]
     decode = ("fast_attention_kernel<", "fast_attention_merge_kernel", "fast_gemm_kernel<4, true, false, 1, 2, 6>",
               "fast_gemm_kernel<1, false, false, 1, 1, 12>", "fast_gemm_kernel<2, true, false, 2, 1, 6>",
-              "fast_gemm_kernel<3, true, true, 4, 4, 3>")
+              "fast_gemm_kernel<3, true, true, 4, 4, ")
     pick = lambda n: next((k for k in decode if k in n), None)
     per, meta = defaultdict(dict), {}
     for r in csv.DictReader(open(counter_csv)):
