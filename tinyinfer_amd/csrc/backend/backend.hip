@@ -515,10 +515,13 @@ int mp_hip_upload_tensor(mp_hip* h, int32_t layer, int32_t slot, const float* da
         }
         return hipMemcpyAsync(h->staging, data, bytes, h2d, h->stream);
     };
+    // Fast mode with 64-wide heads: q and k pair-permuted for the RoPE
+    // projection (fast_rope_column).
+    const bool rope = h->fast && c.hidden / c.heads == 64 && (slot == MP_TENSOR_Q || slot == MP_TENSOR_K);
     auto transposed = [&](float* dst, int rows, int cols) -> hipError_t {
         hipError_t r = staged();
         if (r != hipSuccess) return r;
-        return h->fast ? mphip::launch_to_fragments(h->stream, h->staging, dst, cols, rows, true)
+        return h->fast ? mphip::launch_to_fragments(h->stream, h->staging, dst, cols, rows, true, layer >= 0 && rope)
                        : mphip::launch_transpose(h->stream, h->staging, dst, rows, cols, rows);
     };
     if (layer < 0) {
@@ -870,9 +873,11 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
         // Matrix-core projections; RMSNorm folded into the next projection
         // through per-16-column sums of squares of the residual stream.
         const int ssq_stride = h->workspace_rows, parts = hd / 16;
+        int rope_columns = 0;
         auto fast = [&](mphip::Epilogue epi, const float* x, int inner, const float* w, const float* w2, int columns,
                         float* out, const float* norm) {
             mphip::FastGemmArgs a{};
+            a.rope_columns = rope_columns;
             a.x = x;
             a.w = w;
             a.w2 = w2;
@@ -934,7 +939,10 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
                     return mphip::launch_fast_gemm(s, mphip::kRope, a);
                 });
             } else {
+                // q and k come out of the pair-permuted weights in natural order.
+                rope_columns = dim == 64 ? hd + kvw : 0;
                 e = timed(P, [&] { return fast(mphip::kStore, h->x, hd, h->qkv[l], nullptr, qw, h->qkv_out, h->input_norm[l]); });
+                rope_columns = 0;
             }
             if (e == hipSuccess) {
                 if (fast_decode) {

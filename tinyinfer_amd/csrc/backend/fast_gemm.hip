@@ -35,10 +35,11 @@
 // the sum of squares of the updated x over each 16-column block; SwiGLU
 // (gate and up accumulated side by side); LM head (per row and column group
 // of 16*CB columns, the first maximum and a non-finite flag, logits
-// row-major on request); RoPE (the q|k|v projection of a decode step:
-// column blocks j and j+2 of a 64-wide head are computed together, so each
-// split-half pair (d, d+32) is in one lane; q is rotated in place, the
-// rotated k and the v go to the paged pools at the row's position).
+// row-major on request); RoPE (the q|k|v projection of a decode step, over
+// q and k columns stored pair-permuted so that each 16-column block holds
+// whole split-half pairs (d, d+32) in lanes c and c+8; q is rotated in
+// place, the rotated k and the v go to the paged pools at the row's
+// position).
 // RMSNorm on the input (NORM): a[r][k] = x[r][k] * g[k], and the result is
 // scaled by 1/sqrt(sum_k x[r][k]^2 / K + eps), the sum assembled from the
 // producer's per-block partials.
@@ -84,8 +85,17 @@ __device__ __forceinline__ uint64_t max_key(uint64_t key) {
     return k > key ? k : key;
 }
 
+// The q and k columns of the RoPE projection are stored pair-permuted
+// within each 64-wide head (fast_rope_column): column 16b + c of a head is
+// dim rope_dim = 8b + c%8 + 32(c/8), so each 16-column block holds 8 whole
+// split-half pairs (d, d + 32) in lanes c and c + 8; rope_pair is the
+// pair's rotation index d % 32.
+__device__ __forceinline__ int rope_dim(int cb, int lane) { return fast_rope_column(cb * 16 + (lane & 15)) & 63; }
+__device__ __forceinline__ int rope_pair(int cb, int lane) { return 8 * (cb & 3) + (lane & 7); }
+
 template <int EPI, bool NORM, bool GATHER, int RB, int CB, int CH>
 __global__ __launch_bounds__(kWaves * 64, CH == 1 ? 4 : 1) void fast_gemm_kernel(FastGemmArgs a) {
+    static_assert(EPI != kRope || CB == 1, "the RoPE epilogue takes one column block");
     constexpr int M = EPI == kSwiglu ? 2 : 1;
     constexpr int NB = CB * M;  // B operands per step
     constexpr int T = RB * NB;  // accumulator tiles
@@ -109,7 +119,7 @@ __global__ __launch_bounds__(kWaves * 64, CH == 1 ? 4 : 1) void fast_gemm_kernel
     if (cg >= ncg) return;
     int cblock[CB];
 #pragma unroll
-    for (int j = 0; j < CB; ++j) cblock[j] = EPI == kRope ? 4 * (cg >> 1) + (cg & 1) + 2 * j : cg * CB + j;
+    for (int j = 0; j < CB; ++j) cblock[j] = cg * CB + j;
     const int row0 = rg * RB * 16;
     const int K = a.inner, Q = K >> 2, steps = K >> 4;
     // A: row row0 + 16rb + l%16 (gathered), quads 4s + l/16.
@@ -155,19 +165,19 @@ __global__ __launch_bounds__(kWaves * 64, CH == 1 ? 4 : 1) void fast_gemm_kernel
             old[i] = a.out[quad_index(row, cblock[0] * 16 + (lane & 15), a.columns)];
         }
     }
-    // RoPE rows of the owned row block: position, page and rotation
-    // (cos, sin of dim d = 16(cg&1) + l%16 at the row's position).
+    // RoPE rows of the owned row block: position, page and rotation (cos,
+    // sin of rotation index rope_pair() at the row's position; CB == 1).
     int rope_pos[4], rope_block[4];
     float rope_cs[4], rope_sn[4];
     if (EPI == kRope && wave < OW) {
-        const int d = (cg & 1) * 16 + (lane & 15);
+        const int rd = rope_pair(cblock[0], lane);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int row = min(row0 + wave * 16 + 4 * (lane >> 4) + i, a.rows - 1);
             rope_pos[i] = a.meta.row_pos[row];
             rope_block[i] = a.row_block[row];
-            rope_cs[i] = a.row_rope[(size_t)row * kRopeDim + d];
-            rope_sn[i] = a.row_rope[(size_t)row * kRopeDim + kRopeDim / 2 + d];
+            rope_cs[i] = a.row_rope[(size_t)row * kRopeDim + rd];
+            rope_sn[i] = a.row_rope[(size_t)row * kRopeDim + kRopeDim / 2 + rd];
         }
     }
 
@@ -308,45 +318,43 @@ __global__ __launch_bounds__(kWaves * 64, CH == 1 ? 4 : 1) void fast_gemm_kernel
 
     const int N = a.columns;
     if (EPI == kRope) {
-        // acc[2rb] holds dims d = 16(cg&1) + l%16 of head cg>>1, acc[2rb+1]
-        // dims d + 32 (head dim 64, split-half rotation). RB <= 4 here, so
+        // One column block (CB == 1) of the pair-permuted q|k|v columns:
+        // lanes c and c + 8 of a q or k block hold the split-half pair
+        // (d, d + 32) of one head (rope_dim), exchanged by a DPP rotation of
+        // the 16-lane row by 8; v blocks are in natural order. RB <= 4, so
         // wavefront w owns row block w.
         const int rb = wave;
-        const int hcol = (cg >> 1) * kRopeDim;
-        const int d = (cg & 1) * 16 + (lane & 15);
+        const int cb = cblock[0];
+        const int hcol = cb * 16 / kRopeDim * kRopeDim;  // the head's first column
         const int hidden = a.heads * kRopeDim, kvw = a.kv.kv_width;
         const int bt = a.kv.block_tokens;
+        const bool rotate = hcol < hidden + kvw;
+        const int d = rotate ? rope_dim(cb, lane) : (cb * 16) % kRopeDim + (lane & 15);
+        const bool low = (lane & 8) == 0;  // the d < 32 half of a pair
+        float x[4], xp[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int rl = 4 * (lane >> 4) + i;
-            const int row = row0 + rb * 16 + rl;
-            if (row >= a.rows) continue;
-            const float inv = inv_s[rb * 16 + rl];
-            float x0 = 0.0f, x1 = 0.0f;
+            float v = 0.0f;
 #pragma unroll
             for (int r2 = 0; r2 < RB; ++r2)
-                if (r2 == rb) {
-                    x0 = acc[2 * r2][i] * inv;
-                    x1 = acc[2 * r2 + 1][i] * inv;
-                }
+                if (r2 == rb) v = acc[r2][i];
+            x[i] = v * inv_s[rb * 16 + 4 * (lane >> 4) + i];
+            xp[i] = dpp<kDppRowRor8>(x[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = row0 + rb * 16 + 4 * (lane >> 4) + i;
+            if (row >= a.rows) continue;
             const float cs = rope_cs[i], sn = rope_sn[i];
-            const float y0 = x0 * cs - x1 * sn, y1 = x1 * cs + x0 * sn;
+            const float y = !rotate ? x[i] : low ? x[i] * cs - xp[i] * sn : x[i] * cs + xp[i] * sn;
             if (hcol < hidden) {
-                a.out[quad_index(row, hcol + d, N)] = y0;
-                a.out[quad_index(row, hcol + d + kRopeDim / 2, N)] = y1;
+                a.out[quad_index(row, hcol + d, N)] = y;
                 continue;
             }
             const size_t base = kv_page_base(rope_block[i], a.layer, a.kv.layers, bt, kvw);
             const int slot = rope_pos[i] % bt;
-            if (hcol < hidden + kvw) {
-                const int kvh = (hcol - hidden) / kRopeDim;
-                a.kv.keys[base + key_offset(slot, kvh, d, bt, kRopeDim)] = y0;
-                a.kv.keys[base + key_offset(slot, kvh, d + kRopeDim / 2, bt, kRopeDim)] = y1;
-            } else {
-                const int kvh = (hcol - hidden - kvw) / kRopeDim;
-                a.kv.values[base + value_offset(slot, kvh, d, bt, kRopeDim)] = x0;
-                a.kv.values[base + value_offset(slot, kvh, d + kRopeDim / 2, bt, kRopeDim)] = x1;
-            }
+            if (rotate) a.kv.keys[base + key_offset(slot, (hcol - hidden) / kRopeDim, d, bt, kRopeDim)] = y;
+            else a.kv.values[base + value_offset(slot, (hcol - hidden - kvw) / kRopeDim, d, bt, kRopeDim)] = y;
         }
         return;
     }
@@ -409,7 +417,8 @@ __global__ __launch_bounds__(kWaves * 64, CH == 1 ? 4 : 1) void fast_gemm_kernel
                     v[m] = NORM ? s * inv_s[rb * 16 + rl] : s;
                 }
                 if (EPI == kStore) {
-                    if (live) a.out[quad_index(row, col, N)] = v[0];
+                    const int oc = col < a.rope_columns ? fast_rope_column(col) : col;
+                    if (live) a.out[quad_index(row, oc, N)] = v[0];
                 } else if (EPI == kResidual) {
                     float nx = 0.0f;
                     if (live) {
@@ -498,8 +507,8 @@ hipError_t launch_fast_gemm(hipStream_t s, Epilogue epilogue, const FastGemmArgs
         if (a.columns % kRopeDim || a.heads * kRopeDim + 2 * a.kv.kv_width != a.columns || !norm ||
             a.kv.block_tokens <= 0 || !a.row_block || !a.row_rope)
             return hipErrorInvalidValue;
-        if (a.rows > 64) return launch_fast<kRope, true, false, 4, 2, 2>(s, a);
-        return launch_fast<kRope, true, false, 1, 2, 6>(s, a);
+        if (a.rows > 64) return launch_fast<kRope, true, false, 4, 1, 2>(s, a);
+        return launch_fast<kRope, true, false, 1, 1, 12>(s, a);
     }
     return hipErrorInvalidValue;
 }

@@ -70,7 +70,11 @@ hipError_t launch_head_argmax(hipStream_t s, const GemmArgs& args, int32_t* argm
 // Fast arithmetic mode (fast_gemm.hip): the same projections on FP32 matrix
 // cores, in their summation order. x and out in the quad layout (kHead:
 // logits row-major [rows][columns]); w (and w2, the up matrix of kSwiglu) is
-// [columns][inner]. inner and columns multiples of 16.
+// [columns][inner] in the fragment order of layout.h. inner and columns
+// multiples of 16.
+// - rope_columns (kStore): the first rope_columns output columns (q and k
+//   of a q|k|v projection) are stored pair-permuted within each 64-wide head
+//   (fast_rope_column) and are written back in natural order.
 // - norm (kStore, kSwiglu, kHead): RMSNorm of x with weights `norm`; the row
 //   sums of squares come from ssq_in: ssq_parts partial sums per row at
 //   ssq_in[p*ssq_stride + row] (written by the producer of x).
@@ -82,7 +86,8 @@ hipError_t launch_head_argmax(hipStream_t s, const GemmArgs& args, int32_t* argm
 //   is non-null
 //   (groups = columns/fast_head_group_columns(columns)).
 // - kRope (norm required; head dim 64; columns = q|k|v of `heads` query and
-//   kv.kv_width/64 KV heads): split-half RoPE at meta.row_pos with the
+//   kv.kv_width/64 KV heads, q and k columns pair-permuted as for
+//   rope_columns): split-half RoPE at meta.row_pos with the
 //   per-row rotation row_rope[row][64] (cos of dims 0..31, then sin) and
 //   page row_block[row] (launch_embed writes both); rotated q into out (quad
 //   layout), rotated k and v into the pools of `kv` at `layer` and the
@@ -109,7 +114,16 @@ struct FastGemmArgs {
     int layer, heads;
     const int32_t* row_block;
     const float* row_rope;
+    int rope_columns;
 };
+// Source column of stored column n of a q or k matrix whose 64-wide heads are
+// pair-permuted for the fast RoPE projection: within a head, stored column
+// 16b + c holds dim 8b + c%8 + 32(c/8), so each 16-column block carries 8
+// whole split-half pairs (d, d + 32).
+__host__ __device__ inline int fast_rope_column(int n) {
+    const int h = n & ~63, b = (n >> 4) & 3, c = n & 15;
+    return h + 8 * b + (c & 7) + 32 * (c >> 3);
+}
 bool fast_gemm_fits(const FastGemmArgs& args);
 // Columns per LM-head argmax group of the fast head.
 int fast_head_group_columns(int columns);
@@ -171,8 +185,11 @@ hipError_t launch_embed(hipStream_t s, const float* embedding, const int32_t* to
                         int hidden, int32_t* error, const RowRope* rope = nullptr, bool fragments = false);
 // dst = the n_out x k_in matrix W (W[n][k]: output n, input k) in the
 // fragment order of layout.h; src holds it [k_in][n_out] (in_out) or
-// [n_out][k_in]. n_out and k_in are multiples of 16.
-hipError_t launch_to_fragments(hipStream_t s, const float* src, float* dst, int n_out, int k_in, bool in_out);
+// [n_out][k_in]. n_out and k_in are multiples of 16. With rope_heads, the
+// stored output n is the source's fast_rope_column(n) (n_out a multiple of
+// 64).
+hipError_t launch_to_fragments(hipStream_t s, const float* src, float* dst, int n_out, int k_in, bool in_out,
+                               bool rope_heads = false);
 
 // out[r] = (x[r']*scale_r')*w with scale = 1/sqrt(sequential sum of squares/width + eps);
 // r' = row_map[r] when row_map is non-null, else r.

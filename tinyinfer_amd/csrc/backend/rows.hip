@@ -272,16 +272,18 @@ __global__ void table_update_kernel(int32_t* __restrict__ tables, const int2* __
 
 // W[n][k] (n < n_out, k < k_in) to the fragment order of layout.h: float4
 // f of the destination is lane f%64 of fragment f/64 = (n/16) * (k_in/16) +
-// k/16, holding W[16(n/16) + lane%16][16(k/16) + 4(lane/16) .. +3].
+// k/16, holding W[16(n/16) + lane%16][16(k/16) + 4(lane/16) .. +3] (with
+// rope_heads, stored output n holds source output fast_rope_column(n)).
 __global__ void to_fragments_kernel(const float* __restrict__ src, float* __restrict__ dst, int n_out, int k_in,
-                                    bool in_out) {
+                                    bool in_out, bool rope_heads) {
     const size_t total = (size_t)n_out * k_in;
     const int steps = k_in >> 4;
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
         const int c = (int)(i & 3);
         const int lane = (int)((i >> 2) & 63);
         const size_t fragment = i >> 8;
-        const int n = (int)(fragment / steps) * 16 + (lane & 15);
+        const int stored = (int)(fragment / steps) * 16 + (lane & 15);
+        const int n = rope_heads ? fast_rope_column(stored) : stored;
         const int k = (int)(fragment % steps) * 16 + 4 * (lane >> 4) + c;
         dst[i] = in_out ? src[(size_t)k * n_out + n] : src[(size_t)n * k_in + k];
     }
@@ -316,9 +318,10 @@ hipError_t launch_embed(hipStream_t s, const float* embedding, const int32_t* to
     return hipGetLastError();
 }
 
-hipError_t launch_to_fragments(hipStream_t s, const float* src, float* dst, int n_out, int k_in, bool in_out) {
-    if (n_out % 16 || k_in % 16) return hipErrorInvalidValue;
-    to_fragments_kernel<<<4096, 256, 0, s>>>(src, dst, n_out, k_in, in_out);
+hipError_t launch_to_fragments(hipStream_t s, const float* src, float* dst, int n_out, int k_in, bool in_out,
+                               bool rope_heads) {
+    if (n_out % 16 || k_in % 16 || (rope_heads && n_out % 64)) return hipErrorInvalidValue;
+    to_fragments_kernel<<<4096, 256, 0, s>>>(src, dst, n_out, k_in, in_out, rope_heads);
     return hipGetLastError();
 }
 
