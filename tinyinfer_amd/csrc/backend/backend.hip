@@ -693,17 +693,17 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
     const size_t table_pairs = h->pending_tables.size();
     const size_t copies = h->pending_copies.size();
     // Fast-mode decode attention: work items (row, KV head, first token,
-    // tokens) over 128-token splits, and per row (first item, splits per KV
-    // head). The split depends on nothing but the row, so a row's result
-    // does not depend on the rest of the batch.
+    // tokens | split << 16) over each row's splits (fast_attention_split).
+    // The split depends on nothing but the row, so a row's result does not
+    // depend on the rest of the batch.
     const int dim_ = c.hidden / c.heads, group_ = c.heads / c.kv_heads;
     const bool fast_decode = h->fast && decode && h->kv.block_tokens == 16 && dim_ == 64 && group_ <= 4;
-    const int split = mphip::fast_attention_split_tokens();
     size_t fast_items = 0;
     int max_splits = 0;
     if (fast_decode)
         for (int q = 0; q < nseq; ++q) {
-            const int splits = (steps[q].used + 1 + split - 1) / split;
+            const int length = steps[q].used + 1, split = mphip::fast_attention_split(length);
+            const int splits = (length + split - 1) / split;
             fast_items += (size_t)c.kv_heads * splits;
             max_splits = std::max(max_splits, splits);
         }
@@ -762,13 +762,14 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
         // Decode: row q is sequence q's only row.
         size_t f = 0;
         for (int q = 0; q < nseq; ++q) {
-            const int length = steps[q].used + 1, splits = (length + split - 1) / split;
+            const int length = steps[q].used + 1, split = mphip::fast_attention_split(length);
+            const int splits = (length + split - 1) / split;
             for (int kvh = 0; kvh < c.kv_heads; ++kvh)
                 for (int sp = 0; sp < splits; ++sp, ++f) {
                     m_fast[4 * f] = q;
                     m_fast[4 * f + 1] = steps[q].table_slot * c.kv_heads + kvh;
                     m_fast[4 * f + 2] = sp * split;
-                    m_fast[4 * f + 3] = std::min(split, length - sp * split);
+                    m_fast[4 * f + 3] = std::min(split, length - sp * split) | (sp << 16);
                 }
         }
     }

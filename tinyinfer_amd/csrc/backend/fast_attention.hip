@@ -1,7 +1,8 @@
 // Decode attention of the fast arithmetic mode: flash-decoding over the
 // paged pools. The reference computes each (row, head) with an explicit
 // two-pass softmax and sequential sums (llama_runner.cpp:85-93); here the
-// context is cut into page-aligned splits of 128 tokens, each split keeps
+// context is cut into page-aligned splits (fast_attention_split: 128
+// tokens; a row of up to 256 tokens in 8 splits), each split keeps
 // a running maximum, denominator and weighted sum per query head, and the
 // splits are combined at the end (the order of the floating-point sums
 // differs; the result matches the reference within 1e-4 absolute on the
@@ -50,7 +51,6 @@ constexpr int kDim = 64;
 constexpr int kPage = 16;
 constexpr int kMaxGroup = 4;
 constexpr int kSplitPages = 8;
-constexpr int kSplitTokens = kSplitPages * kPage;  // 128
 constexpr int kRing = 3;                           // pages in flight per wavefront
 constexpr int kItemsPerGroup = 4;
 constexpr int kMergeHeld = 16;  // splits whose partial outputs the merge loads up front
@@ -69,7 +69,7 @@ __global__ __launch_bounds__(kItemsPerGroup * 64) void fast_attention_kernel(con
     const int index = blockIdx.x * kItemsPerGroup + wave;
     if (index >= w.items_count) return;
     const int4 item = reinterpret_cast<const int4*>(w.items)[index];
-    const int row = item.x, kvh = item.y % w.kv_heads, t0 = item.z, n = item.w;
+    const int row = item.x, kvh = item.y % w.kv_heads, t0 = item.z, n = item.w & 0xFFFF, sp = item.w >> 16;
     const int32_t* table = kv.tables + (size_t)(item.y / w.kv_heads) * kv.table_stride;
     const int t = lane >> 2, dq = lane & 3;
     const int end = t0 + n;           // tokens t0..end-1 (t0 page-aligned)
@@ -213,7 +213,7 @@ __global__ __launch_bounds__(kItemsPerGroup * 64) void fast_attention_kernel(con
         for (int h = 0; h < G; ++h) out[quad_index(row, (kvh * G + h) * kDim + lane, ldo)] = acc[h] / l[h];
         return;
     }
-    const size_t slot = ((size_t)row * w.kv_heads + kvh) * w.max_splits + t0 / kSplitTokens;
+    const size_t slot = ((size_t)row * w.kv_heads + kvh) * w.max_splits + sp;
 #pragma unroll
     for (int h = 0; h < G; ++h) {
         const size_t at = slot * G + h;
@@ -277,7 +277,8 @@ __global__ __launch_bounds__(256) void fast_attention_merge_kernel(int rows, int
     // The row's position is first needed here, after the loads above are in flight.
     __builtin_amdgcn_sched_barrier(0);
     asm volatile("" : "+v"(pos));
-    const int splits = (pos + kSplitTokens) / kSplitTokens;  // ceil((pos + 1) / split)
+    const int split = fast_attention_split(pos + 1);
+    const int splits = (pos + split) / split;  // ceil((pos + 1) / split)
     combine(0, min(64, splits));
     for (int s0 = 64; s0 < splits; s0 += 64) {
         load(s0);
@@ -296,7 +297,6 @@ void launch_items(hipStream_t s, const float* qkv, int ldq, const RowMeta& meta,
 
 }  // namespace
 
-int fast_attention_split_tokens() { return kSplitTokens; }
 
 hipError_t launch_fast_attention(hipStream_t s, const float* qkv, int ldq, int rows, int heads, int kv_heads,
                                  const RowMeta& meta, const PagedKv& kv, int layer, float* out, int ldo,

@@ -135,13 +135,23 @@ hipError_t launch_fast_ssq(hipStream_t s, const float* x, int rows, int width, f
 // Fast-mode decode attention (fast_attention.hip): every row is one new
 // token (already rotated q, its K/V already in the pools). Flash-decoding
 // split over the context: work item (row, KV head, split of
-// fast_attention_split_tokens() tokens, page-aligned) computes a maximum,
+// fast_attention_split(length) tokens, page-aligned) computes a maximum,
 // denominator and output per query head; a merge kernel combines the splits
-// of every (row, head). Scratch: partial outputs [items][group][dim] and
-// (max, denominator) pairs [items][group][2]. Head dim 64, page 16.
+// of every (row, head). Head dim 64, page 16.
+//
+// Tokens per split of a row of `length` tokens: 8 pages (128 tokens), and
+// for rows of up to 256 tokens the row in (at most) 8 splits of whole
+// pages, so that a short row is still spread over several wavefronts (a
+// small batch of short rows is bound by one wavefront's chain of pages). A
+// function of the row alone: a row's result does not depend on the batch.
+__host__ __device__ inline int fast_attention_split(int length) {
+    const int pages = (length + 15) / 16;
+    return pages <= 16 ? 16 * ((pages + 7) / 8) : 128;
+}
 struct FastAttentionWork {
-    // per work item (int4): row, table slot * kv_heads + KV head, first token, token count;
-    // the items of a row are KV head major, then split order
+    // per work item (int4): row, table slot * kv_heads + KV head, first
+    // token, token count | split index << 16; the items of a row are KV head
+    // major, then split order
     const int32_t* items;
     int items_count;
     // Splits of the longest row; the partial results of (row, KV head,
@@ -158,7 +168,6 @@ struct FastAttentionWork {
     const float* prefetch[kPrefetchRanges];
     uint64_t prefetch_bytes[kPrefetchRanges];
 };
-int fast_attention_split_tokens();
 hipError_t launch_fast_attention(hipStream_t s, const float* qkv, int ldq, int rows, int heads, int kv_heads,
                                  const RowMeta& meta, const PagedKv& kv, int layer, float* out, int ldo,
                                  const FastAttentionWork& work);
