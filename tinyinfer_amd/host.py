@@ -274,6 +274,7 @@ class Engine:
         self.handle = h
         runner.owned = False  # the engine frees it; the handle stays a borrowed view
         self.runner = runner
+        self._poll_buffer = ctypes.create_string_buffer(1 << 16)
 
     def close(self):
         if getattr(self, "handle", None):
@@ -297,11 +298,16 @@ class Engine:
         return bool(progressed.value)
 
     def poll_events(self) -> list[dict]:
+        # One call into a reused buffer; the library keeps the events until
+        # a call whose buffer holds them, so a short buffer is grown and the
+        # call repeated.
         needed = ctypes.c_size_t()
-        _check(self.lib, self.lib.mpx_engine_poll(self.handle, None, 0, ctypes.byref(needed)))
-        buf = ctypes.create_string_buffer(needed.value + 1)
-        _check(self.lib, self.lib.mpx_engine_poll(self.handle, buf, needed.value + 1, ctypes.byref(needed)))
-        return json.loads(buf.value.decode())
+        while True:
+            buf = self._poll_buffer
+            _check(self.lib, self.lib.mpx_engine_poll(self.handle, buf, len(buf), ctypes.byref(needed)))
+            if needed.value < len(buf):
+                return json.loads(buf.value)
+            self._poll_buffer = ctypes.create_string_buffer(2 * (needed.value + 1))
 
     def cancel(self, rid: str):
         _check(self.lib, self.lib.mpx_engine_cancel(self.handle, _b(rid)))
