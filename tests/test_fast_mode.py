@@ -29,8 +29,16 @@ def margin(v):
     return float(top[1] - top[0])
 
 
-def test_fast_prefill_and_decode_track_the_oracle(torch_cuda):
-    cfg = smollm_config(layers=2, context=1024)
+NARROW = dict(layers=2, hidden=128, intermediate=192, heads=2, kv_heads=1, vocabulary=256, context=1024, eos=0,
+              rms_epsilon=1e-5, rope_theta=10000.0, tied=0)
+
+
+@pytest.mark.parametrize("shape", ["smollm", "narrow_untied"])
+def test_fast_prefill_and_decode_track_the_oracle(torch_cuda, shape):
+    """smollm: the SmolLM2 shape (tied head, 3 query heads per KV head);
+    narrow_untied: hidden 128, 2 query heads on 1 KV head, an untied LM head
+    (uploaded [hidden][vocab]), 192-wide SwiGLU."""
+    cfg = smollm_config(layers=2, context=1024) if shape == "smollm" else dict(NARROW)
     model = OracleModel(cfg, seed=41)
     bt, max_blocks = 16, 192
     backend = HipBackend(cfg, block_tokens=bt, max_blocks=max_blocks, max_sequences=8, arithmetic=ARITHMETIC_FAST)
@@ -57,7 +65,8 @@ def test_fast_prefill_and_decode_track_the_oracle(torch_cuda):
             worst = max(worst, err)
             assert err <= 1e-3, f"step {step} row {i}: relative error {err:.3e}"
             assert am[i] == int(np.argmax(got[i]))
-            assert am[i] == int(np.argmax(want[i])), \
+            # A near-tie may go either way under another summation order.
+            assert am[i] == int(np.argmax(want[i])) or margin(want[i]) < 1e-5, \
                 f"step {step} row {i}: token differs (oracle top-2 margin {margin(want[i]):.3e})"
             used[i] += len(chunks[i])
         # Teacher-forced with the oracle's tokens: both sides extend the same history.
