@@ -11,7 +11,10 @@ every request decodes one token):
 - config2: 1 request, 128-token prompt, 128 greedy tokens;
 - config4: a 1000-token prefix published once, then 32 requests of prefix +
   64 unique tokens with the prefix cache on (copy-on-write of the shared
-  8-token tail), 64 greedy tokens each.
+  8-token tail), 64 greedy tokens each;
+- config5a: 8 requests with 16384-token prompts (chunk 512), 256 greedy
+  tokens each;
+- config5b: 256 requests with 1024-token prompts, 64 greedy tokens each.
 Weights are synthetic N(0, 0.02) (RMSNorm weights 1.0), seeded. The runner
 computes in the fast arithmetic by default (FP32 matrix cores, flash-decoding
 attention; logits within 1e-3 of the reference, greedy tokens checked
@@ -68,8 +71,10 @@ METRICS = {
     "config3": "decode tok/s (B=64, SmolLM2-135M-shape FP32); paged-attn HBM GB/s % peak",
     "config2": "decode tok/s (B=1, SmolLM2-135M-shape FP32); projections HBM GB/s % peak",
     "config4": "decode tok/s (32 prefix-sharing requests with COW, SmolLM2-135M-shape FP32); paged-attn HBM GB/s % peak",
+    "config5a": "decode tok/s (B=8, 16384-token prompts, SmolLM2-135M-shape FP32); paged-attn HBM GB/s % peak",
+    "config5b": "decode tok/s (B=256, 1024-token contexts, SmolLM2-135M-shape FP32); paged-attn HBM GB/s % peak",
 }
-DEFAULT_STEPS = {"config3": (96, 8), "config2": (96, 8), "config4": (48, 8)}
+DEFAULT_STEPS = {"config3": (96, 8), "config2": (96, 8), "config4": (48, 8), "config5a": (64, 8), "config5b": (40, 6)}
 HBM_PEAK_GBS = 8000.0
 FP32_MATRIX_PEAK_TFLOPS = 157.3
 PROBE_BYTES = 128 << 20  # --traffic-probe: one copy of 128 MiB (read and written)

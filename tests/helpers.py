@@ -85,3 +85,39 @@ def weights_with(tensors: dict, config: dict, library=None):
     for name, data in tensors.items():
         w.set_tensor(name, data)
     return w
+
+
+def device_key_order(pool: np.ndarray, blocks: int, layers: int, kv_heads: int) -> np.ndarray:
+    """A K pool of 16-token pages and 64-dim heads from the reference order
+    (block, layer, slot, kv head, d) to the device order: per (block,
+    layer), kv head major, then [d/4][slot][4]."""
+    p = pool.reshape(blocks, layers, 16, kv_heads, 16, 4)  # slot, head, d/4, d%4
+    return np.ascontiguousarray(p.transpose(0, 1, 3, 4, 2, 5)).reshape(-1)
+
+
+def device_value_order(pool: np.ndarray, blocks: int, layers: int, kv_heads: int) -> np.ndarray:
+    """The V pool likewise: per (block, layer), kv head major, then
+    [slot/4][d][4]."""
+    p = pool.reshape(blocks, layers, 4, 4, kv_heads, 64)  # slot/4, slot%4, head, d
+    return np.ascontiguousarray(p.transpose(0, 1, 4, 2, 5, 3)).reshape(-1)
+
+
+def write_pools(backend: HipBackend, keys: np.ndarray, values: np.ndarray):
+    """Host pools in the reference order into a context's device pools
+    (16-token pages, 64-dim heads)."""
+    import ctypes
+    c = backend.config
+    layers, kv_heads = c["layers"], c["kv_heads"]
+    assert c["hidden"] // c["heads"] == 64 and backend.block_tokens == 16
+    k_ptr, v_ptr, n = backend.kv_pools()
+    page = layers * 16 * kv_heads * 64
+    assert keys.size == n and values.size == n and n % page == 0
+    hip = ctypes.CDLL("libamdhip64.so.7")  # the HIP runtime this process has loaded
+    hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    hip.hipMemcpy.restype = ctypes.c_int
+    backend.sync()
+    for ptr, data in ((k_ptr, device_key_order(keys, n // page, layers, kv_heads)),
+                      (v_ptr, device_value_order(values, n // page, layers, kv_heads))):
+        data = np.ascontiguousarray(data, dtype=np.float32)
+        assert data.size == n
+        assert hip.hipMemcpy(ptr, data.ctypes.data, data.nbytes, 1) == 0  # host to device

@@ -15,7 +15,7 @@ import pytest
 from oracle import Oracle, OracleModel
 from tinyinfer_amd.backend import ARITHMETIC_FAST, HipBackend
 
-from .helpers import pool_elements, smollm_config, upload_model
+from .helpers import pool_elements, smollm_config, upload_model, write_pools
 
 pytestmark = pytest.mark.gpu
 
@@ -106,3 +106,69 @@ def test_fast_rows_do_not_depend_on_the_batch(torch_cuda):
         backend.close()
     for key, v in results["together"].items():
         assert np.array_equal(v.view(np.uint32), results["apart"][key].view(np.uint32)), key
+
+
+
+def attention_probe_model(context: int, seed: int) -> OracleModel:
+    """One layer whose logits follow the attention output: o_proj the
+    identity, the MLP zero, an embedding 1e-3 the attention's scale and an
+    untied N(0, 1) head, so a logit's relative error is about the attention
+    output's (hidden 192: 3 query heads on 1 KV head of 64 dims)."""
+    o = Oracle()
+    h, kv, inter, vocab = 192, 64, 64, 256
+    cfg = dict(layers=1, hidden=h, intermediate=inter, heads=3, kv_heads=1, vocabulary=vocab, context=context,
+               eos=0, rms_epsilon=1e-5, rope_theta=100000.0, tied=0)
+    normal = lambda shape, std, stream: o.fill_normal(int(np.prod(shape)), seed, stream, std).reshape(shape)
+    layer = dict(input_norm=np.ones(h, np.float32), q=normal((h, h), 0.1, 1), k=normal((h, kv), 0.1, 2),
+                 v=normal((h, kv), 0.1, 3), o=np.eye(h, dtype=np.float32), post_norm=np.ones(h, np.float32),
+                 gate=np.zeros((h, inter), np.float32), up=np.zeros((h, inter), np.float32),
+                 down=np.zeros((inter, h), np.float32))
+    tensors = dict(layers=[layer], embedding=normal((vocab, h), 1e-3, 4), final_norm=np.ones(h, np.float32),
+                   lm_head=normal((h, vocab), 1.0, 5))
+    return OracleModel(cfg, tensors=tensors)
+
+
+@pytest.mark.parametrize("key_scale", [0.5, 6.0])
+def test_fast_long_rows_merge_many_splits(torch_cuda, key_scale):
+    """Decode rows whose contexts are cut into 1 to 129 splits (16,401 tokens:
+    three rounds of the merge's loads; 8,251: two; 1,901; 131 and 33 and 17
+    tokens in 32- and 16-token splits, where some of the merge's four lane
+    groups hold no split; 10: one split, written directly), over pools of
+    seeded keys and values: key_scale 0.5 spreads the softmax over the whole
+    context, 6.0 makes it peak at a few tokens and raises the running
+    maxima inside splits. One decode step against the oracle on the same
+    pools, logits within 1e-3 relative."""
+    used = [16400, 8250, 1900, 130, 32, 16, 9]
+    context = 16640
+    model = attention_probe_model(context, seed=47)
+    cfg = model.config
+    bt = 16
+    pages = [(u + 1 + bt - 1) // bt for u in used]
+    max_blocks = sum(pages) + 24
+    o = Oracle()
+    perm = o.permutation(max_blocks, 47, 9400)
+    tables, at = [], 0
+    for p in pages:
+        tables.append(perm[at:at + p].copy())
+        at += p
+    n = pool_elements(cfg, bt, max_blocks)
+    keys = o.fill_normal(n, 47, 9401, key_scale)
+    values = o.fill_normal(n, 47, 9402, 1.0)
+    tokens = [int(t) for t in o.fill_tokens(len(used), 47, 9403, cfg["vocabulary"])]
+    backend = HipBackend(cfg, block_tokens=bt, max_blocks=max_blocks, max_sequences=len(used),
+                         arithmetic=ARITHMETIC_FAST)
+    upload_model(backend, model)
+    for i, t in enumerate(tables):
+        backend.table_write(i, 0, t)
+    write_pools(backend, keys, values)
+    am, got = backend.forward([(i, used[i], 1) for i in range(len(used))], tokens)
+    worst = 0.0
+    for i in range(len(used)):
+        want = model.append(keys, values, bt, tables[i], used[i], [tokens[i]])
+        assert np.all(np.isfinite(got[i]))
+        err = rel_inf(got[i], want)
+        worst = max(worst, err)
+        assert err <= 1e-3, f"row {i} ({used[i] + 1} tokens): relative error {err:.3e}"
+        assert am[i] == int(np.argmax(got[i]))
+    backend.close()
+    print(f"max relative logit error {worst:.3e}")

@@ -30,7 +30,7 @@
 // Loads past the split's last page re-read that page (a cache hit) so that
 // every load is unconditional and the waits stay exact. A row whose
 // context is one split writes its output directly; otherwise every split
-// writes its partial and a merge kernel combines them in split order.
+// writes its partial and a merge kernel combines them.
 // (Combining in the last split to finish costs each split a store
 // completion and an atomic round trip at its end, more than the extra
 // launch; with a device-scope release fence it would also write back the
@@ -53,7 +53,7 @@ constexpr int kMaxGroup = 4;
 constexpr int kSplitPages = 8;
 constexpr int kRing = 3;                           // pages in flight per wavefront
 constexpr int kItemsPerGroup = 4;
-constexpr int kMergeHeld = 16;  // splits whose partial outputs the merge loads up front
+constexpr int kMergeHeld = 16;  // splits per lane group whose partials the merge loads in one round
 constexpr float kScale = 0.125f;  // 1/sqrt(64)
 constexpr float kRescale = 16.0f;  // probabilities stay below e^16 before a rescale
 
@@ -226,12 +226,15 @@ __global__ __launch_bounds__(kItemsPerGroup * 64) void fast_attention_kernel(con
 }
 
 // out[row][h*64 + d] for rows of more than one split: the splits of
-// (row, h/G) combined in split order. One wavefront per (row, head): lane
-// sp holds split sp's (max, denominator) and weight exp(m_sp - max); lane d
-// sums its dimension over the splits. The partials sit at a fixed stride
-// per (row, KV head), so the first 64 (max, denominator) pairs and the
-// first kMergeHeld partial outputs are loaded together with the row's
-// position, in one round.
+// (row, h/G) combined. One wavefront per (row, head), as four groups of 16
+// lanes: lane 16g + c holds dims 4c..4c+3, and group g takes splits g,
+// g+4, g+8, ... with its own running maximum, denominator and weighted sum,
+// kMergeHeld splits' partials loaded per round (a row of up to 64 splits
+// takes one round of loads, a 16k-token row of 128 splits two). The four
+// groups are then rescaled to the common maximum and summed as
+// (g0 + g1) + (g2 + g3). The order depends on nothing but the row's split
+// count. The partials sit at a fixed stride per (row, KV head), so the
+// first round is issued together with the load of the row's position.
 __global__ __launch_bounds__(256) void fast_attention_merge_kernel(int rows, int heads, int kv_heads, RowMeta meta,
                                                                    FastAttentionWork w, float* __restrict__ out,
                                                                    int ldo) {
@@ -240,52 +243,69 @@ __global__ __launch_bounds__(256) void fast_attention_merge_kernel(int rows, int
     if (pair >= rows * heads) return;
     const int row = pair / heads, h = pair % heads;
     const int G = heads / kv_heads, kvh = h / G, hg = h % G;
-    const int S = w.max_splits;
-    const size_t slot0 = ((size_t)row * kv_heads + kvh) * S;  // split 0 of (row, kvh)
+    const int grp = lane >> 4, c = lane & 15;
+    const size_t slot0 = ((size_t)row * kv_heads + kvh) * w.max_splits;  // split 0 of (row, kvh)
     auto at = [&](int sp) { return (slot0 + sp) * G + hg; };
     int pos = meta.row_pos[row];
-    float num = 0.0f, den = 0.0f, cm = 0.0f;
-    // Splits s0.. s0+63 (loaded up to the longest row's splits, in bounds),
-    // used up to this row's.
-    float mv, lv, ov[kMergeHeld];
-    auto load = [&](int s0) {
-        const int loaded = min(64, S - s0);
-        mv = w.partial_ml[at(s0 + min(lane, loaded - 1)) * 2];
-        lv = w.partial_ml[at(s0 + min(lane, loaded - 1)) * 2 + 1];
+    float gm = -__builtin_inff(), gl = 0.0f;
+    f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    float mv[kMergeHeld], lv[kMergeHeld];
+    f4 ov[kMergeHeld];
+    // Round r: this group's splits grp + 4(r*kMergeHeld + j), clamped to the
+    // last split that may hold data (loads past the row's splits are not used).
+    auto load = [&](int r, int last) {
 #pragma unroll
-        for (int j = 0; j < kMergeHeld; ++j) ov[j] = w.partial_out[at(s0 + min(j, loaded - 1)) * kDim + lane];
+        for (int j = 0; j < kMergeHeld; ++j) {
+            const int sp = min(grp + 4 * (r * kMergeHeld + j), last);
+            mv[j] = w.partial_ml[at(sp) * 2];
+            lv[j] = w.partial_ml[at(sp) * 2 + 1];
+            ov[j] = reinterpret_cast<const f4*>(w.partial_out + at(sp) * kDim)[c];
+        }
     };
-    auto combine = [&](int s0, int count) {
-        const bool mine = lane < count;
-        float hm = mine ? mv : -__builtin_inff();
-        hm = fmaxf(hm, dpp<kDppQuadXor1>(hm));
-        hm = fmaxf(hm, dpp<kDppQuadXor2>(hm));
-        hm = rows_max(row_quads_max(hm));
-        // A later chunk of 64 splits rescales what the earlier ones summed.
-        const float m_new = s0 == 0 ? hm : fmaxf(cm, hm);
-        const float keep = s0 == 0 ? 0.0f : __expf(cm - m_new);
-        const float f = mine ? __expf(mv - m_new) : 0.0f;
-        den = den * keep + rows_sum(row_sum(lv * f));
-        num *= keep;
+    auto combine = [&](int r, int splits) {
+        float rm = gm;
 #pragma unroll
         for (int j = 0; j < kMergeHeld; ++j)
-            if (j < count) num += ov[j] * lane_value(f, j);
-        for (int j = kMergeHeld; j < count; ++j) num += w.partial_out[at(s0 + j) * kDim + lane] * lane_value(f, j);
-        cm = m_new;
+            if (grp + 4 * (r * kMergeHeld + j) < splits) rm = fmaxf(rm, mv[j]);
+        // 0 when the group's first splits arrive, 1 while it has none (its sums are 0).
+        const float keep = gm == rm ? 1.0f : __expf(gm - rm);
+        gl *= keep;
+        acc *= keep;
+#pragma unroll
+        for (int j = 0; j < kMergeHeld; ++j) {
+            const bool valid = grp + 4 * (r * kMergeHeld + j) < splits;
+            const float f = valid ? __expf(mv[j] - rm) : 0.0f;
+            gl = valid ? gl + lv[j] * f : gl;
+            acc = valid ? acc + ov[j] * f : acc;
+        }
+        gm = rm;
     };
-    load(0);
+    load(0, w.max_splits - 1);
     // The row's position is first needed here, after the loads above are in flight.
     __builtin_amdgcn_sched_barrier(0);
     asm volatile("" : "+v"(pos));
     const int split = fast_attention_split(pos + 1);
     const int splits = (pos + split) / split;  // ceil((pos + 1) / split)
-    combine(0, min(64, splits));
-    for (int s0 = 64; s0 < splits; s0 += 64) {
-        load(s0);
-        combine(s0, min(64, splits - s0));
+    if (splits == 1) return;  // written by the split kernel
+    combine(0, splits);
+    for (int r = 1; 4 * r * kMergeHeld < splits; ++r) {
+        load(r, splits - 1);
+        combine(r, splits);
     }
-    // A row of one split was written by the split kernel.
-    if (splits > 1) out[quad_index(row, h * kDim + lane, ldo)] = num / den;
+    // Groups to the common maximum (group 0 holds split 0, so it is finite).
+    float m = fmaxf(gm, __shfl_xor(gm, 16));
+    m = fmaxf(m, __shfl_xor(m, 32));
+    const float f = __expf(gm - m);
+    float den = gl * f;
+    f4 num = acc * f;
+    den += __shfl_xor(den, 16);
+    den += __shfl_xor(den, 32);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        num[i] += __shfl_xor(num[i], 16);
+        num[i] += __shfl_xor(num[i], 32);
+    }
+    if (grp == 0) *reinterpret_cast<f4*>(out + quad_index(row, h * kDim + 4 * c, ldo)) = num / den;
 }
 
 template <int G>

@@ -466,10 +466,15 @@ hipError_t launch_fast(hipStream_t s, const FastGemmArgs& a) {
 
 // Tile shape by size. At decode sizes (one row tile) the tiles are small,
 // for many work-groups (SwiGLU takes two row blocks: its two weight
-// matrices make its column blocks the heaviest); the LM head and any
-// projection of more than one row tile take 64-row x 64-column tiles, which
-// read each weight and each activation a quarter as often.
+// matrices make its column blocks the heaviest). The LM head takes
+// 64-row x 64-column tiles, and so does a projection of more than one row
+// tile when they still give every CU a work-group: they read each weight and
+// each activation a quarter as often. Between the two (a few hundred rows
+// over a 576-column projection: 36 such tiles) the largest of 64 x 16,
+// 32 x 16 and 16 x 16 that gives every CU a work-group.
+constexpr int kCus = 256;
 bool head_wide(int columns) { return columns % 64 == 0; }
+int tiles(const FastGemmArgs& a, int rb, int cb) { return ((a.rows + 15) / 16 + rb - 1) / rb * (a.columns / 16 / cb); }
 
 template <int EPI, bool NORM, bool GATHER>
 hipError_t launch_sized(hipStream_t s, const FastGemmArgs& a) {
@@ -478,7 +483,12 @@ hipError_t launch_sized(hipStream_t s, const FastGemmArgs& a) {
         if (head_wide(a.columns)) return launch_fast<EPI, NORM, GATHER, 4, 4, 1>(s, a);
         return launch_fast<EPI, NORM, GATHER, 1, 1, 6>(s, a);
     } else {
-        if (a.rows > 64 && a.columns % 64 == 0) return launch_fast<EPI, NORM, GATHER, 4, 4 / M, 2>(s, a);
+        if (a.rows > 64) {
+            if (a.columns % 64 == 0 && tiles(a, 4, 4 / M) >= kCus)
+                return launch_fast<EPI, NORM, GATHER, 4, 4 / M, 2>(s, a);
+            if (tiles(a, 4, 1) >= kCus) return launch_fast<EPI, NORM, GATHER, 4, 1, 2>(s, a);
+            if (tiles(a, 2, 1) >= kCus) return launch_fast<EPI, NORM, GATHER, 2, 1, 6>(s, a);
+        }
         if constexpr (M == 2) return launch_fast<EPI, NORM, GATHER, 2, 1, 6>(s, a);
         return launch_fast<EPI, NORM, GATHER, 1, 1, 12>(s, a);
     }
@@ -507,7 +517,8 @@ hipError_t launch_fast_gemm(hipStream_t s, Epilogue epilogue, const FastGemmArgs
         if (a.columns % kRopeDim || a.heads * kRopeDim + 2 * a.kv.kv_width != a.columns || !norm ||
             a.kv.block_tokens <= 0 || !a.row_block || !a.row_rope)
             return hipErrorInvalidValue;
-        if (a.rows > 64) return launch_fast<kRope, true, false, 4, 1, 2>(s, a);
+        if (a.rows > 64 && tiles(a, 4, 1) >= kCus) return launch_fast<kRope, true, false, 4, 1, 2>(s, a);
+        if (a.rows > 64 && tiles(a, 2, 1) >= kCus) return launch_fast<kRope, true, false, 2, 1, 6>(s, a);
         return launch_fast<kRope, true, false, 1, 1, 12>(s, a);
     }
     return hipErrorInvalidValue;
