@@ -249,14 +249,16 @@ __global__ __launch_bounds__(256) void fast_attention_merge_kernel(int rows, int
     int pos = meta.row_pos[row];
     float gm = -__builtin_inff(), gl = 0.0f;
     f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    float mv[kMergeHeld], lv[kMergeHeld];
-    f4 ov[kMergeHeld];
-    // Round r: this group's splits grp + 4(r*kMergeHeld + j), clamped to the
-    // last split that may hold data (loads past the row's splits are not used).
-    auto load = [&](int r, int last) {
+    float mv[kMergeHeld] = {}, lv[kMergeHeld] = {};
+    f4 ov[kMergeHeld] = {};
+    // Round r: this group's splits grp + 4(r*kMergeHeld + j) for the j whose
+    // split of group 0 is below `count` (a wave-uniform bound), clamped to
+    // split count - 1 (loads past the row's splits are not used).
+    auto load = [&](int r, int count) {
 #pragma unroll
         for (int j = 0; j < kMergeHeld; ++j) {
-            const int sp = min(grp + 4 * (r * kMergeHeld + j), last);
+            if (4 * (r * kMergeHeld + j) >= count) break;
+            const int sp = min(grp + 4 * (r * kMergeHeld + j), count - 1);
             mv[j] = w.partial_ml[at(sp) * 2];
             lv[j] = w.partial_ml[at(sp) * 2 + 1];
             ov[j] = reinterpret_cast<const f4*>(w.partial_out + at(sp) * kDim)[c];
@@ -280,7 +282,7 @@ __global__ __launch_bounds__(256) void fast_attention_merge_kernel(int rows, int
         }
         gm = rm;
     };
-    load(0, w.max_splits - 1);
+    load(0, w.max_splits);  // bounded by the batch's longest row until the row's own count is known
     // The row's position is first needed here, after the loads above are in flight.
     __builtin_amdgcn_sched_barrier(0);
     asm volatile("" : "+v"(pos));
@@ -289,7 +291,7 @@ __global__ __launch_bounds__(256) void fast_attention_merge_kernel(int rows, int
     if (splits == 1) return;  // written by the split kernel
     combine(0, splits);
     for (int r = 1; 4 * r * kMergeHeld < splits; ++r) {
-        load(r, splits - 1);
+        load(r, splits);
         combine(r, splits);
     }
     // Groups to the common maximum (group 0 holds split 0, so it is finite).
