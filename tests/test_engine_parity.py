@@ -122,3 +122,35 @@ def test_hip_engine_matches_reference_engine(torch_cuda, batching, kind):
         assert g == r, f"step {r[0]} differs:\nHIP       {g}\nreference {r}"
     assert len(got) == len(want)
     assert costs["cow_pages"] == want_costs["cow_pages"] and costs["cow_bytes"] == want_costs["cow_bytes"]
+
+
+def test_undelivered_events_stay_with_their_engine():
+    """CPU: events that did not fit the caller's buffer wait in their own
+    engine; polling another engine in between neither returns nor drops
+    them (two engines in one process, the reference CpuRunner)."""
+    import ctypes
+
+    ref = reference_library()
+    if ref is None:
+        pytest.skip("oracle/_ref not built")
+    cfg = dict(smollm_config(layers=1, context=128))
+    engines = []
+    for rid in ("a", "b"):
+        w = Weights.synthetic(cfg, seed=SEED, stddev=0.02, library=ref)
+        runner = Runner(w, context=128, block_tokens=16, max_blocks=16)
+        engine = Engine(runner, max_batch_size=1, token_budget=32, prefill_chunk=32, context=128)
+        engine.submit(rid, [1, 2, 3, 4], max_new_tokens=1, eos_token_id=None)
+        engine.step()
+        engines.append((engine, runner, w))
+    a, b = engines[0][0], engines[1][0]
+    needed = ctypes.c_size_t()
+    tiny = ctypes.create_string_buffer(4)
+    assert a.lib.mpx_engine_poll(a.handle, tiny, len(tiny), ctypes.byref(needed)) == 0
+    assert needed.value >= len(tiny)  # a's events did not fit: still pending in a
+    got_b = b.poll_events()
+    assert [e["id"] for e in got_b] == ["b"] and got_b[0]["finish"] is not None
+    got_a = a.poll_events()
+    assert [e["id"] for e in got_a] == ["a"] and got_a[0]["token"] == got_b[0]["token"]
+    assert a.poll_events() == [] and b.poll_events() == []
+    for engine, _, _ in engines:
+        engine.shutdown()

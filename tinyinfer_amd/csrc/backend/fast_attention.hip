@@ -12,9 +12,10 @@
 // One wavefront per work item (row, KV head, split: the item carries the
 // row's table slot beside the KV head), four items per work-group; the
 // wavefront serves the G query heads of the KV head, so each K and V byte
-// is read once. It walks the split's (up to 8) pages with three pages in
-// flight in a ring of registers: the loads of page k+3 are issued as soon
-// as page k has been used. Per page (16 tokens of one layer and KV head,
+// is read once. It walks the split's (up to 8) pages with two pages in
+// flight in a ring of registers: the loads of page k+2 are issued as soon
+// as page k has been used (with 2,000-3,000 wavefronts in flight a third
+// page only deepens the queues at HBM). Per page (16 tokens of one layer and KV head,
 // 4 KB of K then 4 KB of V, device page order of layout.h):
 //  - scores: lane = (token t = lane/4, quarter dq = lane%4 of the 64 dims);
 //    a lane reads 4 float4 of K (dims 16dq..16dq+15 of token t, the 16 lanes
@@ -51,7 +52,7 @@ constexpr int kDim = 64;
 constexpr int kPage = 16;
 constexpr int kMaxGroup = 4;
 constexpr int kSplitPages = 8;
-constexpr int kRing = 3;                           // pages in flight per wavefront
+constexpr int kRing = 2;                           // pages in flight per wavefront
 constexpr int kItemsPerGroup = 4;
 constexpr int kMergeHeld = 16;  // splits per lane group whose partials the merge loads in one round
 constexpr float kScale = 0.125f;  // 1/sqrt(64)

@@ -56,6 +56,9 @@ struct Runner {
 struct EngineBox {
     std::unique_ptr<Engine> engine;
     Runner* view;
+    // Events taken from the engine but not yet delivered (the caller's
+    // buffer was too short); the next poll of this engine returns them first.
+    std::vector<GenerationEvent> pending;
     ~EngineBox() { delete view; }
 };
 
@@ -321,17 +324,15 @@ int mpx_engine_step(void* engine, int32_t* progressed) {
     });
 }
 
-namespace {
-thread_local std::vector<GenerationEvent> g_pending;
-}
-
 int mpx_engine_poll(void* engine, char* buffer, size_t capacity, size_t* needed) {
     return guarded([&] {
-        auto fresh = static_cast<EngineBox*>(engine)->engine->poll_events();
-        g_pending.insert(g_pending.end(), fresh.begin(), fresh.end());
+        EngineBox& box = *static_cast<EngineBox*>(engine);
+        std::vector<GenerationEvent>& pending = box.pending;
+        auto fresh = box.engine->poll_events();
+        pending.insert(pending.end(), fresh.begin(), fresh.end());
         std::string json = "[";
-        for (std::size_t i = 0; i < g_pending.size(); ++i) {
-            const GenerationEvent& e = g_pending[i];
+        for (std::size_t i = 0; i < pending.size(); ++i) {
+            const GenerationEvent& e = pending[i];
             if (i) json += ',';
             json += "{\"id\":";
             json_string(json, e.request_id);
@@ -348,7 +349,7 @@ int mpx_engine_poll(void* engine, char* buffer, size_t capacity, size_t* needed)
         if (needed) *needed = json.size();
         if (buffer && json.size() < capacity) {
             std::memcpy(buffer, json.c_str(), json.size() + 1);
-            g_pending.clear();
+            pending.clear();
         }
     });
 }
