@@ -331,19 +331,23 @@ def summarise_counters(fetch_csv: str, write_csv: str, bench_json: str, out: str
     # The decode kernels (prefill runs other instantiations).
     att_kernels = (("fast_attention_kernel<", "fast_attention_merge_kernel") if fast else
                    ("attn_scores_kernel<16, 64, true>", "attn_decode_kernel<"))
-    proj_kernels = (("fast_gemm_kernel<4, true, false, 1, 2, 6>", "fast_gemm_kernel<1, false, false, 1, 1, 12>",
+    proj_kernels = (("fast_gemm_kernel<4, true, false, 1, 1, 12>", "fast_gemm_kernel<1, false, false, 1, 1, 12>",
                      "fast_gemm_kernel<2, true, false, 2, 1, 6>") if fast else ("gemm_column",))
 
     def read(path):
-        per = defaultdict(list)
+        per = defaultdict(list)  # name -> [(grid, KiB)] in dispatch order
         probe = []
-        for r in csv.DictReader(open(path)):
+        for r in sorted(csv.DictReader(open(path)), key=lambda r: int(r["Dispatch_Id"])):
             name = r["Kernel_Name"].replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0]
             kib = float(r["Counter_Value"])
             if name.startswith("__amd_rocclr_copyBuffer") and kib * 1024 > PROBE_BYTES / 4:
                 probe.append(kib)
-            per[name].append(kib)
-        return per, probe
+            per[name].append((int(r["Grid_Size"]), kib))
+        # The decode launches: a projection instantiation that the prefill's
+        # short chunks also run counts only at the grid of its last launch
+        # (the timed decode steps run last).
+        return {k: [kib for g, kib in v if g == v[-1][0] or not any(p in k for p in proj_kernels)]
+                for k, v in per.items()}, probe
 
     result = {"workload": line["config"]["workload"], "seed": line["config"]["seed"],
               "arithmetic": line["config"].get("arithmetic"), "mean_context": line["config"]["mean_context"],
@@ -435,17 +439,18 @@ def summarise_sq(counter_csv: str, trace_csv: str, out: str, command: str):
     counter run serialises dispatches, so its own cycle counts include the
     profiler's gaps) at the 2.4 GHz peak engine clock."""
     clean = lambda n: n.replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0]
-    decode = ("fast_attention_kernel<", "fast_attention_merge_kernel", "fast_gemm_kernel<4, true, false, 1, 2, 6>",
+    decode = ("fast_attention_kernel<", "fast_attention_merge_kernel", "fast_gemm_kernel<4, true, false, 1, 1, 12>",
               "fast_gemm_kernel<1, false, false, 1, 1, 12>", "fast_gemm_kernel<2, true, false, 2, 1, 6>",
               "fast_gemm_kernel<3, true, true, 4, 4, ")
+    # Grid (threads) of the B=64 decode launches of instantiations that the
+    # prefill's last short chunk also runs, on other shapes.
+    decode_grid = {"fast_gemm_kernel<4, true, false, 1, 1, 12>": 131072,
+                   "fast_gemm_kernel<1, false, false, 1, 1, 12>": 81920}
     pick = lambda n: next((k for k in decode if k in n), None)
     per, meta = defaultdict(dict), {}
     for r in csv.DictReader(open(counter_csv)):
         k = pick(clean(r["Kernel_Name"]))
-        if k is None:
-            continue
-        # prefill runs the same residual instantiation on other shapes
-        if "<1, false, false, 1, 1, 12>" in k and int(r["Grid_Size"]) != 81920:
+        if k is None or int(r["Grid_Size"]) != decode_grid.get(k, int(r["Grid_Size"])):
             continue
         d = int(r["Dispatch_Id"])
         per[d][r["Counter_Name"]] = float(r["Counter_Value"])
@@ -453,7 +458,7 @@ def summarise_sq(counter_csv: str, trace_csv: str, out: str, command: str):
     durations = defaultdict(list)
     for r in csv.DictReader(open(trace_csv)):
         k = pick(clean(r["Kernel_Name"]))
-        if k and not ("<1, false, false, 1, 1, 12>" in k and int(r["Grid_Size_X"]) != 81920):
+        if k and int(r["Grid_Size_X"]) == decode_grid.get(k, int(r["Grid_Size_X"])):
             durations[k].append(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
     agg, n = defaultdict(lambda: defaultdict(float)), defaultdict(int)
     for d, c in per.items():
