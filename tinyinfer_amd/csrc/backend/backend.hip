@@ -759,19 +759,26 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
     }
     int32_t* const m_fast = m0 + fast_at;
     if (fast_decode) {
-        // Decode: row q is sequence q's only row.
+        // Decode: row q is sequence q's only row. Whole splits first, then
+        // each row's shorter last split (attention per layer: config 4 15.8-16.1
+        // vs 17.2 us in row order, config 5B 80.1 vs 82.4, config 3 within
+        // noise).
         size_t f = 0;
-        for (int q = 0; q < nseq; ++q) {
-            const int length = steps[q].used + 1, split = mphip::fast_attention_split(length);
-            const int splits = (length + split - 1) / split;
-            for (int kvh = 0; kvh < c.kv_heads; ++kvh)
-                for (int sp = 0; sp < splits; ++sp, ++f) {
-                    m_fast[4 * f] = q;
-                    m_fast[4 * f + 1] = steps[q].table_slot * c.kv_heads + kvh;
-                    m_fast[4 * f + 2] = sp * split;
-                    m_fast[4 * f + 3] = std::min(split, length - sp * split) | (sp << 16);
-                }
-        }
+        for (int pass = 0; pass < 2; ++pass)
+            for (int q = 0; q < nseq; ++q) {
+                const int length = steps[q].used + 1, split = mphip::fast_attention_split(length);
+                const int splits = (length + split - 1) / split;
+                for (int kvh = 0; kvh < c.kv_heads; ++kvh)
+                    for (int sp = 0; sp < splits; ++sp) {
+                        const int n = std::min(split, length - sp * split);
+                        if ((n == split) != (pass == 0)) continue;
+                        m_fast[4 * f] = q;
+                        m_fast[4 * f + 1] = steps[q].table_slot * c.kv_heads + kvh;
+                        m_fast[4 * f + 2] = sp * split;
+                        m_fast[4 * f + 3] = n | (sp << 16);
+                        ++f;
+                    }
+            }
     }
     status = check(h, hipMemcpyAsync(h->meta, m0, sizeof(int32_t) * entries, hipMemcpyHostToDevice, h->stream),
                    "upload input tokens");

@@ -150,8 +150,8 @@ __host__ __device__ inline int fast_attention_split(int length) {
 }
 struct FastAttentionWork {
     // per work item (int4): row, table slot * kv_heads + KV head, first
-    // token, token count | split index << 16; the items of a row are KV head
-    // major, then split order
+    // token, token count | split index << 16, in any order (the forward
+    // puts every row's whole splits before the shorter last ones)
     const int32_t* items;
     int items_count;
     // Splits of the longest row; the partial results of (row, KV head,
