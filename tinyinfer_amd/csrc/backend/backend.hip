@@ -698,19 +698,23 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
     // depend on the rest of the batch.
     const int dim_ = c.hidden / c.heads, group_ = c.heads / c.kv_heads;
     const bool fast_decode = h->fast && decode && h->kv.block_tokens == 16 && dim_ == 64 && group_ <= 4;
-    size_t fast_items = 0;
+    size_t fast_items = 0, fast_short = 0;
     int max_splits = 0;
     if (fast_decode)
         for (int q = 0; q < nseq; ++q) {
             const int length = steps[q].used + 1, split = mphip::fast_attention_split(length);
             const int splits = (length + split - 1) / split;
+            if (mphip::fast_attention_short(length)) {
+                fast_short += (size_t)c.kv_heads;
+                continue;
+            }
             fast_items += (size_t)c.kv_heads * splits;
             max_splits = std::max(max_splits, splits);
         }
     const size_t base_entries =
         3 * (size_t)R + 2 * (size_t)nseq + 2 * nblocks + 2 * items + 2 * table_pairs + 3 * copies;
     const size_t fast_at = (base_entries + 3) / 4 * 4;  // int4 items need 16-byte alignment
-    const size_t entries = fast_decode ? fast_at + 4 * fast_items : base_entries;
+    const size_t entries = fast_decode ? fast_at + 4 * fast_items + 4 * fast_short : base_entries;
     if ((status = ensure_call_buffers(h, entries))) return status;
     if (fast_decode) {
         // Partials of (row, KV head, split) at a fixed stride of max_splits.
@@ -768,6 +772,7 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
             for (int q = 0; q < nseq; ++q) {
                 const int length = steps[q].used + 1, split = mphip::fast_attention_split(length);
                 const int splits = (length + split - 1) / split;
+                if (mphip::fast_attention_short(length)) continue;
                 for (int kvh = 0; kvh < c.kv_heads; ++kvh)
                     for (int sp = 0; sp < splits; ++sp) {
                         const int n = std::min(split, length - sp * split);
@@ -779,6 +784,16 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
                         ++f;
                     }
             }
+        int32_t* const m_short = m_fast + 4 * fast_items;
+        size_t r = 0;
+        for (int q = 0; q < nseq; ++q)
+            if (mphip::fast_attention_short(steps[q].used + 1))
+                for (int kvh = 0; kvh < c.kv_heads; ++kvh, ++r) {
+                    m_short[4 * r] = q;
+                    m_short[4 * r + 1] = steps[q].table_slot * c.kv_heads + kvh;
+                    m_short[4 * r + 2] = steps[q].used + 1;
+                    m_short[4 * r + 3] = 0;
+                }
     }
     status = check(h, hipMemcpyAsync(h->meta, m0, sizeof(int32_t) * entries, hipMemcpyHostToDevice, h->stream),
                    "upload input tokens");
@@ -904,6 +919,8 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
         mphip::FastAttentionWork fw{};
         fw.items = h->meta + (m_fast - m0);
         fw.items_count = (int)fast_items;
+        fw.short_items = h->meta + (m_fast - m0) + 4 * fast_items;
+        fw.short_count = (int)fast_short;
         fw.max_splits = max_splits;
         fw.partial_out = h->fast_partials;
         fw.partial_ml = h->fast_partials + (size_t)R * c.kv_heads * max_splits * group_ * 64;

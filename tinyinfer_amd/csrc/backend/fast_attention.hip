@@ -29,9 +29,10 @@
 // exceeds it by more than 16 (probabilities then stay below e^16 and the
 // sums are rescaled), so most pages need no cross-lane maximum.
 // Loads past the split's last page re-read that page (a cache hit) so that
-// every load is unconditional and the waits stay exact. A row whose
-// context is one split writes its output directly; otherwise every split
-// writes its partial and a merge kernel combines them.
+// every load is unconditional and the waits stay exact. Rows of up to 256
+// tokens (at most 8 splits) run as one work-group per (row, KV head) that
+// combines its splits in LDS; the splits of longer rows write partials that
+// a merge kernel combines.
 // (Combining in the last split to finish costs each split a store
 // completion and an atomic round trip at its end, more than the extra
 // launch; with a device-scope release fence it would also write back the
@@ -59,19 +60,17 @@ constexpr float kScale = 0.125f;  // 1/sqrt(64)
 constexpr float kRescale = 16.0f;  // probabilities stay below e^16 before a rescale
 
 
+// One split: tokens t0..t0+n-1 (t0 page-aligned, at most kSplitPages pages)
+// of the row whose page table is `table`, for the G query heads of KV head
+// kvh. Gives per head the reference maximum m, the denominator l and lane
+// d's weighted sum acc (not yet divided). `touch` numbers this wavefront's
+// 8 KB slice of the weight prefetch; p_s is the wavefront's own LDS.
 template <int G>
-__global__ __launch_bounds__(kItemsPerGroup * 64) void fast_attention_kernel(const float* __restrict__ qkv, int ldq,
-                                                                             RowMeta meta, PagedKv kv, int layer,
-                                                                             FastAttentionWork w,
-                                                                             float* __restrict__ out, int ldo) {
+__device__ __forceinline__ void attend_split(const float* __restrict__ qkv, int ldq, const PagedKv& kv, int layer,
+                                             const FastAttentionWork& w, const int32_t* table, int row, int kvh,
+                                             int t0, int n, uint64_t touch, float (&p_s)[G][kPage], float (&m)[G],
+                                             float (&l)[G], float (&acc)[G]) {
     const int lane = threadIdx.x & 63;
-    __shared__ float p_s[kItemsPerGroup][G][kPage];
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int index = blockIdx.x * kItemsPerGroup + wave;
-    if (index >= w.items_count) return;
-    const int4 item = reinterpret_cast<const int4*>(w.items)[index];
-    const int row = item.x, kvh = item.y % w.kv_heads, t0 = item.z, n = item.w & 0xFFFF, sp = item.w >> 16;
-    const int32_t* table = kv.tables + (size_t)(item.y / w.kv_heads) * kv.table_stride;
     const int t = lane >> 2, dq = lane & 3;
     const int end = t0 + n;           // tokens t0..end-1 (t0 page-aligned)
     const int first = t0 / kPage;     // the split's first page
@@ -106,7 +105,7 @@ __global__ __launch_bounds__(kItemsPerGroup * 64) void fast_attention_kernel(con
     // i (128 bytes) of the slice.
     float touched = 0.0f;
     {
-        uint64_t at = ((uint64_t)index * 64 + lane) * 128;
+        uint64_t at = (touch * 64 + lane) * 128;
         const char* line = nullptr;
 #pragma unroll
         for (int r = 0; r < FastAttentionWork::kPrefetchRanges; ++r) {
@@ -125,7 +124,7 @@ __global__ __launch_bounds__(kItemsPerGroup * 64) void fast_attention_kernel(con
     // d's output. Probabilities are exp(s - m) with m raised only when a
     // score exceeds it by more than kRescale (then the sums are rescaled),
     // so a page costs no cross-lane maximum unless the scores climb.
-    float m[G], lp[G], acc[G];
+    float lp[G];
 #pragma unroll
     for (int h = 0; h < G; ++h) {
         lp[h] = 0.0f;
@@ -166,7 +165,7 @@ __global__ __launch_bounds__(kItemsPerGroup * 64) void fast_attention_kernel(con
             }
             const float p = valid ? __expf(s[h] - m[h]) : 0.0f;
             lp[h] += p;
-            if (dq == 0) p_s[wave][h][t] = p;
+            if (dq == 0) p_s[h][t] = p;
         }
         // Slots past the context (last page only) hold stale values: they
         // take no part, whatever they are.
@@ -191,7 +190,7 @@ __global__ __launch_bounds__(kItemsPerGroup * 64) void fast_attention_kernel(con
             float ag[4];
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-                const f4 pv = reinterpret_cast<const f4*>(p_s[wave][h])[g];
+                const f4 pv = reinterpret_cast<const f4*>(p_s[h])[g];
                 ag[g] = pv.x * v[g].x;
                 ag[g] += pv.y * v[g].y;
                 ag[g] += pv.z * v[g].z;
@@ -205,15 +204,26 @@ __global__ __launch_bounds__(kItemsPerGroup * 64) void fast_attention_kernel(con
         __builtin_amdgcn_sched_barrier(0);
     }
     asm volatile("" ::"v"(touched));  // the prefetch's value is not used
-    float l[G];
 #pragma unroll
     for (int h = 0; h < G; ++h) l[h] = rows_sum(row_quads_sum(lp[h]));  // each token once
-    if (t0 == 0 && n == meta.row_pos[row] + 1) {
-        // The row's only split: the output itself.
-#pragma unroll
-        for (int h = 0; h < G; ++h) out[quad_index(row, (kvh * G + h) * kDim + lane, ldo)] = acc[h] / l[h];
-        return;
-    }
+}
+
+// Splits of rows of more than 256 tokens, one wavefront per work item.
+template <int G>
+__global__ __launch_bounds__(kItemsPerGroup * 64) void fast_attention_kernel(const float* __restrict__ qkv, int ldq,
+                                                                             RowMeta meta, PagedKv kv, int layer,
+                                                                             FastAttentionWork w,
+                                                                             float* __restrict__ out, int ldo) {
+    const int lane = threadIdx.x & 63;
+    __shared__ float p_s[kItemsPerGroup][G][kPage];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int index = blockIdx.x * kItemsPerGroup + wave;
+    if (index >= w.items_count) return;
+    const int4 item = reinterpret_cast<const int4*>(w.items)[index];
+    const int row = item.x, kvh = item.y % w.kv_heads, t0 = item.z, n = item.w & 0xFFFF, sp = item.w >> 16;
+    const int32_t* table = kv.tables + (size_t)(item.y / w.kv_heads) * kv.table_stride;
+    float m[G], l[G], acc[G];
+    attend_split<G>(qkv, ldq, kv, layer, w, table, row, kvh, t0, n, (uint64_t)index, p_s[wave], m, l, acc);
     const size_t slot = ((size_t)row * w.kv_heads + kvh) * w.max_splits + sp;
 #pragma unroll
     for (int h = 0; h < G; ++h) {
@@ -224,6 +234,64 @@ __global__ __launch_bounds__(kItemsPerGroup * 64) void fast_attention_kernel(con
             w.partial_ml[at * 2 + 1] = l[h];
         }
     }
+}
+
+// Rows of up to 256 tokens (fast_attention_short: at most kSplitPages
+// splits of 16 or 32 tokens): one work-group per (row, KV head) of
+// w.short_items, wavefront s takes split s, and the splits are combined
+// through LDS in split order by one wavefront per query head, so these
+// rows need no merge launch. A row of one split gives acc / l exactly.
+template <int G>
+__global__ __launch_bounds__(kSplitPages * 64) void fast_attention_short_kernel(const float* __restrict__ qkv,
+                                                                                int ldq, RowMeta meta, PagedKv kv,
+                                                                                int layer, FastAttentionWork w,
+                                                                                float* __restrict__ out, int ldo) {
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    __shared__ float p_s[kSplitPages][G][kPage];
+    __shared__ float part_ml[kSplitPages][G][2];
+    __shared__ float part_acc[kSplitPages][G][kDim];
+    // (row, slot * kv_heads + KV head, tokens): the length rides in the item,
+    // one dependent load fewer before the pages.
+    const int4 item = reinterpret_cast<const int4*>(w.short_items)[blockIdx.x];
+    const int row = item.x, kvh = item.y % w.kv_heads, length = item.z;
+    const int32_t* table = kv.tables + (size_t)(item.y / w.kv_heads) * kv.table_stride;
+    const int split = fast_attention_split(length);
+    const int splits = (length + split - 1) / split;  // 1..kSplitPages
+    if (wave < splits) {
+        float m[G], l[G], acc[G];
+        const int t0 = wave * split;
+        attend_split<G>(qkv, ldq, kv, layer, w, table, row, kvh, t0, min(split, length - t0),
+                        (uint64_t)blockIdx.x * kSplitPages + wave, p_s[wave], m, l, acc);
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+            part_acc[wave][h][lane] = acc[h];
+            if (lane == 0) {
+                part_ml[wave][h][0] = m[h];
+                part_ml[wave][h][1] = l[h];
+            }
+        }
+    }
+    __syncthreads();
+    if (wave >= G) return;
+    // Query head h: lane s < splits holds split s's (maximum, denominator)
+    // (all in the first 16-lane row), lane d sums its dimension over the
+    // splits in order.
+    const int h = wave;
+    const bool mine = lane < splits;
+    const int sl = min(lane, kSplitPages - 1);
+    const float ms = mine ? part_ml[sl][h][0] : -__builtin_inff();
+    const float ls = mine ? part_ml[sl][h][1] : 0.0f;
+    float mx = fmaxf(ms, dpp<kDppQuadXor1>(ms));
+    mx = fmaxf(mx, dpp<kDppQuadXor2>(mx));
+    mx = lane_value(row_quads_max(mx), 0);
+    const float f = mine ? (splits == 1 ? 1.0f : __expf(ms - mx)) : 0.0f;
+    const float den = lane_value(row_sum(ls * f), 0);
+    float num = 0.0f;
+#pragma unroll
+    for (int s = 0; s < kSplitPages; ++s)
+        if (s < splits) num += part_acc[s][h][lane] * lane_value(f, s);
+    out[quad_index(row, (kvh * G + h) * kDim + lane, ldo)] = num / den;
 }
 
 // out[row][h*64 + d] for rows of more than one split: the splits of
@@ -287,9 +355,9 @@ __global__ __launch_bounds__(256) void fast_attention_merge_kernel(int rows, int
     // The row's position is first needed here, after the loads above are in flight.
     __builtin_amdgcn_sched_barrier(0);
     asm volatile("" : "+v"(pos));
+    if (fast_attention_short(pos + 1)) return;  // written by the short-row kernel
     const int split = fast_attention_split(pos + 1);
     const int splits = (pos + split) / split;  // ceil((pos + 1) / split)
-    if (splits == 1) return;  // written by the split kernel
     combine(0, splits);
     for (int r = 1; 4 * r * kMergeHeld < splits; ++r) {
         load(r, splits);
@@ -314,8 +382,12 @@ __global__ __launch_bounds__(256) void fast_attention_merge_kernel(int rows, int
 template <int G>
 void launch_items(hipStream_t s, const float* qkv, int ldq, const RowMeta& meta, const PagedKv& kv, int layer,
                   const FastAttentionWork& w, float* out, int ldo) {
-    fast_attention_kernel<G><<<(w.items_count + kItemsPerGroup - 1) / kItemsPerGroup, kItemsPerGroup * 64, 0, s>>>(
-        qkv, ldq, meta, kv, layer, w, out, ldo);
+    if (w.short_count > 0)
+        fast_attention_short_kernel<G><<<w.short_count, kSplitPages * 64, 0, s>>>(qkv, ldq, meta, kv, layer, w, out,
+                                                                                  ldo);
+    if (w.items_count > 0)
+        fast_attention_kernel<G><<<(w.items_count + kItemsPerGroup - 1) / kItemsPerGroup, kItemsPerGroup * 64, 0,
+                                   s>>>(qkv, ldq, meta, kv, layer, w, out, ldo);
 }
 
 }  // namespace
@@ -336,7 +408,7 @@ hipError_t launch_fast_attention(hipStream_t s, const float* qkv, int ldq, int r
     default: launch_items<4>(s, qkv, ldq, meta, kv, layer, w, out, ldo); break;
     }
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
+    if (e != hipSuccess || w.items_count <= 0) return e;
     fast_attention_merge_kernel<<<(rows * heads + 3) / 4, 256, 0, s>>>(rows, heads, kv_heads, meta, w, out, ldo);
     return hipGetLastError();
 }

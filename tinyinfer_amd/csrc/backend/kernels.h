@@ -148,12 +148,19 @@ __host__ __device__ inline int fast_attention_split(int length) {
     const int pages = (length + 15) / 16;
     return pages <= 16 ? 16 * ((pages + 7) / 8) : 128;
 }
+// Rows of up to 256 tokens (at most 8 splits) are combined inside one
+// work-group; longer rows through the partials and the merge kernel.
+__host__ __device__ inline bool fast_attention_short(int length) { return (length + 15) / 16 <= 16; }
 struct FastAttentionWork {
     // per work item (int4): row, table slot * kv_heads + KV head, first
     // token, token count | split index << 16, in any order (the forward
     // puts every row's whole splits before the shorter last ones)
-    const int32_t* items;
+    const int32_t* items;  // splits of the rows longer than 256 tokens
     int items_count;
+    // per row of up to 256 tokens and KV head (int4): row, table slot *
+    // kv_heads + KV head, tokens, 0
+    const int32_t* short_items;
+    int short_count;
     // Splits of the longest row; the partial results of (row, KV head,
     // split) sit at slot (row * kv_heads + KV head) * max_splits + split.
     int max_splits;
