@@ -131,14 +131,15 @@ def attention_probe_model(context: int, seed: int) -> OracleModel:
 @pytest.mark.parametrize("key_scale", [0.5, 6.0])
 def test_fast_long_rows_merge_many_splits(torch_cuda, key_scale):
     """Decode rows whose contexts are cut into 1 to 129 splits (16,401 tokens:
-    three rounds of the merge's loads; 8,251: two; 1,901; 131 and 33 and 17
-    tokens in 32- and 16-token splits, where some of the merge's four lane
-    groups hold no split; 10: one split, written directly), over pools of
+    three rounds of the merge's loads; 8,251: two; 1,901; 257: the shortest
+    row of 128-token splits, three of them; 256: the longest row combined in
+    one work-group, 8 splits of 32 tokens; 131, 33, 17 tokens in 32- and
+    16-token splits; 10: one split), over pools of
     seeded keys and values: key_scale 0.5 spreads the softmax over the whole
     context, 6.0 makes it peak at a few tokens and raises the running
     maxima inside splits. One decode step against the oracle on the same
     pools, logits within 1e-3 relative."""
-    used = [16400, 8250, 1900, 130, 32, 16, 9]
+    used = [16400, 8250, 1900, 256, 255, 130, 32, 16, 9]
     context = 16640
     model = attention_probe_model(context, seed=47)
     cfg = model.config
