@@ -351,7 +351,7 @@ __global__ __launch_bounds__(256) void fast_attention_merge_kernel(int rows, int
         }
         gm = rm;
     };
-    load(0, w.max_splits);  // bounded by the batch's longest row until the row's own count is known
+    load(0, w.max_splits);  // bounded by the batch's longest long row until the row's own count is known
     // The row's position is first needed here, after the loads above are in flight.
     __builtin_amdgcn_sched_barrier(0);
     asm volatile("" : "+v"(pos));

@@ -161,7 +161,8 @@ struct FastAttentionWork {
     // kv_heads + KV head, tokens, 0
     const int32_t* short_items;
     int short_count;
-    // Splits of the longest row; the partial results of (row, KV head,
+    // Splits of the longest row (of those longer than 256 tokens; 0 if
+    // none); the partial results of (row, KV head,
     // split) sit at slot (row * kv_heads + KV head) * max_splits + split.
     int max_splits;
     float* partial_out;  // [slot][G][64]
