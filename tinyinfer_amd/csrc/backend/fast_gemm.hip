@@ -465,14 +465,16 @@ hipError_t launch_fast(hipStream_t s, const FastGemmArgs& a) {
 }
 
 // Tile shape by size. At decode sizes (one row tile) the tiles are small,
-// for many work-groups (SwiGLU over 33-64 rows takes two row blocks: its two
-// weight matrices make its column blocks the heaviest; up to 32 rows one,
-// 6.3-6.5 instead of 8.0-8.7 us at 1 and 32 rows). The LM head takes
-// 64-row x 64-column tiles, and so does a projection of more than one row
-// tile when they still give every CU a work-group: they read each weight and
-// each activation a quarter as often. Between the two (a few hundred rows
-// over a 576-column projection: 36 such tiles) the largest of 64 x 16,
-// 32 x 16 and 16 x 16 that gives every CU a work-group.
+// for many work-groups (SwiGLU over more than 32 rows takes two row blocks:
+// its two weight matrices make its column blocks the heaviest; up to 32 rows one,
+// 6.3-6.5 instead of 8.0-8.7 us at 1 and 32 rows), and so up to 256 rows
+// (at 256 rows they beat the larger tiles below: O 6.6 vs 7.5, down 12.5 vs
+// 14.8, gate/up 16.9 vs 18.9 us). The LM head takes 64-row x 64-column
+// tiles, and so does a projection of more than 256 rows when they still
+// give every CU a work-group: they read each weight and each activation a
+// quarter as often. Otherwise the largest of 64 x 16, 32 x 16 and 16 x 16
+// that gives every CU a work-group. (The q|k|v+RoPE projection keeps
+// 64 x 16 or 32 x 16 tiles above 64 rows: 11.2 vs 16.0 us at 256 rows.)
 constexpr int kCus = 256;
 bool head_wide(int columns) { return columns % 64 == 0; }
 int tiles(const FastGemmArgs& a, int rb, int cb) { return ((a.rows + 15) / 16 + rb - 1) / rb * (a.columns / 16 / cb); }
@@ -484,7 +486,7 @@ hipError_t launch_sized(hipStream_t s, const FastGemmArgs& a) {
         if (head_wide(a.columns)) return launch_fast<EPI, NORM, GATHER, 4, 4, 1>(s, a);
         return launch_fast<EPI, NORM, GATHER, 1, 1, 6>(s, a);
     } else {
-        if (a.rows > 64) {
+        if (a.rows > 256) {
             if (a.columns % 64 == 0 && tiles(a, 4, 4 / M) >= kCus)
                 return launch_fast<EPI, NORM, GATHER, 4, 4 / M, 2>(s, a);
             if (tiles(a, 4, 1) >= kCus) return launch_fast<EPI, NORM, GATHER, 4, 1, 2>(s, a);
