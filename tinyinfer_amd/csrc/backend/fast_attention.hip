@@ -15,8 +15,8 @@
 // is read once. It walks the split's (up to 8) pages with two pages in
 // flight in a ring of registers: the loads of page k+2 are issued as soon
 // as page k has been used (with 2,000-3,000 wavefronts in flight a third
-// page only deepens the queues at HBM). Per page (16 tokens of one layer and KV head,
-// 4 KB of K then 4 KB of V, device page order of layout.h):
+// page only deepens the queues at HBM). Per page (16 tokens of one layer
+// and KV head, 4 KB of K then 4 KB of V, device page order of layout.h):
 //  - scores: lane = (token t = lane/4, quarter dq = lane%4 of the 64 dims);
 //    a lane reads 4 float4 of K (dims 16dq..16dq+15 of token t, the 16 lanes
 //    of one float4 index forming a 256-byte run) and the four quarters are
