@@ -53,6 +53,7 @@ from __future__ import annotations
 
 import argparse
 import csv
+import gc
 import json
 import os
 import platform
@@ -114,6 +115,12 @@ def gpu_leg(args, wl):
     engine.set_batching(True)
     log(f"setup {time.perf_counter() - t:.1f}s: {wl.name}, pool {wl.max_blocks} pages, "
         f"prompts sum {sum(len(r.prompt) for r in wl.requests)}")
+    # Long-lived objects (torch, numpy, the workload) move out of the cyclic
+    # garbage collector's reach: a full collection over them otherwise lands
+    # in some timed windows as one ~35 ms pause inside poll_events (the event
+    # dicts trigger it), 0.9 ms per step at B=256.
+    gc.collect()
+    gc.freeze()
 
     generated = defaultdict(int)
     finished = set()
