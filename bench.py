@@ -524,7 +524,7 @@ def main():
         summarise_counters(*args.summarise_counters)
         return
     if args.gpus != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (decode would shard by request, "
+        print("bench.py measures one GPU: this library has no multi-GPU path (decode would shard by request, "
               "one engine per GPU); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
     from tinyinfer_amd import workloads

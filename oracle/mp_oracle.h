@@ -9,7 +9,8 @@
  * built with its default (SSE2, no FMA) flags.
  *
  * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
- * load this library, and only as the checker. The product path never does.
+ * load this library, and only to check results against it. The product path
+ * never does.
  *
  * Build: `make -C oracle` (gcc -ffp-contract=off; libm supplies expf, powf,
  * cosf and sinf exactly as the reference's std::exp/pow/cos/sin on float).

@@ -39,7 +39,7 @@ def pool_elements(config: dict, block_tokens: int, max_blocks: int) -> int:
 
 def reference_library():
     """The reference's own MiniPrefix (Engine, KVManager, CpuRunner) compiled
-    from its sources into oracle/_ref (the checker), or None if not built."""
+    from its sources into oracle/_ref, or None if not built."""
     from oracle import ref_library
     return ref_library()
 

@@ -3,7 +3,7 @@ FP32 matrix cores, decode attention split over the context) against the
 oracle, which restates the reference CPU path.
 
 The fast mode sums in its own order, so logits are compared within the
-north-star bound, max relative error 1e-3, taken over the whole logit vector
+specified bound, max relative error 1e-3, taken over the whole logit vector
 (max |got - want| / max |want|: an element-wise ratio is meaningless for
 logits near zero), and the greedy token must equal the oracle's, which the
 test also reports against the oracle's top-2 margin. Per-row results must

@@ -2,7 +2,7 @@
 
 The oracle restates the reference CPU path (miniprefix/src/backend/cpu/
 llama_runner.cpp:10-104) op for op; the HIP kernels keep its floating-point
-order, so logits are compared bit for bit (max relative
+order, so logits are compared bit for bit (the specified bar, max relative
 error 1e-3, is asserted as well to report how far off a failure is)."""
 import numpy as np
 import pytest
@@ -25,8 +25,8 @@ def _logits_match(got, want):
 
 
 def test_config1_paged_attention_decode(torch_cuda):
-    """T=503 (31 full pages + 7), 256-page pool, seeded
-    permutation table, Q/K/V ~ N(0,1), scale 1/sqrt(64)."""
+    """The single paged-attention op: T=503 (31 full pages + 7), 256-page
+    pool, seeded permutation table, Q/K/V ~ N(0,1), scale 1/sqrt(64)."""
     torch = torch_cuda
     o = Oracle()
     seed, bt, pages, heads, kvh, dim, T = 2024, 16, 256, 9, 3, 64, 503

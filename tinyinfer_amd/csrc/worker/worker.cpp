@@ -1,6 +1,6 @@
 // MiniPrefix worker over the HIP runner: the reference worker's command line
 // and protocol v3 on stdin/stdout (miniprefix/apps/worker.cpp:6-21), with the
-// backends of this build:
+// backends of this worker:
 //   hip       the HIP runner in the exact arithmetic (logits bit-identical
 //             to the reference CPU runner), the drop-in for cpu/cuda;
 //   hip-fast  the HIP runner in the fast arithmetic (FP32 matrix cores,
