@@ -22,8 +22,11 @@ Per configuration, tests/golden/<config>.npz holds:
   30-layer model;
 - cow [2]: copy-on-write pages and bytes of that run, scaled to the real
   model's bytes per token.
+With --engine-only there are no token streams (R = 0): the page tables, token
+counts and COW counts alone, for a workload whose reference CPU prefill takes
+too long (config 5A's 16,384-token prompts).
 
-Usage: python tests/golden/make_fixtures.py [config ...] [--jobs N]
+Usage: python tests/golden/make_fixtures.py [config ...] [--jobs N] [--engine-only]
 """
 from __future__ import annotations
 
@@ -179,26 +182,27 @@ def engine_trace(name: str):
     return digests, np.array(stats, dtype=np.int64), np.array([cost["cow_pages"], cow_bytes], dtype=np.int64)
 
 
-def generate(name: str, jobs: int):
+def generate(name: str, jobs: int, engine_only: bool = False):
     wl = WORKLOADS[name]()
-    rows = rows_of(name, wl)
+    rows = [] if engine_only else rows_of(name, wl)
     t0 = time.time()
     digests, stats, cow = engine_trace(name)
     print(f"{name}: engine trace of {len(digests)} steps in {time.time() - t0:.1f}s, cow {cow.tolist()}", flush=True)
-    groups = [rows[i::jobs] for i in range(jobs) if rows[i::jobs]]
-    with mp.get_context("spawn").Pool(len(groups)) as pool:
-        parts = pool.map(stream_job, [(name, g) for g in groups])
     merged = {}
-    for p in parts:
-        merged.update(p)
-    steps = decode_steps(name, wl, rows[0])
+    groups = [rows[i::jobs] for i in range(jobs) if rows[i::jobs]]
+    if groups:
+        with mp.get_context("spawn").Pool(len(groups)) as pool:
+            parts = pool.map(stream_job, [(name, g) for g in groups])
+        for p in parts:
+            merged.update(p)
+    steps = decode_steps(name, wl, rows[0]) if rows else 0
     np.savez_compressed(
         OUT / f"{name}.npz",
         rows=np.array(rows, dtype=np.int32),
-        tokens=np.array([merged[r][0] for r in rows], dtype=np.int32),
-        top=np.array([merged[r][1] for r in rows], dtype=np.float32),
-        margins=np.array([merged[r][2] for r in rows], dtype=np.float32),
-        sample_steps=np.array(sample_steps(steps), dtype=np.int32),
+        tokens=np.array([merged[r][0] for r in rows], dtype=np.int32).reshape(len(rows), steps),
+        top=np.array([merged[r][1] for r in rows], dtype=np.float32).reshape(len(rows), steps),
+        margins=np.array([merged[r][2] for r in rows], dtype=np.float32).reshape(len(rows), steps),
+        sample_steps=np.array(sample_steps(steps) if steps else [], dtype=np.int32),
         samples=np.array([merged[r][3] for r in rows], dtype=np.float32),
         sample_stride=np.int32(SAMPLE_STRIDE),
         table_hash=np.array(digests),
@@ -206,7 +210,8 @@ def generate(name: str, jobs: int):
         cow=cow,
         meta=np.array(json.dumps({"workload": name, "description": wl.description,
                                   "reference": "miniprefix CpuRunner + Engine compiled from its sources",
-                                  "decode_steps": steps})))
+                                  "decode_steps": steps,
+                                  "token_streams": "none: engine trace only" if engine_only else "rows"})))
     print(f"{name}: wrote {OUT / (name + '.npz')} in {time.time() - t0:.1f}s", flush=True)
 
 
@@ -214,11 +219,14 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("configs", nargs="*", default=["config2", "config3", "config4", "config5b", "config5a"])
     ap.add_argument("--jobs", type=int, default=8)
+    ap.add_argument("--engine-only", action="store_true",
+                    help="page tables, token counts and COW counts of the reference Engine only, no token streams "
+                         "(config5a's reference CPU prefill of a 16,384-token prompt takes many hours)")
     args = ap.parse_args()
     if ref_library() is None:
         raise SystemExit("oracle/_ref/libmp_ref.so is not built (make -C oracle ref, with the reference tree)")
     for name in args.configs:
-        generate(name, args.jobs)
+        generate(name, args.jobs, args.engine_only)
 
 
 if __name__ == "__main__":
