@@ -449,10 +449,11 @@ def summarise_sq(counter_csv: str, trace_csv: str, out: str, command: str):
     decode = ("fast_attention_kernel<", "fast_attention_merge_kernel", "fast_gemm_kernel<4, true, false, 1, 1, 12>",
               "fast_gemm_kernel<1, false, false, 1, 1, 12>", "fast_gemm_kernel<2, true, false, 2, 1, 6>",
               "fast_gemm_kernel<3, true, true, 4, 4, ")
-    # Grid (threads) of the B=64 decode launches of instantiations that the
-    # prefill's last short chunk also runs, on other shapes.
+    # Grid (threads) of the B=64 decode launches of instantiations that
+    # prefill steps of up to 256 rows also run, on other shapes.
     decode_grid = {"fast_gemm_kernel<4, true, false, 1, 1, 12>": 131072,
-                   "fast_gemm_kernel<1, false, false, 1, 1, 12>": 81920}
+                   "fast_gemm_kernel<1, false, false, 1, 1, 12>": 81920,
+                   "fast_gemm_kernel<2, true, false, 2, 1, 6>": 98304}
     pick = lambda n: next((k for k in decode if k in n), None)
     per, meta = defaultdict(dict), {}
     for r in csv.DictReader(open(counter_csv)):
