@@ -8,12 +8,12 @@ arithmetic). After every engine step the digest of every resident
 sequence's committed page table and the step's token counts must equal the
 reference Engine's; the copy-on-write counters must equal its counts at the
 end; and the greedy tokens of the fixture's requests must equal the
-reference CpuRunner's at every recorded step. Config 5A's fixture may hold
-no token streams (tests/golden/make_fixtures.py --engine-only: the
-reference's CPU prefill of a 16,384-token prompt takes many hours); its
-page tables, token counts and COW counts are checked at full size all the
-same. The fixtures also hold each step's top-2 logit margin, which tells how
-close a mismatch would have been to a tie."""
+reference CpuRunner's at every recorded step (config 5A: the first 16
+decode steps of one request, the reference's 16,384-token CPU prefill being
+the cost; a fixture written with make_fixtures.py --engine-only holds no
+token streams, and then only the page tables and counts are checked). The
+fixtures also hold each step's top-2 logit margin, which tells how close a
+mismatch would have been to a tie."""
 import hashlib
 from pathlib import Path
 
