@@ -695,7 +695,8 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
     // Fast-mode decode attention: work items (row, KV head, first token,
     // tokens | split << 16) over each row's splits (fast_attention_split).
     // The split depends on nothing but the row, so a row's result does not
-    // depend on the rest of the batch.
+    // depend on the rest of the batch (steps that also prefill take the
+    // prefill attention for every row).
     const int dim_ = c.hidden / c.heads, group_ = c.heads / c.kv_heads;
     const bool fast_decode = h->fast && decode && h->kv.block_tokens == 16 && dim_ == 64 && group_ <= 4;
     size_t fast_items = 0, fast_short = 0;
