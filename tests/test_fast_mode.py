@@ -173,3 +173,43 @@ def test_fast_long_rows_merge_many_splits(torch_cuda, key_scale):
         assert am[i] == int(np.argmax(got[i]))
     backend.close()
     print(f"max relative logit error {worst:.3e}")
+
+
+def test_fast_decode_rows_same_in_mixed_steps(torch_cuda):
+    """A decoding row's logits are bit-identical whether its step only
+    decodes or also prefills another sequence: one-token rows take the
+    decode attention in both (rows of 120 tokens: one work-group; 700
+    tokens: splits and merge), the prefilling rows the row-block kernels.
+    In the mixed step every row is also checked against the oracle."""
+    cfg = smollm_config(layers=2, context=1024, vocabulary=4096)
+    model = OracleModel(cfg, seed=53)
+    bt, o = 16, Oracle()
+    lengths = [119, 699, 300]
+    prompts = [[int(t) for t in o.fill_tokens(L, 53, 9500 + i, cfg["vocabulary"])] for i, L in enumerate(lengths)]
+    tables = [np.arange(60 * i, 60 * i + 60, dtype=np.int32) for i in range(3)]
+
+    def run(mixed):
+        backend = HipBackend(cfg, block_tokens=bt, max_blocks=180, max_sequences=3, arithmetic=ARITHMETIC_FAST)
+        upload_model(backend, model)
+        for i, t in enumerate(tables):
+            backend.table_write(i, 0, t)
+        am, _ = backend.forward([(0, 0, lengths[0]), (1, 0, lengths[1])], prompts[0] + prompts[1])
+        nxt = [int(am[0]), int(am[1])]
+        steps = [(0, lengths[0], 1), (1, lengths[1], 1)] + ([(2, 0, lengths[2])] if mixed else [])
+        _, got = backend.forward(steps, nxt + (prompts[2] if mixed else []))
+        backend.close()
+        return nxt, got
+
+    nxt, alone = run(False)
+    nxt_mixed, mixed = run(True)
+    assert nxt == nxt_mixed
+    for i in range(2):
+        assert np.array_equal(alone[i].view(np.uint32), mixed[i].view(np.uint32)), f"row {i}"
+    n = pool_elements(cfg, bt, 180)
+    keys, values = np.zeros(n, dtype=np.float32), np.zeros(n, dtype=np.float32)
+    for i in range(2):
+        model.append(keys, values, bt, tables[i], 0, prompts[i])
+    want = [model.append(keys, values, bt, tables[i], lengths[i], [nxt[i]]) for i in range(2)]
+    want.append(model.append(keys, values, bt, tables[2], 0, prompts[2]))
+    for i in range(3):
+        assert rel_inf(mixed[i], want[i]) <= 1e-3, f"row {i}: relative error {rel_inf(mixed[i], want[i]):.3e}"

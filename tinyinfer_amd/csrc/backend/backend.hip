@@ -676,11 +676,20 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
     // attention row blocks (first row, rows) by decreasing attended length |
     // scores work items (block, chunk).
     const int block_rows = mphip::attention_row_block(c.heads, c.kv_heads, c.hidden / c.heads);
+    // Fast mode (16-token pages, 64-wide heads, at most 4 query heads per KV
+    // head): every one-token sequence takes the decode attention kernels,
+    // also in a step that prefills others, so a decoding row's result does
+    // not depend on the rest of the batch; the prefill rows take the
+    // row-block kernels.
+    const int dim_ = c.hidden / c.heads, group_ = c.heads / c.kv_heads;
+    const bool fast_rows = h->fast && h->kv.block_tokens == 16 && dim_ == 64 && group_ <= 4;
     struct Block { int first, rows, length; };
     std::vector<Block> blocks;
     bool decode = true;
-    for (int s = 0, first = 0; s < nseq; first += steps[s].count, ++s) {
+    for (int s = 0; s < nseq; ++s)
         if (steps[s].count != 1) decode = false;
+    for (int s = 0, first = 0; s < nseq; first += steps[s].count, ++s) {
+        if (fast_rows && steps[s].count == 1) continue;
         for (int i = 0; i < steps[s].count; i += block_rows) {
             const int rows_b = std::min(block_rows, steps[s].count - i);
             blocks.push_back({first + i, rows_b, steps[s].used + i + rows_b});
@@ -692,17 +701,17 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
     const size_t nblocks = blocks.size();
     const size_t table_pairs = h->pending_tables.size();
     const size_t copies = h->pending_copies.size();
-    // Fast-mode decode attention: work items (row, KV head, first token,
-    // tokens | split << 16) over each row's splits (fast_attention_split).
-    // The split depends on nothing but the row, so a row's result does not
-    // depend on the rest of the batch (steps that also prefill take the
-    // prefill attention for every row).
-    const int dim_ = c.hidden / c.heads, group_ = c.heads / c.kv_heads;
-    const bool fast_decode = h->fast && decode && h->kv.block_tokens == 16 && dim_ == 64 && group_ <= 4;
-    size_t fast_items = 0, fast_short = 0;
+    // Fast-mode decode attention of the one-token sequences: work items
+    // (row, KV head, first token, tokens | split << 16) over each row's
+    // splits (fast_attention_split); rows of up to 256 tokens as (row, KV
+    // head, tokens) items of the one-work-group kernel; the rows the merge
+    // kernel combines. The split depends on nothing but the row.
+    const bool fast_decode = fast_rows && decode;  // q|k|v with the RoPE epilogue
+    size_t fast_items = 0, fast_short = 0, fast_merge = 0;
     int max_splits = 0;
-    if (fast_decode)
+    if (fast_rows)
         for (int q = 0; q < nseq; ++q) {
+            if (steps[q].count != 1) continue;
             const int length = steps[q].used + 1, split = mphip::fast_attention_split(length);
             const int splits = (length + split - 1) / split;
             if (mphip::fast_attention_short(length)) {
@@ -710,14 +719,16 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
                 continue;
             }
             fast_items += (size_t)c.kv_heads * splits;
+            ++fast_merge;
             max_splits = std::max(max_splits, splits);
         }
+    const bool fast_any = fast_items + fast_short > 0;
     const size_t base_entries =
         3 * (size_t)R + 2 * (size_t)nseq + 2 * nblocks + 2 * items + 2 * table_pairs + 3 * copies;
     const size_t fast_at = (base_entries + 3) / 4 * 4;  // int4 items need 16-byte alignment
-    const size_t entries = fast_decode ? fast_at + 4 * fast_items + 4 * fast_short : base_entries;
+    const size_t entries = fast_any ? fast_at + 4 * fast_items + 4 * fast_short + fast_merge : base_entries;
     if ((status = ensure_call_buffers(h, entries))) return status;
-    if (fast_decode) {
+    if (fast_any) {
         // Partials of (row, KV head, split) at a fixed stride of max_splits.
         const size_t need = (size_t)R * c.kv_heads * max_splits * group_ * (64 + 2);
         if (need > h->fast_partial_floats) {
@@ -763,8 +774,8 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
         }
     }
     int32_t* const m_fast = m0 + fast_at;
-    if (fast_decode) {
-        // Decode: row q is sequence q's only row. Whole splits first, then
+    if (fast_any) {
+        // A one-token sequence q's row is m_last[q]. Whole splits first, then
         // each row's shorter last split (attention per layer: config 4 15.8-16.1
         // vs 17.2 us in row order, config 5B 80.1 vs 82.4, config 3 within
         // noise).
@@ -773,12 +784,12 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
             for (int q = 0; q < nseq; ++q) {
                 const int length = steps[q].used + 1, split = mphip::fast_attention_split(length);
                 const int splits = (length + split - 1) / split;
-                if (mphip::fast_attention_short(length)) continue;
+                if (steps[q].count != 1 || mphip::fast_attention_short(length)) continue;
                 for (int kvh = 0; kvh < c.kv_heads; ++kvh)
                     for (int sp = 0; sp < splits; ++sp) {
                         const int n = std::min(split, length - sp * split);
                         if ((n == split) != (pass == 0)) continue;
-                        m_fast[4 * f] = q;
+                        m_fast[4 * f] = m_last[q];
                         m_fast[4 * f + 1] = steps[q].table_slot * c.kv_heads + kvh;
                         m_fast[4 * f + 2] = sp * split;
                         m_fast[4 * f + 3] = n | (sp << 16);
@@ -786,15 +797,21 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
                     }
             }
         int32_t* const m_short = m_fast + 4 * fast_items;
-        size_t r = 0;
-        for (int q = 0; q < nseq; ++q)
-            if (mphip::fast_attention_short(steps[q].used + 1))
-                for (int kvh = 0; kvh < c.kv_heads; ++kvh, ++r) {
-                    m_short[4 * r] = q;
-                    m_short[4 * r + 1] = steps[q].table_slot * c.kv_heads + kvh;
-                    m_short[4 * r + 2] = steps[q].used + 1;
-                    m_short[4 * r + 3] = 0;
-                }
+        int32_t* const m_merge = m_short + 4 * fast_short;
+        size_t r = 0, mr = 0;
+        for (int q = 0; q < nseq; ++q) {
+            if (steps[q].count != 1) continue;
+            if (!mphip::fast_attention_short(steps[q].used + 1)) {
+                m_merge[mr++] = m_last[q];
+                continue;
+            }
+            for (int kvh = 0; kvh < c.kv_heads; ++kvh, ++r) {
+                m_short[4 * r] = m_last[q];
+                m_short[4 * r + 1] = steps[q].table_slot * c.kv_heads + kvh;
+                m_short[4 * r + 2] = steps[q].used + 1;
+                m_short[4 * r + 3] = 0;
+            }
+        }
     }
     status = check(h, hipMemcpyAsync(h->meta, m0, sizeof(int32_t) * entries, hipMemcpyHostToDevice, h->stream),
                    "upload input tokens");
@@ -922,6 +939,8 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
         fw.items_count = (int)fast_items;
         fw.short_items = h->meta + (m_fast - m0) + 4 * fast_items;
         fw.short_count = (int)fast_short;
+        fw.merge_rows = fw.short_items + 4 * fast_short;
+        fw.merge_count = (int)fast_merge;
         fw.max_splits = max_splits;
         fw.partial_out = h->fast_partials;
         fw.partial_ml = h->fast_partials + (size_t)R * c.kv_heads * max_splits * group_ * 64;
@@ -978,9 +997,14 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
                                                             h->ctx, hd, fw);
                     });
                 } else {
+                    // RoPE and the K/V append of every row, then the prefill
+                    // rows; the one-token rows after them.
                     e = mphip::launch_attention(s, h->qkv_out, qw, R, c.heads, c.kv_heads, dim, meta, kv, l, h->ctx, hd,
                                                 work, decode, mphip::RopeTables{h->cos_table, h->sin_table},
                                                 attention_events());
+                    if (e == hipSuccess && fast_any)
+                        e = mphip::launch_fast_attention(s, h->qkv_out, qw, R, c.heads, c.kv_heads, meta, kv, l,
+                                                         h->ctx, hd, fw);
                 }
             }
             if (e == hipSuccess) e = timed(P, [&] { return fast(mphip::kResidual, h->ctx, hd, h->o[l], nullptr, hd, h->x, nullptr); });

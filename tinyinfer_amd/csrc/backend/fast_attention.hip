@@ -294,9 +294,10 @@ __global__ __launch_bounds__(kSplitPages * 64) void fast_attention_short_kernel(
     out[quad_index(row, (kvh * G + h) * kDim + lane, ldo)] = num / den;
 }
 
-// out[row][h*64 + d] for rows of more than one split: the splits of
-// (row, h/G) combined. One wavefront per (row, head), as four groups of 16
-// lanes: lane 16g + c holds dims 4c..4c+3, and group g takes splits g,
+// out[row][h*64 + d] for the listed rows (w.merge_rows: one-token rows of
+// more than 256 tokens): the splits of (row, h/G) combined. One wavefront
+// per (row, head), as four groups of 16 lanes: lane 16g + c holds dims
+// 4c..4c+3, and group g takes splits g,
 // g+4, g+8, ... with its own running maximum, denominator and weighted sum,
 // kMergeHeld splits' partials loaded per round (a row of up to 64 splits
 // takes one round of loads, a 16k-token row of 128 splits two). The four
@@ -304,13 +305,13 @@ __global__ __launch_bounds__(kSplitPages * 64) void fast_attention_short_kernel(
 // (g0 + g1) + (g2 + g3). The order depends on nothing but the row's split
 // count. The partials sit at a fixed stride per (row, KV head), so the
 // first round is issued together with the load of the row's position.
-__global__ __launch_bounds__(256) void fast_attention_merge_kernel(int rows, int heads, int kv_heads, RowMeta meta,
+__global__ __launch_bounds__(256) void fast_attention_merge_kernel(int heads, int kv_heads, RowMeta meta,
                                                                    FastAttentionWork w, float* __restrict__ out,
                                                                    int ldo) {
     const int lane = threadIdx.x & 63;
     const int pair = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (pair >= rows * heads) return;
-    const int row = pair / heads, h = pair % heads;
+    if (pair >= w.merge_count * heads) return;
+    const int row = w.merge_rows[pair / heads], h = pair % heads;
     const int G = heads / kv_heads, kvh = h / G, hg = h % G;
     const int grp = lane >> 4, c = lane & 15;
     const size_t slot0 = ((size_t)row * kv_heads + kvh) * w.max_splits;  // split 0 of (row, kvh)
@@ -408,8 +409,8 @@ hipError_t launch_fast_attention(hipStream_t s, const float* qkv, int ldq, int r
     default: launch_items<4>(s, qkv, ldq, meta, kv, layer, w, out, ldo); break;
     }
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess || w.items_count <= 0) return e;
-    fast_attention_merge_kernel<<<(rows * heads + 3) / 4, 256, 0, s>>>(rows, heads, kv_heads, meta, w, out, ldo);
+    if (e != hipSuccess || w.items_count <= 0 || w.merge_count <= 0) return e;
+    fast_attention_merge_kernel<<<(w.merge_count * heads + 3) / 4, 256, 0, s>>>(heads, kv_heads, meta, w, out, ldo);
     return hipGetLastError();
 }
 

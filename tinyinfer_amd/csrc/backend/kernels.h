@@ -143,8 +143,8 @@ hipError_t launch_fast_ssq(hipStream_t s, const float* x, int rows, int width, f
 // for rows of up to 256 tokens the row in (at most) 8 splits of whole
 // pages, so that a short row is still spread over several wavefronts (a
 // small batch of short rows is bound by one wavefront's chain of pages). A
-// function of the row alone: in a decode step a row's result does not
-// depend on the rest of the batch.
+// function of the row alone: a decoding row's result does not depend on
+// the rest of the batch.
 __host__ __device__ inline int fast_attention_split(int length) {
     const int pages = (length + 15) / 16;
     return pages <= 16 ? 16 * ((pages + 7) / 8) : 128;
@@ -162,6 +162,10 @@ struct FastAttentionWork {
     // kv_heads + KV head, tokens, 0
     const int32_t* short_items;
     int short_count;
+    // the rows whose splits the merge kernel combines (the one-token rows
+    // longer than 256 tokens)
+    const int32_t* merge_rows;
+    int merge_count;
     // Splits of the longest row (of those longer than 256 tokens; 0 if
     // none); the partial results of (row, KV head,
     // split) sit at slot (row * kv_heads + KV head) * max_splits + split.
