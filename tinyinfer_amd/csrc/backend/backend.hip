@@ -680,7 +680,8 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
     // head): every one-token sequence takes the decode attention kernels,
     // also in a step that prefills others, so a decoding row's result does
     // not depend on the rest of the batch; the prefill rows take the
-    // row-block kernels.
+    // matrix-core prefill kernel (fast_prefill.hip). The row-block kernels
+    // serve the exact mode.
     const int dim_ = c.hidden / c.heads, group_ = c.heads / c.kv_heads;
     const bool fast_rows = h->fast && h->kv.block_tokens == 16 && dim_ == 64 && group_ <= 4;
     struct Block { int first, rows, length; };
@@ -689,7 +690,7 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
     for (int s = 0; s < nseq; ++s)
         if (steps[s].count != 1) decode = false;
     for (int s = 0, first = 0; s < nseq; first += steps[s].count, ++s) {
-        if (fast_rows && steps[s].count == 1) continue;
+        if (fast_rows) continue;
         for (int i = 0; i < steps[s].count; i += block_rows) {
             const int rows_b = std::min(block_rows, steps[s].count - i);
             blocks.push_back({first + i, rows_b, steps[s].used + i + rows_b});
@@ -707,11 +708,14 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
     // head, tokens) items of the one-work-group kernel; the rows the merge
     // kernel combines. The split depends on nothing but the row.
     const bool fast_decode = fast_rows && decode;  // q|k|v with the RoPE epilogue
-    size_t fast_items = 0, fast_short = 0, fast_merge = 0;
+    size_t fast_items = 0, fast_short = 0, fast_merge = 0, fast_pre = 0;
     int max_splits = 0;
     if (fast_rows)
         for (int q = 0; q < nseq; ++q) {
-            if (steps[q].count != 1) continue;
+            if (steps[q].count != 1) {
+                fast_pre += (size_t)(steps[q].count + 15) / 16 * c.kv_heads;  // 16-row blocks x KV heads
+                continue;
+            }
             const int length = steps[q].used + 1, split = mphip::fast_attention_split(length);
             const int splits = (length + split - 1) / split;
             if (mphip::fast_attention_short(length)) {
@@ -722,11 +726,12 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
             ++fast_merge;
             max_splits = std::max(max_splits, splits);
         }
-    const bool fast_any = fast_items + fast_short > 0;
+    const bool fast_any = fast_items + fast_short + fast_pre > 0;
     const size_t base_entries =
         3 * (size_t)R + 2 * (size_t)nseq + 2 * nblocks + 2 * items + 2 * table_pairs + 3 * copies;
     const size_t fast_at = (base_entries + 3) / 4 * 4;  // int4 items need 16-byte alignment
-    const size_t entries = fast_any ? fast_at + 4 * fast_items + 4 * fast_short + fast_merge : base_entries;
+    const size_t pre_at = (fast_at + 4 * fast_items + 4 * fast_short + fast_merge + 3) / 4 * 4;
+    const size_t entries = fast_any ? pre_at + 4 * fast_pre : base_entries;
     if ((status = ensure_call_buffers(h, entries))) return status;
     if (fast_any) {
         // Partials of (row, KV head, split) at a fixed stride of max_splits.
@@ -811,6 +816,21 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
                 m_short[4 * r + 2] = steps[q].used + 1;
                 m_short[4 * r + 3] = 0;
             }
+        }
+        // Prefill: (first row, slot * kv_heads + KV head, position, rows) per
+        // 16-row block of each prefilling sequence and KV head.
+        int32_t* const m_pre = m0 + pre_at;
+        size_t pr = 0;
+        for (int q = 0; q < nseq; ++q) {
+            if (steps[q].count == 1) continue;
+            const int first = m_last[q] - steps[q].count + 1;
+            for (int b = 0; b < steps[q].count; b += 16)
+                for (int kvh = 0; kvh < c.kv_heads; ++kvh, ++pr) {
+                    m_pre[4 * pr] = first + b;
+                    m_pre[4 * pr + 1] = steps[q].table_slot * c.kv_heads + kvh;
+                    m_pre[4 * pr + 2] = steps[q].used + b;
+                    m_pre[4 * pr + 3] = std::min(16, steps[q].count - b);
+                }
         }
     }
     status = check(h, hipMemcpyAsync(h->meta, m0, sizeof(int32_t) * entries, hipMemcpyHostToDevice, h->stream),
@@ -996,15 +1016,21 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
                         return mphip::launch_fast_attention(s, h->qkv_out, qw, R, c.heads, c.kv_heads, meta, kv, l,
                                                             h->ctx, hd, fw);
                     });
-                } else {
+                } else if (fast_rows) {
                     // RoPE and the K/V append of every row, then the prefill
                     // rows; the one-token rows after them.
+                    e = mphip::launch_rope_append(s, h->qkv_out, qw, R, c.heads, c.kv_heads, dim, h->cos_table,
+                                                  h->sin_table, meta, kv, l);
+                    if (e == hipSuccess)
+                        e = mphip::launch_fast_prefill(s, h->qkv_out, qw, c.heads, c.kv_heads, kv, l,
+                                                       h->meta + pre_at, (int)fast_pre, h->ctx, hd);
+                    if (e == hipSuccess && fast_items + fast_short > 0)
+                        e = mphip::launch_fast_attention(s, h->qkv_out, qw, R, c.heads, c.kv_heads, meta, kv, l,
+                                                         h->ctx, hd, fw);
+                } else {
                     e = mphip::launch_attention(s, h->qkv_out, qw, R, c.heads, c.kv_heads, dim, meta, kv, l, h->ctx, hd,
                                                 work, decode, mphip::RopeTables{h->cos_table, h->sin_table},
                                                 attention_events());
-                    if (e == hipSuccess && fast_any)
-                        e = mphip::launch_fast_attention(s, h->qkv_out, qw, R, c.heads, c.kv_heads, meta, kv, l,
-                                                         h->ctx, hd, fw);
                 }
             }
             if (e == hipSuccess) e = timed(P, [&] { return fast(mphip::kResidual, h->ctx, hd, h->o[l], nullptr, hd, h->x, nullptr); });

@@ -181,6 +181,13 @@ struct FastAttentionWork {
     const float* prefetch[kPrefetchRanges];
     uint64_t prefetch_bytes[kPrefetchRanges];
 };
+// Prefill attention of the fast mode: work items (int4) of up to 16
+// consecutive rows of one sequence's chunk and one KV head: first row,
+// table slot * kv_heads + KV head, position of the first row, rows. The
+// rows' K/V must already be in the pools (launch_rope_append).
+bool fast_prefill_fits(int heads, int kv_heads, const PagedKv& kv);
+hipError_t launch_fast_prefill(hipStream_t s, const float* qkv, int ldq, int heads, int kv_heads, const PagedKv& kv,
+                               int layer, const int32_t* items, int count, float* out, int ldo);
 hipError_t launch_fast_attention(hipStream_t s, const float* qkv, int ldq, int rows, int heads, int kv_heads,
                                  const RowMeta& meta, const PagedKv& kv, int layer, float* out, int ldo,
                                  const FastAttentionWork& work);
