@@ -48,13 +48,15 @@ enum {
  * - MP_ARITHMETIC_EXACT: every sum in the reference CPU path's order
  *   (sequential k, separate multiply and add, two-pass softmax): logits
  *   bit-identical to miniprefix/src/backend/cpu/llama_runner.cpp:60-104;
- * - MP_ARITHMETIC_FAST: projections and the LM head on FP32 matrix cores and
- *   decode attention split over the context (flash-decoding), in their own
- *   summation order: logits within 1e-3 relative and decode attention within
- *   1e-4 absolute of the reference, greedy tokens checked against it.
- *   Prefill attention keeps the exact kernels. Needs hidden, intermediate,
- *   q+2*kv width and vocabulary multiples of 16, else the context computes
- *   exactly. */
+ * - MP_ARITHMETIC_FAST: projections and the LM head on FP32 matrix cores,
+ *   decode attention split over the context (flash-decoding) and prefill
+ *   attention on the matrix cores (flash attention), in their own summation
+ *   order: logits within 1e-3 relative and decode attention within 1e-4
+ *   absolute of the reference, greedy tokens checked against it. The
+ *   attention paths need 16-token pages, 64-wide heads and at most 4 query
+ *   heads per KV head (else they run the exact kernels). Needs hidden,
+ *   intermediate, q+2*kv width and vocabulary multiples of 16, else the
+ *   context computes exactly. */
 enum { MP_ARITHMETIC_EXACT = 0, MP_ARITHMETIC_FAST = 1 };
 
 /* Model shape; same fields and limits as ModelConfig (model.h:9-16,
