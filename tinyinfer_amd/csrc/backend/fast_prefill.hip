@@ -8,8 +8,12 @@
 // here, and a row's result depends only on the row (its query and keys),
 // not on the block, the chunking or the batch.
 //
-// One wavefront per work item (first row, table slot * kv_heads + KV head,
-// position of the first row, rows). MFMA operand layout (gfx950): lane l
+// One work-group per work item (first row, table slot * kv_heads + KV head,
+// position of the first row, rows): wavefront w of W walks pages w, w + W,
+// ... with its own running maxima and sums, and wavefront 0
+// combines the W results in order through LDS. The page-to-wavefront map
+// depends only on the page, so the order of the sums is a function of the
+// row. Per wavefront and page, with the MFMA operand layout (gfx950): lane l
 // supplies A[l%16][l/16] and B[l/16][l%16]; result register i of lane l is
 // D[4(l/16)+i][l%16]. With c = l%16 and g = l/16:
 //  - scores S = Q K^T, 16 MFMAs per head over the 64 dims: lane (c, g)
@@ -38,7 +42,10 @@ namespace {
 
 constexpr int kDim = 64;
 constexpr int kPage = 16;
-constexpr int kWavesPerGroup = 4;
+// Wavefronts per work item, each over every fourth page: one per SIMD. Eight
+// (two per SIMD, for G <= 3) took 4% less time on 16384-token prompts but 25%
+// more on prompts of 256 to 2048 tokens, whose wavefronts then hold few pages.
+constexpr int kWaves = 4;
 constexpr float kScale = 0.125f;  // 1/sqrt(64)
 
 typedef float f4 __attribute__((ext_vector_type(4)));
@@ -49,16 +56,20 @@ __device__ __forceinline__ float row16_max(float v) {
     return row_quads_max(v);
 }
 
-template <int G>
-__global__ __launch_bounds__(kWavesPerGroup * 64) void fast_prefill_kernel(const float* __restrict__ qkv, int ldq,
+template <int G, int W = kWaves>
+__global__ __launch_bounds__(W * 64) void fast_prefill_kernel(const float* __restrict__ qkv, int ldq,
                                                                             PagedKv kv, int layer,
                                                                             const int4* __restrict__ items, int count,
                                                                             int kv_heads, float* __restrict__ out,
                                                                             int ldo) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    __shared__ float p_s[kWavesPerGroup][G][kPage][kPage + 1];
-    const int index = blockIdx.x * kWavesPerGroup + wave;
+    __shared__ float p_s[W][G][kPage][kPage + 1];
+    // The other wavefronts' results, combined by wavefront 0: output tiles
+    // (per lane, as held) and per row the running maximum and denominator.
+    __shared__ f4 o_s[W - 1][G][4][64];
+    __shared__ float ml_s[W][G][kPage][2];
+    const int index = blockIdx.x;  // one work item per work-group (uniform)
     if (index >= count) return;
     const int4 item = items[index];
     const int row0 = item.x, kvh = item.y % kv_heads, pos0 = item.z, nrows = item.w;
@@ -87,7 +98,8 @@ __global__ __launch_bounds__(kWavesPerGroup * 64) void fast_prefill_kernel(const
             ls[h][i] = 0.0f;
         }
     const size_t head_base = (size_t)kvh * kPage * kDim;
-    for (int p = 0; p < pages; ++p) {
+    // Page p goes to wavefront p % W, whatever the block.
+    for (int p = wave; p < pages; p += W) {
         const size_t base = kv_page_base(table[p], layer, kv.layers, kPage, kv.kv_width) + head_base;
         const float* kp = kv.keys + base;
         const float* vp = kv.values + base;
@@ -116,9 +128,13 @@ __global__ __launch_bounds__(kWavesPerGroup * 64) void fast_prefill_kernel(const
             for (int i = 0; i < 4; ++i) {
                 const int qpos = min(pos0 + 4 * g + i, last);
                 const float si = key <= qpos ? s[i] : -__builtin_inff();
-                const float m_new = fmaxf(mx[h][i], row16_max(si));  // finite: key 0 is never masked
-                const float keep = __expf(mx[h][i] - m_new);
-                const float pv = __expf(si - m_new);
+                // A row may have no unmasked key yet in this wavefront's pages
+                // (a position below its first page): its maximum stays -inf
+                // and its sums 0.
+                const float m_new = fmaxf(mx[h][i], row16_max(si));
+                const bool any = m_new != -__builtin_inff();
+                const float keep = any ? __expf(mx[h][i] - m_new) : 1.0f;
+                const float pv = any ? __expf(si - m_new) : 0.0f;
                 ls[h][i] = ls[h][i] * keep + pv;
                 o[h][0][i] *= keep;
                 o[h][1][i] *= keep;
@@ -140,17 +156,47 @@ __global__ __launch_bounds__(kWavesPerGroup * 64) void fast_prefill_kernel(const
         __builtin_amdgcn_wave_barrier();
     }
     // Each row's denominator: the sum of its 16 lanes' shares (lane group g
-    // holds rows 4g..4g+3), then the output of the block's rows.
+    // holds rows 4g..4g+3). A wavefront without pages holds maximum -inf,
+    // sums 0 and outputs 0, and takes no part below.
 #pragma unroll
     for (int h = 0; h < G; ++h)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const float l = row_sum(ls[h][i]);
-            const int r = 4 * g + i;
-            if (r < nrows)
+            if (c == 0) {
+                ml_s[wave][h][4 * g + i][0] = mx[h][i];
+                ml_s[wave][h][4 * g + i][1] = l;
+            }
+        }
+    if (wave > 0)
 #pragma unroll
-                for (int n = 0; n < 4; ++n)
-                    out[quad_index(row0 + r, (kvh * G + h) * kDim + 16 * n + c, ldo)] = o[h][n][i] / l;
+        for (int h = 0; h < G; ++h)
+#pragma unroll
+            for (int n = 0; n < 4; ++n) o_s[wave - 1][h][n][lane] = o[h][n];
+    __syncthreads();
+    if (wave != 0) return;
+    // Wavefront 0: the wavefronts' results in order, then the block's rows.
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int r = 4 * g + i;
+            float m = ml_s[0][h][r][0];
+#pragma unroll
+            for (int w = 1; w < W; ++w) m = fmaxf(m, ml_s[w][h][r][0]);  // finite: page 0 is wave 0's
+            float f[W], l = 0.0f;
+#pragma unroll
+            for (int w = 0; w < W; ++w) {
+                f[w] = __expf(ml_s[w][h][r][0] - m);
+                l += ml_s[w][h][r][1] * f[w];
+            }
+#pragma unroll
+            for (int n = 0; n < 4; ++n) {
+                float v = o[h][n][i] * f[0];
+#pragma unroll
+                for (int w = 1; w < W; ++w) v += o_s[w - 1][h][n][lane][i] * f[w];
+                if (r < nrows) out[quad_index(row0 + r, (kvh * G + h) * kDim + 16 * n + c, ldo)] = v / l;
+            }
         }
 }
 
@@ -165,13 +211,13 @@ hipError_t launch_fast_prefill(hipStream_t s, const float* qkv, int ldq, int hea
                                int layer, const int32_t* items, int count, float* out, int ldo) {
     if (count <= 0) return hipSuccess;
     if (!fast_prefill_fits(heads, kv_heads, kv)) return hipErrorInvalidValue;
-    const dim3 grid((count + kWavesPerGroup - 1) / kWavesPerGroup);
+    const dim3 grid(count);
     const int4* it = reinterpret_cast<const int4*>(items);
     switch (heads / kv_heads) {
-    case 1: fast_prefill_kernel<1><<<grid, kWavesPerGroup * 64, 0, s>>>(qkv, ldq, kv, layer, it, count, kv_heads, out, ldo); break;
-    case 2: fast_prefill_kernel<2><<<grid, kWavesPerGroup * 64, 0, s>>>(qkv, ldq, kv, layer, it, count, kv_heads, out, ldo); break;
-    case 3: fast_prefill_kernel<3><<<grid, kWavesPerGroup * 64, 0, s>>>(qkv, ldq, kv, layer, it, count, kv_heads, out, ldo); break;
-    default: fast_prefill_kernel<4><<<grid, kWavesPerGroup * 64, 0, s>>>(qkv, ldq, kv, layer, it, count, kv_heads, out, ldo); break;
+    case 1: fast_prefill_kernel<1><<<grid, kWaves * 64, 0, s>>>(qkv, ldq, kv, layer, it, count, kv_heads, out, ldo); break;
+    case 2: fast_prefill_kernel<2><<<grid, kWaves * 64, 0, s>>>(qkv, ldq, kv, layer, it, count, kv_heads, out, ldo); break;
+    case 3: fast_prefill_kernel<3><<<grid, kWaves * 64, 0, s>>>(qkv, ldq, kv, layer, it, count, kv_heads, out, ldo); break;
+    default: fast_prefill_kernel<4><<<grid, kWaves * 64, 0, s>>>(qkv, ldq, kv, layer, it, count, kv_heads, out, ldo); break;
     }
     return hipGetLastError();
 }
