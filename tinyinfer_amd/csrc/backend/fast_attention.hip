@@ -37,6 +37,8 @@
 // completion and an atomic round trip at its end, more than the extra
 // launch; with a device-scope release fence it would also write back the
 // whole L2 on this chip.)
+#include <algorithm>
+
 #include "kernels.h"
 #include "lanes.h"
 #include "layout.h"
@@ -59,6 +61,19 @@ constexpr int kMergeHeld = 16;  // splits per lane group whose partials the merg
 constexpr float kScale = 0.125f;  // 1/sqrt(64)
 constexpr float kRescale = 16.0f;  // probabilities stay below e^16 before a rescale
 
+
+// Slice `touch` (8 KB) of the weights to prefetch: lane i reads one dword
+// of line i (128 bytes) of the slice; slices past the ranges read nothing.
+__device__ __forceinline__ float touch_weights(const FastAttentionWork& w, uint64_t touch, int lane) {
+    uint64_t at = (touch * 64 + lane) * 128;
+    const char* line = nullptr;
+#pragma unroll
+    for (int r = 0; r < FastAttentionWork::kPrefetchRanges; ++r) {
+        if (!line && at < w.prefetch_bytes[r]) line = reinterpret_cast<const char*>(w.prefetch[r]) + at;
+        if (!line) at -= w.prefetch_bytes[r];
+    }
+    return line ? *reinterpret_cast<const float*>(line) : 0.0f;
+}
 
 // One split: tokens t0..t0+n-1 (t0 page-aligned, at most kSplitPages pages)
 // of the row whose page table is `table`, for the G query heads of KV head
@@ -101,19 +116,7 @@ __device__ __forceinline__ void attend_split(const float* __restrict__ qkv, int 
             q[h][j] = *reinterpret_cast<const f4*>(qkv + quad_index(row, c, ldq));
         }
     __builtin_amdgcn_sched_barrier(0);
-    // This wavefront's 8 KB of the weights to prefetch: lane i touches line
-    // i (128 bytes) of the slice.
-    float touched = 0.0f;
-    {
-        uint64_t at = (touch * 64 + lane) * 128;
-        const char* line = nullptr;
-#pragma unroll
-        for (int r = 0; r < FastAttentionWork::kPrefetchRanges; ++r) {
-            if (!line && at < w.prefetch_bytes[r]) line = reinterpret_cast<const char*>(w.prefetch[r]) + at;
-            if (!line) at -= w.prefetch_bytes[r];
-        }
-        if (line) touched = *reinterpret_cast<const float*>(line);
-    }
+    const float touched = touch_weights(w, touch, lane);
 #pragma unroll
     for (int k = 0; k < kRing; ++k) load(k, kb[k], vb[k]);
     // Keep the loads where they are: the scheduler would otherwise sink
@@ -251,6 +254,13 @@ __global__ __launch_bounds__(kSplitPages * 64) void fast_attention_short_kernel(
     __shared__ float p_s[kSplitPages][G][kPage];
     __shared__ float part_ml[kSplitPages][G][2];
     __shared__ float part_acc[kSplitPages][G][kDim];
+    if (blockIdx.x >= w.short_count) {
+        // A work-group past the items (small batches, whose items leave
+        // most CUs idle) only touches its slices of the weights to prefetch.
+        const float touched = touch_weights(w, (uint64_t)blockIdx.x * kSplitPages + wave, lane);
+        asm volatile("" ::"v"(touched));
+        return;
+    }
     // (row, slot * kv_heads + KV head, tokens): the length rides in the item,
     // one dependent load fewer before the pages.
     const int4 item = reinterpret_cast<const int4*>(w.short_items)[blockIdx.x];
@@ -383,9 +393,18 @@ __global__ __launch_bounds__(256) void fast_attention_merge_kernel(int heads, in
 template <int G>
 void launch_items(hipStream_t s, const float* qkv, int ldq, const RowMeta& meta, const PagedKv& kv, int layer,
                   const FastAttentionWork& w, float* out, int ldo) {
-    if (w.short_count > 0)
-        fast_attention_short_kernel<G><<<w.short_count, kSplitPages * 64, 0, s>>>(qkv, ldq, meta, kv, layer, w, out,
-                                                                                  ldo);
+    if (w.short_count > 0) {
+        // Without split items (whose wavefronts touch the whole prefetch at
+        // 8 KB each), enough work-groups for every slice of it.
+        int groups = w.short_count;
+        if (w.items_count <= 0) {
+            uint64_t bytes = 0;
+            for (int r = 0; r < FastAttentionWork::kPrefetchRanges; ++r) bytes += w.prefetch_bytes[r];
+            const uint64_t per_group = (uint64_t)kSplitPages * 64 * 128;
+            groups = (int)std::max<uint64_t>((uint64_t)groups, (bytes + per_group - 1) / per_group);
+        }
+        fast_attention_short_kernel<G><<<groups, kSplitPages * 64, 0, s>>>(qkv, ldq, meta, kv, layer, w, out, ldo);
+    }
     if (w.items_count > 0)
         fast_attention_kernel<G><<<(w.items_count + kItemsPerGroup - 1) / kItemsPerGroup, kItemsPerGroup * 64, 0,
                                    s>>>(qkv, ldq, meta, kv, layer, w, out, ldo);
