@@ -328,6 +328,18 @@ def roofline(kind: str, g: dict, rec: dict | None):
                      "frac": round(p["tflops"] / FP32_MATRIX_PEAK_TFLOPS, 4), "flops_per_launch": int(p["flops"])}}
 
 
+def decode_dispatches(rows: list, steps: int, path: str) -> range:
+    """Dispatch ids of the last `steps` engine steps of a rocprofv3 --pmc
+    run of this script (each step ends with the LM head's argmax kernel; the
+    pure decode steps, warmup and timed, run last). Counting by step, not by
+    kernel name or grid, keeps out the prefill steps, which run the same
+    instantiations for their one-token rows and short chunks."""
+    ends = sorted({int(r["Dispatch_Id"]) for r in rows if "head_argmax_kernel" in r["Kernel_Name"]})
+    if len(ends) < steps + 1:
+        raise SystemExit(f"{path}: {len(ends) - 1} complete steps, {steps} asked for")
+    return range(ends[-steps - 1] + 1, ends[-1] + 1)
+
+
 def summarise_counters(fetch_csv: str, write_csv: str, bench_json: str, out: str):
     """Per-launch HBM bytes of the decode attention and projections from two
     rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE; KiB per dispatch) of
@@ -342,19 +354,18 @@ def summarise_counters(fetch_csv: str, write_csv: str, bench_json: str, out: str
                      "fast_gemm_kernel<2, true, false, 2, 1, 6>") if fast else ("gemm_column",))
 
     def read(path):
-        per = defaultdict(list)  # name -> [(grid, KiB)] in dispatch order
+        rows = list(csv.DictReader(open(path)))
+        window = decode_dispatches(rows, line["warmup"] + line["steps"], path)
+        per = defaultdict(list)  # name -> KiB per decode launch
         probe = []
-        for r in sorted(csv.DictReader(open(path)), key=lambda r: int(r["Dispatch_Id"])):
+        for r in rows:
             name = r["Kernel_Name"].replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0]
             kib = float(r["Counter_Value"])
             if name.startswith("__amd_rocclr_copyBuffer") and kib * 1024 > PROBE_BYTES / 4:
                 probe.append(kib)
-            per[name].append((int(r["Grid_Size"]), kib))
-        # The decode launches: a projection instantiation that the prefill's
-        # short chunks also run counts only at the grid of its last launch
-        # (the timed decode steps run last).
-        return {k: [kib for g, kib in v if g == v[-1][0] or not any(p in k for p in proj_kernels)]
-                for k, v in per.items()}, probe
+            elif int(r["Dispatch_Id"]) in window:
+                per[name].append(kib)
+        return per, probe
 
     result = {"workload": line["config"]["workload"], "seed": line["config"]["seed"],
               "arithmetic": line["config"].get("arithmetic"), "mean_context": line["config"]["mean_context"],
@@ -449,24 +460,28 @@ def summarise_sq(counter_csv: str, trace_csv: str, out: str, command: str):
     decode = ("fast_attention_kernel<", "fast_attention_merge_kernel", "fast_gemm_kernel<4, true, false, 1, 1, 12>",
               "fast_gemm_kernel<1, false, false, 1, 1, 12>", "fast_gemm_kernel<2, true, false, 2, 1, 6>",
               "fast_gemm_kernel<3, true, true, 4, 4, ")
-    # Grid (threads) of the B=64 decode launches of instantiations that
-    # prefill steps of up to 256 rows also run, on other shapes.
-    decode_grid = {"fast_gemm_kernel<4, true, false, 1, 1, 12>": 131072,
-                   "fast_gemm_kernel<1, false, false, 1, 1, 12>": 81920,
-                   "fast_gemm_kernel<2, true, false, 2, 1, 6>": 98304}
     pick = lambda n: next((k for k in decode if k in n), None)
+    # The pure decode steps only (warmup and timed, from the command line):
+    # prefill steps run the same instantiations on other shapes.
+    opt = lambda flag, default: int(command.split(flag)[1].split()[0]) if flag in command else default
+    counted = opt("--warmup", 4) + opt("--steps", 20)
+    rows = list(csv.DictReader(open(counter_csv)))
+    window = decode_dispatches(rows, counted, counter_csv)
     per, meta = defaultdict(dict), {}
-    for r in csv.DictReader(open(counter_csv)):
+    for r in rows:
         k = pick(clean(r["Kernel_Name"]))
-        if k is None or int(r["Grid_Size"]) != decode_grid.get(k, int(r["Grid_Size"])):
-            continue
         d = int(r["Dispatch_Id"])
+        if k is None or d not in window:
+            continue
         per[d][r["Counter_Name"]] = float(r["Counter_Value"])
         meta[d] = k
+    # Durations: every launch of the trace's last 24 decode steps.
+    trace = sorted(csv.DictReader(open(trace_csv)), key=lambda r: int(r["Start_Timestamp"]))
+    ends = [i for i, r in enumerate(trace) if "head_argmax_kernel" in r["Kernel_Name"]]
     durations = defaultdict(list)
-    for r in csv.DictReader(open(trace_csv)):
+    for r in trace[ends[-25] + 1 if len(ends) > 24 else 0:ends[-1] + 1]:
         k = pick(clean(r["Kernel_Name"]))
-        if k and int(r["Grid_Size_X"]) == decode_grid.get(k, int(r["Grid_Size_X"])):
+        if k:
             durations[k].append(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
     agg, n = defaultdict(lambda: defaultdict(float)), defaultdict(int)
     for d, c in per.items():
