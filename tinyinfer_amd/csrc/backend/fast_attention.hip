@@ -221,7 +221,13 @@ __global__ __launch_bounds__(kItemsPerGroup * 64) void fast_attention_kernel(con
     __shared__ float p_s[kItemsPerGroup][G][kPage];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int index = blockIdx.x * kItemsPerGroup + wave;
-    if (index >= w.items_count) return;
+    if (index >= w.items_count) {
+        // A wavefront past the items (batches with few splits) only touches
+        // its slice of the weights to prefetch.
+        const float touched = touch_weights(w, (uint64_t)index, lane);
+        asm volatile("" ::"v"(touched));
+        return;
+    }
     const int4 item = reinterpret_cast<const int4*>(w.items)[index];
     const int row = item.x, kvh = item.y % w.kv_heads, t0 = item.z, n = item.w & 0xFFFF, sp = item.w >> 16;
     const int32_t* table = kv.tables + (size_t)(item.y / w.kv_heads) * kv.table_stride;
@@ -393,21 +399,23 @@ __global__ __launch_bounds__(256) void fast_attention_merge_kernel(int heads, in
 template <int G>
 void launch_items(hipStream_t s, const float* qkv, int ldq, const RowMeta& meta, const PagedKv& kv, int layer,
                   const FastAttentionWork& w, float* out, int ldo) {
+    // Slices of 8 KB (one per wavefront) that cover the weights to prefetch.
+    uint64_t bytes = 0;
+    for (int r = 0; r < FastAttentionWork::kPrefetchRanges; ++r) bytes += w.prefetch_bytes[r];
+    const uint64_t slices = (bytes + 64 * 128 - 1) / (64 * 128);
     if (w.short_count > 0) {
-        // Without split items (whose wavefronts touch the whole prefetch at
-        // 8 KB each), enough work-groups for every slice of it.
+        // Without split items (whose launch covers the slices), enough
+        // work-groups for every slice.
         int groups = w.short_count;
-        if (w.items_count <= 0) {
-            uint64_t bytes = 0;
-            for (int r = 0; r < FastAttentionWork::kPrefetchRanges; ++r) bytes += w.prefetch_bytes[r];
-            const uint64_t per_group = (uint64_t)kSplitPages * 64 * 128;
-            groups = (int)std::max<uint64_t>((uint64_t)groups, (bytes + per_group - 1) / per_group);
-        }
+        if (w.items_count <= 0)
+            groups = (int)std::max<uint64_t>((uint64_t)groups, (slices + kSplitPages - 1) / kSplitPages);
         fast_attention_short_kernel<G><<<groups, kSplitPages * 64, 0, s>>>(qkv, ldq, meta, kv, layer, w, out, ldo);
     }
-    if (w.items_count > 0)
-        fast_attention_kernel<G><<<(w.items_count + kItemsPerGroup - 1) / kItemsPerGroup, kItemsPerGroup * 64, 0,
+    if (w.items_count > 0) {
+        const uint64_t waves = std::max<uint64_t>((uint64_t)w.items_count, slices);
+        fast_attention_kernel<G><<<(int)((waves + kItemsPerGroup - 1) / kItemsPerGroup), kItemsPerGroup * 64, 0,
                                    s>>>(qkv, ldq, meta, kv, layer, w, out, ldo);
+    }
 }
 
 }  // namespace

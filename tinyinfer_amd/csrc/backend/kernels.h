@@ -176,9 +176,9 @@ struct FastAttentionWork {
     // Weights the next projections read, touched by the attention's
     // wavefronts (one dword per 128-byte line, 8 KB per wavefront, results
     // unused) so that they are in the memory-side cache when those
-    // projections run: up to kPrefetchRanges ranges of `bytes` each. When
-    // every row takes the short-row kernel, that launch adds work-groups
-    // that only touch, enough for all of the ranges.
+    // projections run: up to kPrefetchRanges ranges of `bytes` each. A
+    // launch with fewer wavefronts than slices adds wavefronts that only
+    // touch, enough for all of the ranges.
     static constexpr int kPrefetchRanges = 6;
     const float* prefetch[kPrefetchRanges];
     uint64_t prefetch_bytes[kPrefetchRanges];
