@@ -2,7 +2,8 @@
 // paged pools. The reference computes each (row, head) with an explicit
 // two-pass softmax and sequential sums (llama_runner.cpp:85-93); here the
 // context is cut into page-aligned splits (fast_attention_split: 128
-// tokens; a row of up to 256 tokens in 8 splits), each split keeps
+// tokens, 256 in rows of more than 4,096; a row of up to 256 tokens in 8
+// splits), each split keeps
 // a running maximum, denominator and weighted sum per query head, and the
 // splits are combined at the end (the order of the floating-point sums
 // differs; the result matches the reference within 1e-4 absolute on the
@@ -12,7 +13,7 @@
 // One wavefront per work item (row, KV head, split: the item carries the
 // row's table slot beside the KV head), four items per work-group; the
 // wavefront serves the G query heads of the KV head, so each K and V byte
-// is read once. It walks the split's (up to 8) pages with two pages in
+// is read once. It walks the split's (up to 16) pages with two pages in
 // flight in a ring of registers: the loads of page k+2 are issued as soon
 // as page k has been used (with 2,000-3,000 wavefronts in flight a third
 // page only deepens the queues at HBM). Per page (16 tokens of one layer
@@ -54,7 +55,8 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 constexpr int kDim = 64;
 constexpr int kPage = 16;
 constexpr int kMaxGroup = 4;
-constexpr int kSplitPages = 8;
+constexpr int kSplitPages = 8;   // splits of a short row (wavefronts of its work-group)
+constexpr int kMaxPages = 16;    // pages of one split
 constexpr int kRing = 2;                           // pages in flight per wavefront
 constexpr int kItemsPerGroup = 4;
 constexpr int kMergeHeld = 16;  // splits per lane group whose partials the merge loads in one round
@@ -75,7 +77,7 @@ __device__ __forceinline__ float touch_weights(const FastAttentionWork& w, uint6
     return line ? *reinterpret_cast<const float*>(line) : 0.0f;
 }
 
-// One split: tokens t0..t0+n-1 (t0 page-aligned, at most kSplitPages pages)
+// One split: tokens t0..t0+n-1 (t0 page-aligned, at most kMaxPages pages)
 // of the row whose page table is `table`, for the G query heads of KV head
 // kvh. Gives per head the reference maximum m, the denominator l and lane
 // d's weighted sum acc (not yet divided). `touch` numbers this wavefront's
@@ -89,10 +91,10 @@ __device__ __forceinline__ void attend_split(const float* __restrict__ qkv, int 
     const int t = lane >> 2, dq = lane & 3;
     const int end = t0 + n;           // tokens t0..end-1 (t0 page-aligned)
     const int first = t0 / kPage;     // the split's first page
-    const int np = (end + kPage - 1) / kPage - first;  // 1..kSplitPages
-    int page_id[kSplitPages];
+    const int np = (end + kPage - 1) / kPage - first;  // 1..kMaxPages
+    int page_id[kMaxPages];
 #pragma unroll
-    for (int k = 0; k < kSplitPages; ++k) page_id[k] = table[first + min(k, np - 1)];
+    for (int k = 0; k < kMaxPages; ++k) page_id[k] = table[first + min(k, np - 1)];
     const size_t head_base = (size_t)kvh * kPage * kDim;  // floats into a page-layer span
     f4 kb[kRing][4], vb[kRing][4];
     auto load = [&](int k, f4 (&kk)[4], f4 (&vv)[4]) {
@@ -134,7 +136,7 @@ __device__ __forceinline__ void attend_split(const float* __restrict__ qkv, int 
         acc[h] = 0.0f;
     }
 #pragma unroll
-    for (int k = 0; k < kSplitPages; ++k) {
+    for (int k = 0; k < kMaxPages; ++k) {
         if (k > 0 && k >= np) break;  // np >= 1
         f4(&kc)[4] = kb[k % kRing];
         f4(&vc)[4] = vb[k % kRing];
@@ -203,7 +205,7 @@ __device__ __forceinline__ void attend_split(const float* __restrict__ qkv, int 
         }
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_sched_barrier(0);
-        if (k + kRing < kSplitPages) load(k + kRing, kb[k % kRing], vb[k % kRing]);
+        if (k + kRing < kMaxPages) load(k + kRing, kb[k % kRing], vb[k % kRing]);
         __builtin_amdgcn_sched_barrier(0);
     }
     asm volatile("" ::"v"(touched));  // the prefetch's value is not used
@@ -315,8 +317,8 @@ __global__ __launch_bounds__(kSplitPages * 64) void fast_attention_short_kernel(
 // per (row, head), as four groups of 16 lanes: lane 16g + c holds dims
 // 4c..4c+3, and group g takes splits g,
 // g+4, g+8, ... with its own running maximum, denominator and weighted sum,
-// kMergeHeld splits' partials loaded per round (a row of up to 64 splits
-// takes one round of loads, a 16k-token row of 128 splits two). The four
+// kMergeHeld splits' partials loaded per round (a row of up to 64 splits,
+// 16k tokens in 256-token splits, takes one round of loads). The four
 // groups are then rescaled to the common maximum and summed as
 // (g0 + g1) + (g2 + g3). The order depends on nothing but the row's split
 // count. The partials sit at a fixed stride per (row, KV head), so the

@@ -139,15 +139,17 @@ hipError_t launch_fast_ssq(hipStream_t s, const float* x, int rows, int width, f
 // denominator and output per query head; a merge kernel combines the splits
 // of every (row, head). Head dim 64, page 16.
 //
-// Tokens per split of a row of `length` tokens: 8 pages (128 tokens), and
-// for rows of up to 256 tokens the row in (at most) 8 splits of whole
-// pages, so that a short row is still spread over several wavefronts (a
-// small batch of short rows is bound by one wavefront's chain of pages). A
-// function of the row alone: a decoding row's result does not depend on
+// Tokens per split of a row of `length` tokens: 8 pages (128 tokens); 16
+// pages (256 tokens) for rows of more than 4,096 tokens, whose merge then
+// reads half as many partials (a 16k-token row: 64 splits, one round of
+// loads); and for rows of up to 256 tokens the row in (at most) 8 splits of
+// whole pages, so that a short row is still spread over several wavefronts
+// (a small batch of short rows is bound by one wavefront's chain of pages).
+// A function of the row alone: a decoding row's result does not depend on
 // the rest of the batch.
 __host__ __device__ inline int fast_attention_split(int length) {
     const int pages = (length + 15) / 16;
-    return pages <= 16 ? 16 * ((pages + 7) / 8) : 128;
+    return pages <= 16 ? 16 * ((pages + 7) / 8) : pages > 256 ? 256 : 128;
 }
 // Rows of up to 256 tokens (at most 8 splits) are combined inside one
 // work-group; longer rows through the partials and the merge kernel.
