@@ -1,8 +1,9 @@
 // Prefill attention of the fast arithmetic mode on FP32 matrix cores
 // (v_mfma_f32_16x16x4f32): for a block of up to 16 consecutive rows of one
 // sequence's chunk and one KV head, the G query heads' scores against each
-// 16-token page and the weighted sum of its values, with a running maximum
-// and denominator per row (flash attention). The reference computes each
+// 16-token page and the weighted sum of its values, with a reference maximum
+// (raised only when a score exceeds it by more than 16) and a denominator
+// per row (flash attention). The reference computes each
 // (row, head) with an explicit two-pass softmax and sequential sums
 // (llama_runner.cpp:85-93); the order of the floating-point sums differs
 // here, and a row's result depends only on the row (its query and keys),
@@ -47,6 +48,7 @@ constexpr int kPage = 16;
 // more on prompts of 256 to 2048 tokens, whose wavefronts then hold few pages.
 constexpr int kWaves = 4;
 constexpr float kScale = 0.125f;  // 1/sqrt(64)
+constexpr float kRescale = 16.0f;  // probabilities stay below e^16 before a rescale
 
 typedef float f4 __attribute__((ext_vector_type(4)));
 
@@ -124,23 +126,39 @@ __global__ __launch_bounds__(W * 64) void fast_prefill_kernel(const float* __res
             f4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int j = 0; j < 16; ++j) s = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[h][j], kb[j], s, 0, 0, 0);
+            // Per row a reference maximum, raised (and the sums rescaled)
+            // only when one of the row's scores exceeds it by more than
+            // kRescale, so the probabilities stay below e^16 and most pages
+            // need no row maximum at all. A row with no unmasked key yet in
+            // this wavefront's pages keeps maximum -inf and sums 0. Each
+            // row's raises depend on its own scores only.
+            float sv[4];
+            bool need = false;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int qpos = min(pos0 + 4 * g + i, last);
-                const float si = key <= qpos ? s[i] : -__builtin_inff();
-                // A row may have no unmasked key yet in this wavefront's pages
-                // (a position below its first page): its maximum stays -inf
-                // and its sums 0.
-                const float m_new = fmaxf(mx[h][i], row16_max(si));
-                const bool any = m_new != -__builtin_inff();
-                const float keep = any ? __expf(mx[h][i] - m_new) : 1.0f;
-                const float pv = any ? __expf(si - m_new) : 0.0f;
-                ls[h][i] = ls[h][i] * keep + pv;
-                o[h][0][i] *= keep;
-                o[h][1][i] *= keep;
-                o[h][2][i] *= keep;
-                o[h][3][i] *= keep;
-                mx[h][i] = m_new;
+                sv[i] = key <= qpos ? s[i] : -__builtin_inff();
+                need |= sv[i] > mx[h][i] + kRescale;
+            }
+            if (__builtin_amdgcn_ballot_w64(need)) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float pm = row16_max(sv[i]);
+                    if (pm > mx[h][i] + kRescale) {  // uniform in the row's lane group
+                        const float keep = __expf(mx[h][i] - pm);  // 0 from maximum -inf
+                        ls[h][i] *= keep;
+                        o[h][0][i] *= keep;
+                        o[h][1][i] *= keep;
+                        o[h][2][i] *= keep;
+                        o[h][3][i] *= keep;
+                        mx[h][i] = pm;
+                    }
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float pv = sv[i] != -__builtin_inff() ? __expf(sv[i] - mx[h][i]) : 0.0f;
+                ls[h][i] += pv;
                 p_s[wave][h][4 * g + i][c] = pv;
             }
         }
