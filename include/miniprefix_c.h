@@ -70,6 +70,18 @@ int mpx_runner_set_cost_timing(void* runner, int32_t enabled);
 /* Committed page table; MPX_LOGIC_ERROR if the runner does not expose it. */
 int mpx_runner_sequence(const void* runner, const char* id, int32_t* blocks, int32_t capacity, int32_t* count,
                         int32_t* used);
+/* Logit keeping, no counterpart in the reference (whose append returns the
+ * logits to its caller; the batched Engine step of this library downloads
+ * only the greedy argmax): while enabled, the last-row logits of every
+ * sequence a forward computes, per-request append or batched step, are kept
+ * on the host until that sequence's next forward, its next creation (a
+ * released sequence keeps them: the Engine releases a request in the step
+ * that emits its last token) or a clear.
+ * MPX_LOGIC_ERROR for a runner without it. mpx_runner_kept_logits copies up
+ * to `capacity` floats of sequence `id`'s kept logits into `logits` (may be
+ * NULL) and their count into `count`; MPX_OTHER when none are kept. */
+int mpx_runner_keep_logits(void* runner, int32_t enabled);
+int mpx_runner_kept_logits(const void* runner, const char* id, float* logits, size_t capacity, size_t* count);
 /* The runner's device context (an mp_hip*, include/mp_hip.h), or NULL for a
  * runner without one; for instrumentation such as mp_hip_set_timing. */
 void* mpx_runner_device(void* runner);

@@ -166,6 +166,26 @@ int mp_hip_paged_attention_decode(const float* q, const float* keys, const float
                                   int32_t layers, int32_t block_tokens, int32_t heads,
                                   int32_t kv_heads, int32_t dim, float* out, void* stream);
 
+/* The decode attention of the fast arithmetic (MP_ARITHMETIC_FAST): the
+ * kernels a fast-mode forward runs for its one-token rows, on caller-owned
+ * DEVICE buffers, for `rows` query rows at once (the attention of
+ * llama_runner.cpp:85-93 in the flash-decoding order: splits of
+ * 16-256 tokens, each with a running maximum, denominator and weighted sum,
+ * combined at the end; within 1e-4 absolute of the reference on its scale of
+ * inputs). q: [rows][heads*dim]; out: [rows][heads*dim]; row r attends
+ * lengths[r] tokens (host array) through its page table at
+ * tables + r*table_stride (device int32). The pools hold the forward's
+ * device page order (mp_hip_kv_pools; layout.h: per (block, layer) KV head
+ * major, K as [d/4][slot][4], V as [slot/4][d][4]), not the reference's
+ * [slot][kv_width]. Needs block_tokens 16, dim 64 and at most 4 query heads
+ * per KV head, else MP_INVALID_ARGUMENT (message:
+ * mp_hip_last_error(NULL)). Allocates its work lists and partials per call
+ * and is synchronous on `stream` (NULL: the null stream). */
+int mp_hip_paged_attention_decode_fast(const float* q, const float* keys, const float* values,
+                                       const int32_t* tables, int32_t table_stride, const int32_t* lengths,
+                                       int32_t rows, int32_t layer, int32_t layers, int32_t block_tokens,
+                                       int32_t heads, int32_t kv_heads, int32_t dim, float* out, void* stream);
+
 /* The same attention as mp_hip_paged_attention_decode with no allocation of
  * any kind: no counterpart in the reference; for callers that cannot
  * allocate (code under HIP graph capture, serving loops that forbid

@@ -162,4 +162,8 @@ bool sequence_of(const ModelRunner& runner, const std::string& id, std::vector<i
 
 void* device_of(ModelRunner&) { return nullptr; }
 
+bool keep_logits(ModelRunner&, bool) { return false; }
+
+bool kept_logits(const ModelRunner&, const std::string&, const std::vector<float>**) { return false; }
+
 }  // namespace mpx

@@ -55,17 +55,11 @@ STAND_IN = dict(layers=1, hidden=8, intermediate=8, heads=2, kv_heads=1, eos=0, 
 
 def rows_of(name: str, wl):
     """Requests whose token streams the fixture records."""
-    if name == "config3":
-        lengths = [len(r.prompt) for r in wl.requests]
-        picks = [int(np.argmin(lengths)), int(np.argmax(lengths)), 0, 1]
-        return sorted(set(picks))
     if name == "config4":
         return list(range(1, len(wl.requests)))  # every follower
     if name == "config5a":
         return [0]
-    if name == "config5b":
-        return [0, 1, 2, 3]
-    return list(range(len(wl.requests)))
+    return list(range(len(wl.requests)))  # every request
 
 
 def decode_steps(name: str, wl, index: int) -> int:

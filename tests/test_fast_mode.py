@@ -109,21 +109,24 @@ def test_fast_rows_do_not_depend_on_the_batch(torch_cuda):
 
 
 
-def attention_probe_model(context: int, seed: int) -> OracleModel:
-    """One layer whose logits follow the attention output: o_proj the
+def attention_probe_model(context: int, seed: int, layers: int = 1) -> OracleModel:
+    """Layers whose logits follow the attention output: o_proj the
     identity, the MLP zero, an embedding 1e-3 the attention's scale and an
     untied N(0, 1) head, so a logit's relative error is about the attention
-    output's (hidden 192: 3 query heads on 1 KV head of 64 dims)."""
+    output's (hidden 192: 3 query heads on 1 KV head of 64 dims). With two
+    layers, the second layer's keys and values carry the first layer's
+    attention output of every row."""
     o = Oracle()
     h, kv, inter, vocab = 192, 64, 64, 256
-    cfg = dict(layers=1, hidden=h, intermediate=inter, heads=3, kv_heads=1, vocabulary=vocab, context=context,
+    cfg = dict(layers=layers, hidden=h, intermediate=inter, heads=3, kv_heads=1, vocabulary=vocab, context=context,
                eos=0, rms_epsilon=1e-5, rope_theta=100000.0, tied=0)
     normal = lambda shape, std, stream: o.fill_normal(int(np.prod(shape)), seed, stream, std).reshape(shape)
-    layer = dict(input_norm=np.ones(h, np.float32), q=normal((h, h), 0.1, 1), k=normal((h, kv), 0.1, 2),
-                 v=normal((h, kv), 0.1, 3), o=np.eye(h, dtype=np.float32), post_norm=np.ones(h, np.float32),
-                 gate=np.zeros((h, inter), np.float32), up=np.zeros((h, inter), np.float32),
-                 down=np.zeros((inter, h), np.float32))
-    tensors = dict(layers=[layer], embedding=normal((vocab, h), 1e-3, 4), final_norm=np.ones(h, np.float32),
+    stack = [dict(input_norm=np.ones(h, np.float32), q=normal((h, h), 0.1, 1 + 10 * l),
+                  k=normal((h, kv), 0.1, 2 + 10 * l), v=normal((h, kv), 0.1, 3 + 10 * l),
+                  o=np.eye(h, dtype=np.float32), post_norm=np.ones(h, np.float32),
+                  gate=np.zeros((h, inter), np.float32), up=np.zeros((h, inter), np.float32),
+                  down=np.zeros((inter, h), np.float32)) for l in range(layers)]
+    tensors = dict(layers=stack, embedding=normal((vocab, h), 1e-3, 4), final_norm=np.ones(h, np.float32),
                    lm_head=normal((h, vocab), 1.0, 5))
     return OracleModel(cfg, tensors=tensors)
 
@@ -242,3 +245,50 @@ def test_fast_prefill_chunking_does_not_change_rows(torch_cuda):
     three = run([100, 7, 193])
     for a, b in zip(one, three):
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_fast_prefill_climbing_scores(torch_cuda):
+    """Prefill rows whose scores climb by far more than the softmax's
+    rescale margin of 16 across the pages a wavefront walks: 2,000 cached
+    tokens of seeded keys whose scale grows from 0.25 to 12 with the
+    position (scores from about +-0.3 to about +-20), then a prompt chunk of
+    100 tokens on the two-layer attention probe. Each chunk's last-row
+    logits are within 1e-3 relative of the oracle, and prefilling the 100
+    tokens in one chunk or in chunks of 30, 7 and 63 gives bit-identical
+    last-row logits."""
+    used, n, bt = 2000, 100, 16
+    model = attention_probe_model(4096, seed=67, layers=2)
+    cfg = model.config
+    o = Oracle()
+    max_blocks = (used + n + bt - 1) // bt + 8
+    table = o.permutation(max_blocks, 67, 9450)[: (used + n + bt - 1) // bt].copy()
+    size = pool_elements(cfg, bt, max_blocks)
+    keys = o.fill_normal(size, 67, 9451, 1.0).reshape(max_blocks, cfg["layers"], bt, 64)
+    values = o.fill_normal(size, 67, 9452, 1.0)
+    for t in range(used):  # the cached tokens' key scale grows with the position
+        keys[table[t // bt], :, t % bt, :] *= np.float32(0.25 + 11.75 * (t / used) ** 2)
+    keys = keys.reshape(-1)
+    prompt = [int(t) for t in o.fill_tokens(n, 67, 9453, cfg["vocabulary"])]
+
+    def run(chunks):
+        backend = HipBackend(cfg, block_tokens=bt, max_blocks=max_blocks, max_sequences=1,
+                             arithmetic=ARITHMETIC_FAST)
+        upload_model(backend, model)
+        backend.table_write(0, 0, table)
+        write_pools(backend, keys, values)
+        k, v = keys.copy(), values.copy()
+        at, outs = used, []
+        for c in chunks:
+            am, got = backend.forward([(0, at, c)], prompt[at - used: at - used + c])
+            want = model.append(k, v, bt, table, at, prompt[at - used: at - used + c])
+            err = rel_inf(got[0], want)
+            assert err <= 1e-3, f"chunk at {at} of {c} rows: relative error {err:.3e}"
+            assert am[0] == int(np.argmax(got[0]))
+            outs.append(got[0].copy())
+            at += c
+        backend.close()
+        return outs
+
+    one = run([n])
+    three = run([30, 7, 63])
+    assert np.array_equal(one[-1].view(np.uint32), three[-1].view(np.uint32))

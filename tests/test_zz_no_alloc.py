@@ -3,10 +3,13 @@ against mp_hip_paged_attention_decode, the entry point it shares its kernel
 with, and against the oracle.
 
 Two calls in a row on rows long enough that their scores leave LDS for the
-static device scratch, the second shorter than the first, so it runs over
-what the first left there. Outputs must be bit-identical to the allocating
-entry point's (and to the oracle's: the kernel keeps the reference CPU
-path's order). A row beyond the scratch is rejected before any launch."""
+static device scratch (a KV head's 3 query heads x round_up(length, 16) >
+kAttentionLdsScores = 10,240 floats), the second shorter than the first, so
+it runs over what the first left there; then a row of 100 tokens, whose
+scores stay in LDS although the entry point passes the scratch as well.
+Outputs must be bit-identical to the allocating entry point's (and to the
+oracle's: the kernel keeps the reference CPU path's order). A row beyond
+the scratch is rejected before any launch."""
 import math
 
 import numpy as np
@@ -34,7 +37,9 @@ def test_noalloc_matches_allocating_entry_point(torch_cuda):
     torch = torch_cuda
     o = Oracle()
     held = None
-    for seed, length in ((5, 6000), (6, 4000)):  # 3 heads x length > 10240: scores in the scratch
+    # 3 x round_up(length, 16) > 10240 for 6000 and 4000 (scores in the
+    # scratch), not for 100 (scores in LDS).
+    for seed, length in ((5, 6000), (6, 4000), (7, 100)):
         q, keys, values, table = _inputs(o, seed, length)
         dq, dk, dv, dt = (torch.from_numpy(a).cuda() for a in (q, keys, values, table))
         base = torch.empty(HEADS * DIM, dtype=torch.float32, device="cuda")

@@ -68,6 +68,8 @@ def _bind(lib):
     lib.mp_hip_copy_tail_timed.argtypes = [vp, ctypes.POINTER(TailRegion), ctypes.POINTER(ctypes.c_uint64)]
     lib.mp_hip_paged_attention_decode.argtypes = [vp, vp, vp, vp] + [ctypes.c_int32] * 7 + [vp, vp]
     lib.mp_hip_paged_attention_decode_noalloc.argtypes = [vp, vp, vp, vp] + [ctypes.c_int32] * 7 + [vp, vp]
+    lib.mp_hip_paged_attention_decode_fast.argtypes = [vp, vp, vp, vp, ctypes.c_int32, I32P] + \
+        [ctypes.c_int32] * 7 + [vp, vp]
     lib.mp_hip_sync.argtypes = [vp]
     lib.mp_hip_stats.argtypes = [vp, ctypes.POINTER(Counters)]
     lib.mp_hip_kv_pools.argtypes = [vp, ctypes.POINTER(vp), ctypes.POINTER(vp), ctypes.POINTER(ctypes.c_size_t)]
@@ -200,3 +202,16 @@ def paged_attention_decode_noalloc(q, keys, values, table, length: int, layer: i
     if status:
         message = (lib().mp_hip_last_error(None) or b"").decode()
         raise BackendError(status, f"mp_hip_paged_attention_decode_noalloc failed ({status}): {message}")
+
+
+def paged_attention_decode_fast(q, keys, values, tables, table_stride: int, lengths, layer: int, layers: int,
+                                heads: int, kv_heads: int, out, stream: int | None = None):
+    """The fast arithmetic's decode attention of len(lengths) rows over
+    device buffers (raw device pointers; pools in the device page order,
+    row r's table at tables + r * table_stride). Synchronous."""
+    n = np.ascontiguousarray(lengths, dtype=np.int32)
+    status = lib().mp_hip_paged_attention_decode_fast(q, keys, values, tables, table_stride, n.ctypes.data_as(I32P),
+                                                      n.size, layer, layers, 16, heads, kv_heads, 64, out, stream)
+    if status:
+        message = (lib().mp_hip_last_error(None) or b"").decode()
+        raise BackendError(status, f"mp_hip_paged_attention_decode_fast failed ({status}): {message}")

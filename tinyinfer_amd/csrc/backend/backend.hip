@@ -205,6 +205,14 @@ void rope_tables(const mp_model_desc& c, std::vector<float>& cs, std::vector<flo
         }
 }
 
+// The fast decode and prefill attention kernels serve the rows: fast
+// arithmetic, 16-token pages, 64-wide heads, at most 4 query heads per KV
+// head (else the exact kernels run).
+bool fast_attention_rows(const mp_hip* h) {
+    const mp_model_desc& c = h->model;
+    return h->fast && h->kv.block_tokens == 16 && c.hidden / c.heads == 64 && c.heads / c.kv_heads <= 4;
+}
+
 int score_stride(int max_length) { return (max_length + 15) & ~15; }
 int score_chunks(int max_length) { return (max_length + 255) / 256; }
 // Score rows and per-256-token chunk maxima of every (row, head).
@@ -212,9 +220,25 @@ size_t attention_scratch_floats(const mp_model_desc& c, int rows, int max_length
     return (size_t)rows * c.heads * ((size_t)score_stride(max_length) + score_chunks(max_length));
 }
 
+// Split partials of the fast decode attention for `seqs` sequences: per
+// (sequence, KV head) the most splits a row within the context limit has,
+// each G x 64 outputs + (maximum, denominator).
+size_t fast_partial_floats(const mp_hip* h, int seqs) {
+    const mp_model_desc& c = h->model;
+    return (size_t)seqs * c.kv_heads * mphip::fast_attention_max_splits(c.context) * (c.heads / c.kv_heads) *
+           (64 + 2);
+}
+
+// Grow-only workspace. Sized so that a decode never allocates once the
+// workspace has grown to its batch: the exact attention's score rows of a
+// call of up to 256 rows are sized for the context limit (a longer call's
+// for its longest row), the fast attention's split partials for the
+// context limit and the workspace's sequences.
 int ensure_workspace(mp_hip* h, int rows, int seqs, int max_length) {
     const mp_model_desc& c = h->model;
-    const size_t need_scratch = attention_scratch_floats(c, rows, max_length);
+    const bool exact_rows = !fast_attention_rows(h);
+    const size_t need_scratch =
+        exact_rows ? attention_scratch_floats(c, rows, rows <= 256 ? std::max(max_length, c.context) : max_length) : 0;
     if (rows <= h->workspace_rows && seqs <= h->workspace_seqs && need_scratch <= h->scratch_floats)
         return MP_OK;
     int status = stream_sync(h);
@@ -225,11 +249,11 @@ int ensure_workspace(mp_hip* h, int rows, int seqs, int max_length) {
     for (void* p : {(void*)h->x, (void*)h->xn, (void*)h->qkv_out, (void*)h->ctx, (void*)h->ffn,
                     (void*)h->last, (void*)h->logits, (void*)h->results,
                     (void*)h->best_value, (void*)h->best_index, (void*)h->best_bad, (void*)h->ssq,
-                    (void*)h->row_block, (void*)h->row_rope})
+                    (void*)h->row_block, (void*)h->row_rope, (void*)h->fast_partials})
         device_free(h, p);
     h->x = h->xn = h->qkv_out = h->ctx = h->ffn = h->last = h->logits = h->best_value = h->ssq = nullptr;
     h->results = h->best_index = h->best_bad = h->row_block = nullptr;
-    h->row_rope = nullptr;
+    h->row_rope = h->fast_partials = nullptr;
     h->workspace_rows = h->workspace_seqs = 0;
     const size_t hd = c.hidden;
     const size_t groups = h->fast ? std::max<size_t>(mphip::head_groups(c.vocabulary), c.vocabulary / 16)
@@ -250,6 +274,7 @@ int ensure_workspace(mp_hip* h, int rows, int seqs, int max_length) {
         {(void**)&h->ssq, h->fast ? sizeof(float) * R * (hd / 16) : 0},
         {(void**)&h->row_block, h->fast ? sizeof(int32_t) * R : 0},
         {(void**)&h->row_rope, h->fast ? sizeof(float) * R * (size_t)(hd / c.heads) : 0},
+        {(void**)&h->fast_partials, fast_attention_rows(h) ? sizeof(float) * fast_partial_floats(h, S) : 0},
     };
     size_t total = 0;
     for (const auto& it : items) {
@@ -276,6 +301,7 @@ int ensure_workspace(mp_hip* h, int rows, int seqs, int max_length) {
     }
     h->workspace_rows = R;
     h->workspace_seqs = S;
+    h->fast_partial_floats = fast_attention_rows(h) ? fast_partial_floats(h, S) : 0;
     h->stats.device_workspace_bytes = total + sizeof(float) * h->scratch_floats;
     return MP_OK;
 }
@@ -682,8 +708,8 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
     // not depend on the rest of the batch; the prefill rows take the
     // matrix-core prefill kernel (fast_prefill.hip). The row-block kernels
     // serve the exact mode.
-    const int dim_ = c.hidden / c.heads, group_ = c.heads / c.kv_heads;
-    const bool fast_rows = h->fast && h->kv.block_tokens == 16 && dim_ == 64 && group_ <= 4;
+    const int group_ = c.heads / c.kv_heads;
+    const bool fast_rows = fast_attention_rows(h);
     struct Block { int first, rows, length; };
     std::vector<Block> blocks;
     bool decode = true;
@@ -730,23 +756,21 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
     const size_t base_entries =
         3 * (size_t)R + 2 * (size_t)nseq + 2 * nblocks + 2 * items + 2 * table_pairs + 3 * copies;
     const size_t fast_at = (base_entries + 3) / 4 * 4;  // int4 items need 16-byte alignment
-    const size_t pre_at = (fast_at + 4 * fast_items + 4 * fast_short + fast_merge + 3) / 4 * 4;
+    const size_t pre_at = (fast_at + 4 * fast_items + 4 * fast_short + 2 * fast_merge + 3) / 4 * 4;
     const size_t entries = fast_any ? pre_at + 4 * fast_pre : base_entries;
-    if ((status = ensure_call_buffers(h, entries))) return status;
-    if (fast_any) {
-        // Partials of (row, KV head, split) at a fixed stride of max_splits.
-        const size_t need = (size_t)R * c.kv_heads * max_splits * group_ * (64 + 2);
-        if (need > h->fast_partial_floats) {
-            if ((status = stream_sync(h))) return status;
-            device_free(h, h->fast_partials);
-            h->fast_partials = nullptr;
-            h->fast_partial_floats = 0;
-            const size_t grow = need + need / 2;
-            if ((status = device_alloc(h, (void**)&h->fast_partials, sizeof(float) * grow, "allocate attention partials")))
-                return status;
-            h->fast_partial_floats = grow;
-        }
-    }
+    // The metadata buffers are sized for any call of this many rows and
+    // sequences within the context limit (plus a page-table entry per
+    // sequence), so a decode does not grow them.
+    const int split_stride = mphip::fast_attention_max_splits(c.context);
+    const size_t chunks_limit = (size_t)score_chunks(c.context);
+    const size_t bound = 3 * (size_t)R + 2 * (size_t)nseq + 2 * (size_t)R * (1 + chunks_limit) + 2 * (size_t)nseq +
+                         2 * table_pairs + 3 * copies + 8 +
+                         (fast_rows ? (size_t)nseq * c.kv_heads * (4 * (size_t)split_stride + 4) + 2 * (size_t)nseq +
+                                          4 * ((size_t)R / 16 + (size_t)nseq) * c.kv_heads
+                                    : 0);
+    if ((status = ensure_call_buffers(h, std::max(entries, bound)))) return status;
+    if (fast_any && (max_splits > split_stride || (size_t)nseq > (size_t)h->workspace_seqs))
+        return fail(h, MP_DEVICE_ERROR, "attention partials smaller than the call");
     int32_t* const m0 = h->host_meta;
     int32_t* m_tokens = m0;
     int32_t* m_seq = m_tokens + R;
@@ -796,8 +820,8 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
                         if ((n == split) != (pass == 0)) continue;
                         m_fast[4 * f] = m_last[q];
                         m_fast[4 * f + 1] = steps[q].table_slot * c.kv_heads + kvh;
-                        m_fast[4 * f + 2] = sp * split;
-                        m_fast[4 * f + 3] = n | (sp << 16);
+                        m_fast[4 * f + 2] = q;
+                        m_fast[4 * f + 3] = mphip::fast_attention_item_w(n, sp, split);
                         ++f;
                     }
             }
@@ -807,7 +831,9 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
         for (int q = 0; q < nseq; ++q) {
             if (steps[q].count != 1) continue;
             if (!mphip::fast_attention_short(steps[q].used + 1)) {
-                m_merge[mr++] = m_last[q];
+                m_merge[2 * mr] = m_last[q];
+                m_merge[2 * mr + 1] = q;
+                ++mr;
                 continue;
             }
             for (int kvh = 0; kvh < c.kv_heads; ++kvh, ++r) {
@@ -962,8 +988,9 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
         fw.merge_rows = fw.short_items + 4 * fast_short;
         fw.merge_count = (int)fast_merge;
         fw.max_splits = max_splits;
+        fw.split_stride = split_stride;
         fw.partial_out = h->fast_partials;
-        fw.partial_ml = h->fast_partials + (size_t)R * c.kv_heads * max_splits * group_ * 64;
+        fw.partial_ml = h->fast_partials + (size_t)h->workspace_seqs * c.kv_heads * split_stride * group_ * 64;
         fw.kv_heads = c.kv_heads;
         auto set_prefetch = [&](int l) {
             // This layer's remaining projections, then the next layer's q|k|v.
@@ -1160,6 +1187,101 @@ int mp_hip_paged_attention_decode(const float* q, const float* keys, const float
         (void)hipFree(scratch);
     }
     return e == hipSuccess ? MP_OK : MP_DEVICE_ERROR;
+}
+
+int mp_hip_paged_attention_decode_fast(const float* q, const float* keys, const float* values,
+                                       const int32_t* tables, int32_t table_stride, const int32_t* lengths,
+                                       int32_t rows, int32_t layer, int32_t layers, int32_t block_tokens,
+                                       int32_t heads, int32_t kv_heads, int32_t dim, float* out, void* stream) {
+    if (!q || !keys || !values || !tables || !lengths || !out || rows < 1 || table_stride < 1 || layer < 0 ||
+        layer >= layers || block_tokens != 16 || dim != 64 || heads < 1 || kv_heads < 1 || heads % kv_heads ||
+        heads / kv_heads > 4) {
+        mphip::set_free_error("invalid fast paged attention arguments (pages of 16 tokens, head dim 64 and at "
+                              "most 4 query heads per KV head)");
+        return MP_INVALID_ARGUMENT;
+    }
+    const int group = heads / kv_heads;
+    // Work lists as the forward builds them for one-token rows (row r is
+    // sequence r): rows of up to 256 tokens in one work-group each, longer
+    // rows as splits (whole splits first) merged afterwards.
+    std::vector<int32_t> split_items, short_items, merge_rows, positions(rows);
+    int max_splits = 0, longest = 1;
+    for (int r = 0; r < rows; ++r) {
+        const int length = lengths[r];
+        if (length < 1 || (length + 15) / 16 > table_stride) {
+            mphip::set_free_error("invalid fast paged attention row length");
+            return MP_INVALID_ARGUMENT;
+        }
+        positions[r] = length - 1;
+        longest = std::max(longest, length);
+        if (mphip::fast_attention_short(length)) {
+            for (int kvh = 0; kvh < kv_heads; ++kvh)
+                short_items.insert(short_items.end(), {r, r * kv_heads + kvh, length, 0});
+            continue;
+        }
+        const int split = mphip::fast_attention_split(length), splits = (length + split - 1) / split;
+        max_splits = std::max(max_splits, splits);
+        merge_rows.insert(merge_rows.end(), {r, r});
+    }
+    for (int pass = 0; pass < 2; ++pass)
+        for (int r = 0; r < rows; ++r) {
+            const int length = lengths[r];
+            if (mphip::fast_attention_short(length)) continue;
+            const int split = mphip::fast_attention_split(length), splits = (length + split - 1) / split;
+            for (int kvh = 0; kvh < kv_heads; ++kvh)
+                for (int sp = 0; sp < splits; ++sp) {
+                    const int n = std::min(split, length - sp * split);
+                    if ((n == split) != (pass == 0)) continue;
+                    split_items.insert(split_items.end(),
+                                       {r, r * kv_heads + kvh, r, mphip::fast_attention_item_w(n, sp, split)});
+                }
+        }
+    // One device buffer: the int32 lists (16-byte aligned), then the partials.
+    const size_t ints = split_items.size() + short_items.size() + merge_rows.size() + positions.size();
+    const size_t int_bytes = (ints * sizeof(int32_t) + 255) / 256 * 256;
+    const size_t partial_floats = (size_t)rows * kv_heads * max_splits * group * (64 + 2);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    char* buffer = nullptr;
+    hipError_t e = hipMalloc(&buffer, int_bytes + partial_floats * sizeof(float));
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        mphip::set_free_error(std::string("allocate fast attention work: ") + hipGetErrorString(e));
+        return e == hipErrorOutOfMemory ? MP_OUT_OF_MEMORY : MP_DEVICE_ERROR;
+    }
+    std::vector<int32_t> host;
+    host.reserve(ints);
+    for (const auto* part : {&split_items, &short_items, &merge_rows, &positions})
+        host.insert(host.end(), part->begin(), part->end());
+    int32_t* const dev = reinterpret_cast<int32_t*>(buffer);
+    e = hipMemcpyAsync(dev, host.data(), ints * sizeof(int32_t), hipMemcpyHostToDevice, s);
+    mphip::FastAttentionWork w{};
+    w.items = dev;
+    w.items_count = (int)(split_items.size() / 4);
+    w.short_items = dev + split_items.size();
+    w.short_count = (int)(short_items.size() / 4);
+    w.merge_rows = w.short_items + short_items.size();
+    w.merge_count = (int)(merge_rows.size() / 2);
+    w.max_splits = max_splits;
+    w.split_stride = max_splits;
+    w.partial_out = reinterpret_cast<float*>(buffer + int_bytes);
+    w.partial_ml = w.partial_out + (size_t)rows * kv_heads * max_splits * group * 64;
+    w.kv_heads = kv_heads;
+    mphip::RowMeta meta{};
+    meta.row_pos = w.merge_rows + merge_rows.size();
+    const mphip::PagedKv kv{const_cast<float*>(keys), const_cast<float*>(values), tables, table_stride, layers,
+                            block_tokens, kv_heads * dim};
+    if (e == hipSuccess)
+        e = mphip::launch_fast_attention(s, q, heads * dim, rows, heads, kv_heads, meta, kv, layer, out, heads * dim,
+                                         w, true);
+    // Synchronous, so that the work lists can be released before returning.
+    const hipError_t done = hipStreamSynchronize(s);
+    if (e == hipSuccess) e = done;
+    (void)hipFree(buffer);
+    if (e != hipSuccess) {
+        mphip::set_free_error(std::string("fast paged attention: ") + hipGetErrorString(e));
+        return MP_DEVICE_ERROR;
+    }
+    return MP_OK;
 }
 
 int mp_hip_sync(mp_hip* h) {

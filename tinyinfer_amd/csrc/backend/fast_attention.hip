@@ -11,7 +11,8 @@
 // so a row's result does not depend on the rest of the batch.
 //
 // One wavefront per work item (row, KV head, split: the item carries the
-// row's table slot beside the KV head), four items per work-group; the
+// row's table slot beside the KV head and the row's sequence, whose index
+// places the split's partial results), four items per work-group; the
 // wavefront serves the G query heads of the KV head, so each K and V byte
 // is read once. It walks the split's (up to 16) pages with two pages in
 // flight in a ring of registers: the loads of page k+2 are issued as soon
@@ -63,6 +64,12 @@ constexpr int kMergeHeld = 16;  // splits per lane group whose partials the merg
 constexpr float kScale = 0.125f;  // 1/sqrt(64)
 constexpr float kRescale = 16.0f;  // probabilities stay below e^16 before a rescale
 
+// Activation addressing: the forward's row-tile quad layout (layout.h), or
+// plain row-major rows (the stand-alone entry point).
+template <bool PLAIN>
+__device__ __forceinline__ size_t act_index(int row, int column, int width) {
+    return PLAIN ? (size_t)row * width + column : quad_index(row, column, width);
+}
 
 // Slice `touch` (8 KB) of the weights to prefetch: lane i reads one dword
 // of line i (128 bytes) of the slice; slices past the ranges read nothing.
@@ -82,7 +89,7 @@ __device__ __forceinline__ float touch_weights(const FastAttentionWork& w, uint6
 // kvh. Gives per head the reference maximum m, the denominator l and lane
 // d's weighted sum acc (not yet divided). `touch` numbers this wavefront's
 // 8 KB slice of the weight prefetch; p_s is the wavefront's own LDS.
-template <int G>
+template <int G, bool PLAIN>
 __device__ __forceinline__ void attend_split(const float* __restrict__ qkv, int ldq, const PagedKv& kv, int layer,
                                              const FastAttentionWork& w, const int32_t* table, int row, int kvh,
                                              int t0, int n, uint64_t touch, float (&p_s)[G][kPage], float (&m)[G],
@@ -107,15 +114,15 @@ __device__ __forceinline__ void attend_split(const float* __restrict__ qkv, int 
             vv[j] = __builtin_nontemporal_load(vp + j * kDim + lane);
         }
     };
-    // q of the group's heads, dims 16dq..16dq+15 (rotated, quad layout);
-    // loaded before the pages, as loads complete in order.
+    // q of the group's heads, dims 16dq..16dq+15 (rotated); loaded before
+    // the pages, as loads complete in order.
     f4 q[G][4];
 #pragma unroll
     for (int h = 0; h < G; ++h)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int c = (kvh * G + h) * kDim + dq * 16 + j * 4;
-            q[h][j] = *reinterpret_cast<const f4*>(qkv + quad_index(row, c, ldq));
+            q[h][j] = *reinterpret_cast<const f4*>(qkv + act_index<PLAIN>(row, c, ldq));
         }
     __builtin_amdgcn_sched_barrier(0);
     const float touched = touch_weights(w, touch, lane);
@@ -214,7 +221,7 @@ __device__ __forceinline__ void attend_split(const float* __restrict__ qkv, int 
 }
 
 // Splits of rows of more than 256 tokens, one wavefront per work item.
-template <int G>
+template <int G, bool PLAIN>
 __global__ __launch_bounds__(kItemsPerGroup * 64) void fast_attention_kernel(const float* __restrict__ qkv, int ldq,
                                                                              RowMeta meta, PagedKv kv, int layer,
                                                                              FastAttentionWork w,
@@ -231,11 +238,12 @@ __global__ __launch_bounds__(kItemsPerGroup * 64) void fast_attention_kernel(con
         return;
     }
     const int4 item = reinterpret_cast<const int4*>(w.items)[index];
-    const int row = item.x, kvh = item.y % w.kv_heads, t0 = item.z, n = item.w & 0xFFFF, sp = item.w >> 16;
+    const int row = item.x, kvh = item.y % w.kv_heads, seq = item.z;
+    const int n = item.w & 0x1FF, sp = (item.w >> 9) & 0x7FFF, t0 = sp << (item.w >> 24);
     const int32_t* table = kv.tables + (size_t)(item.y / w.kv_heads) * kv.table_stride;
     float m[G], l[G], acc[G];
-    attend_split<G>(qkv, ldq, kv, layer, w, table, row, kvh, t0, n, (uint64_t)index, p_s[wave], m, l, acc);
-    const size_t slot = ((size_t)row * w.kv_heads + kvh) * w.max_splits + sp;
+    attend_split<G, PLAIN>(qkv, ldq, kv, layer, w, table, row, kvh, t0, n, (uint64_t)index, p_s[wave], m, l, acc);
+    const size_t slot = ((size_t)seq * w.kv_heads + kvh) * w.split_stride + sp;
 #pragma unroll
     for (int h = 0; h < G; ++h) {
         const size_t at = slot * G + h;
@@ -252,7 +260,7 @@ __global__ __launch_bounds__(kItemsPerGroup * 64) void fast_attention_kernel(con
 // w.short_items, wavefront s takes split s, and the splits are combined
 // through LDS in split order by one wavefront per query head, so these
 // rows need no merge launch. A row of one split gives acc / l exactly.
-template <int G>
+template <int G, bool PLAIN>
 __global__ __launch_bounds__(kSplitPages * 64) void fast_attention_short_kernel(const float* __restrict__ qkv,
                                                                                 int ldq, RowMeta meta, PagedKv kv,
                                                                                 int layer, FastAttentionWork w,
@@ -279,7 +287,7 @@ __global__ __launch_bounds__(kSplitPages * 64) void fast_attention_short_kernel(
     if (wave < splits) {
         float m[G], l[G], acc[G];
         const int t0 = wave * split;
-        attend_split<G>(qkv, ldq, kv, layer, w, table, row, kvh, t0, min(split, length - t0),
+        attend_split<G, PLAIN>(qkv, ldq, kv, layer, w, table, row, kvh, t0, min(split, length - t0),
                         (uint64_t)blockIdx.x * kSplitPages + wave, p_s[wave], m, l, acc);
 #pragma unroll
         for (int h = 0; h < G; ++h) {
@@ -309,11 +317,12 @@ __global__ __launch_bounds__(kSplitPages * 64) void fast_attention_short_kernel(
 #pragma unroll
     for (int s = 0; s < kSplitPages; ++s)
         if (s < splits) num += part_acc[s][h][lane] * lane_value(f, s);
-    out[quad_index(row, (kvh * G + h) * kDim + lane, ldo)] = num / den;
+    out[act_index<PLAIN>(row, (kvh * G + h) * kDim + lane, ldo)] = num / den;
 }
 
 // out[row][h*64 + d] for the listed rows (w.merge_rows: one-token rows of
-// more than 256 tokens): the splits of (row, h/G) combined. One wavefront
+// more than 256 tokens, with their sequences): the splits of (row, h/G)
+// combined. One wavefront
 // per (row, head), as four groups of 16 lanes: lane 16g + c holds dims
 // 4c..4c+3, and group g takes splits g,
 // g+4, g+8, ... with its own running maximum, denominator and weighted sum,
@@ -321,18 +330,20 @@ __global__ __launch_bounds__(kSplitPages * 64) void fast_attention_short_kernel(
 // 16k tokens in 256-token splits, takes one round of loads). The four
 // groups are then rescaled to the common maximum and summed as
 // (g0 + g1) + (g2 + g3). The order depends on nothing but the row's split
-// count. The partials sit at a fixed stride per (row, KV head), so the
+// count. The partials sit at a fixed stride per (sequence, KV head), so the
 // first round is issued together with the load of the row's position.
+template <bool PLAIN>
 __global__ __launch_bounds__(256) void fast_attention_merge_kernel(int heads, int kv_heads, RowMeta meta,
                                                                    FastAttentionWork w, float* __restrict__ out,
                                                                    int ldo) {
     const int lane = threadIdx.x & 63;
     const int pair = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (pair >= w.merge_count * heads) return;
-    const int row = w.merge_rows[pair / heads], h = pair % heads;
+    const int2 rs = reinterpret_cast<const int2*>(w.merge_rows)[pair / heads];
+    const int row = rs.x, h = pair % heads;
     const int G = heads / kv_heads, kvh = h / G, hg = h % G;
     const int grp = lane >> 4, c = lane & 15;
-    const size_t slot0 = ((size_t)row * kv_heads + kvh) * w.max_splits;  // split 0 of (row, kvh)
+    const size_t slot0 = ((size_t)rs.y * kv_heads + kvh) * w.split_stride;  // split 0 of (sequence, kvh)
     auto at = [&](int sp) { return (slot0 + sp) * G + hg; };
     int pos = meta.row_pos[row];
     float gm = -__builtin_inff(), gl = 0.0f;
@@ -395,10 +406,10 @@ __global__ __launch_bounds__(256) void fast_attention_merge_kernel(int heads, in
         num[i] += __shfl_xor(num[i], 16);
         num[i] += __shfl_xor(num[i], 32);
     }
-    if (grp == 0) *reinterpret_cast<f4*>(out + quad_index(row, h * kDim + 4 * c, ldo)) = num / den;
+    if (grp == 0) *reinterpret_cast<f4*>(out + act_index<PLAIN>(row, h * kDim + 4 * c, ldo)) = num / den;
 }
 
-template <int G>
+template <int G, bool PLAIN>
 void launch_items(hipStream_t s, const float* qkv, int ldq, const RowMeta& meta, const PagedKv& kv, int layer,
                   const FastAttentionWork& w, float* out, int ldo) {
     // Slices of 8 KB (one per wavefront) that cover the weights to prefetch.
@@ -411,36 +422,43 @@ void launch_items(hipStream_t s, const float* qkv, int ldq, const RowMeta& meta,
         int groups = w.short_count;
         if (w.items_count <= 0)
             groups = (int)std::max<uint64_t>((uint64_t)groups, (slices + kSplitPages - 1) / kSplitPages);
-        fast_attention_short_kernel<G><<<groups, kSplitPages * 64, 0, s>>>(qkv, ldq, meta, kv, layer, w, out, ldo);
+        fast_attention_short_kernel<G, PLAIN><<<groups, kSplitPages * 64, 0, s>>>(qkv, ldq, meta, kv, layer, w, out, ldo);
     }
     if (w.items_count > 0) {
         const uint64_t waves = std::max<uint64_t>((uint64_t)w.items_count, slices);
-        fast_attention_kernel<G><<<(int)((waves + kItemsPerGroup - 1) / kItemsPerGroup), kItemsPerGroup * 64, 0,
+        fast_attention_kernel<G, PLAIN><<<(int)((waves + kItemsPerGroup - 1) / kItemsPerGroup), kItemsPerGroup * 64, 0,
                                    s>>>(qkv, ldq, meta, kv, layer, w, out, ldo);
     }
 }
 
-}  // namespace
-
-
-hipError_t launch_fast_attention(hipStream_t s, const float* qkv, int ldq, int rows, int heads, int kv_heads,
-                                 const RowMeta& meta, const PagedKv& kv, int layer, float* out, int ldo,
-                                 const FastAttentionWork& w) {
-    const int G = heads / kv_heads;
-    if (rows <= 0) return hipSuccess;
-    if (kv.block_tokens != kPage || kv.kv_width != kv_heads * kDim || G > kMaxGroup || G < 1 ||
-        G * kv_heads != heads || w.kv_heads != kv_heads)
-        return hipErrorInvalidValue;
-    switch (G) {
-    case 1: launch_items<1>(s, qkv, ldq, meta, kv, layer, w, out, ldo); break;
-    case 2: launch_items<2>(s, qkv, ldq, meta, kv, layer, w, out, ldo); break;
-    case 3: launch_items<3>(s, qkv, ldq, meta, kv, layer, w, out, ldo); break;
-    default: launch_items<4>(s, qkv, ldq, meta, kv, layer, w, out, ldo); break;
+template <bool PLAIN>
+hipError_t launch_all(hipStream_t s, const float* qkv, int ldq, int heads, int kv_heads, const RowMeta& meta,
+                      const PagedKv& kv, int layer, float* out, int ldo, const FastAttentionWork& w) {
+    switch (heads / kv_heads) {
+    case 1: launch_items<1, PLAIN>(s, qkv, ldq, meta, kv, layer, w, out, ldo); break;
+    case 2: launch_items<2, PLAIN>(s, qkv, ldq, meta, kv, layer, w, out, ldo); break;
+    case 3: launch_items<3, PLAIN>(s, qkv, ldq, meta, kv, layer, w, out, ldo); break;
+    default: launch_items<4, PLAIN>(s, qkv, ldq, meta, kv, layer, w, out, ldo); break;
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || w.items_count <= 0 || w.merge_count <= 0) return e;
-    fast_attention_merge_kernel<<<(w.merge_count * heads + 3) / 4, 256, 0, s>>>(heads, kv_heads, meta, w, out, ldo);
+    fast_attention_merge_kernel<PLAIN>
+        <<<(w.merge_count * heads + 3) / 4, 256, 0, s>>>(heads, kv_heads, meta, w, out, ldo);
     return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_fast_attention(hipStream_t s, const float* qkv, int ldq, int rows, int heads, int kv_heads,
+                                 const RowMeta& meta, const PagedKv& kv, int layer, float* out, int ldo,
+                                 const FastAttentionWork& w, bool plain) {
+    const int G = heads / kv_heads;
+    if (rows <= 0) return hipSuccess;
+    if (kv.block_tokens != kPage || kv.kv_width != kv_heads * kDim || G > kMaxGroup || G < 1 ||
+        G * kv_heads != heads || w.kv_heads != kv_heads || (w.items_count > 0 && w.split_stride < w.max_splits))
+        return hipErrorInvalidValue;
+    return plain ? launch_all<true>(s, qkv, ldq, heads, kv_heads, meta, kv, layer, out, ldo, w)
+                 : launch_all<false>(s, qkv, ldq, heads, kv_heads, meta, kv, layer, out, ldo, w);
 }
 
 }  // namespace mphip

@@ -154,24 +154,44 @@ __host__ __device__ inline int fast_attention_split(int length) {
 // Rows of up to 256 tokens (at most 8 splits) are combined inside one
 // work-group; longer rows through the partials and the merge kernel.
 __host__ __device__ inline bool fast_attention_short(int length) { return (length + 15) / 16 <= 16; }
+// The most splits a row that is not short has, over every length up to
+// `length` (0 when every such row is short): the stride of the partial
+// results per (sequence, KV head), fixed by the context limit so that the
+// partials never grow during a decode.
+inline int fast_attention_max_splits(int length) {
+    if (fast_attention_short(length)) return 0;
+    const int below = (length < 4096 ? length : 4096) + 127;  // 128-token splits up to 4,096 tokens
+    const int above = length > 4096 ? (length + 255) / 256 : 0;
+    return below / 128 > above ? below / 128 : above;
+}
+// Work item of a split (int4): row, table slot * kv_heads + KV head,
+// sequence (the partials' index), tokens | split index << 9 | log2(split
+// tokens) << 24 (the split's first token is split index << log2).
+inline int fast_attention_item_w(int tokens, int split_index, int split_tokens) {
+    int lg = 0;
+    while ((1 << lg) < split_tokens) ++lg;
+    return tokens | (split_index << 9) | (lg << 24);
+}
 struct FastAttentionWork {
-    // per work item (int4): row, table slot * kv_heads + KV head, first
-    // token, token count | split index << 16, in any order (the forward
-    // puts every row's whole splits before the shorter last ones)
-    const int32_t* items;  // splits of the rows longer than 256 tokens
+    // splits of the rows longer than 256 tokens (fast_attention_item_w), in
+    // any order (the forward puts every row's whole splits before the
+    // shorter last ones)
+    const int32_t* items;
     int items_count;
     // per row of up to 256 tokens and KV head (int4): row, table slot *
     // kv_heads + KV head, tokens, 0
     const int32_t* short_items;
     int short_count;
     // the rows whose splits the merge kernel combines (the one-token rows
-    // longer than 256 tokens)
+    // longer than 256 tokens), as (row, sequence) int32 pairs
     const int32_t* merge_rows;
     int merge_count;
     // Splits of the longest row (of those longer than 256 tokens; 0 if
-    // none); the partial results of (row, KV head,
-    // split) sit at slot (row * kv_heads + KV head) * max_splits + split.
+    // none), the bound of the merge's first round of loads; the partial
+    // results of (sequence, KV head, split) sit at slot (sequence *
+    // kv_heads + KV head) * split_stride + split, split_stride >= max_splits.
     int max_splits;
+    int split_stride;
     float* partial_out;  // [slot][G][64]
     float* partial_ml;   // [slot][G][2]: running maximum, denominator
     int kv_heads;
@@ -192,9 +212,11 @@ struct FastAttentionWork {
 bool fast_prefill_fits(int heads, int kv_heads, const PagedKv& kv);
 hipError_t launch_fast_prefill(hipStream_t s, const float* qkv, int ldq, int heads, int kv_heads, const PagedKv& kv,
                                int layer, const int32_t* items, int count, float* out, int ldo);
+// `plain`: q rows (ldq wide) and out rows (ldo wide) are row-major instead
+// of the quad layout (the stand-alone entry point).
 hipError_t launch_fast_attention(hipStream_t s, const float* qkv, int ldq, int rows, int heads, int kv_heads,
                                  const RowMeta& meta, const PagedKv& kv, int layer, float* out, int ldo,
-                                 const FastAttentionWork& work);
+                                 const FastAttentionWork& work, bool plain = false);
 
 // Per-row RoPE inputs of a forward for the fast q|k|v projection: for row r
 // at position p = meta.row_pos[r], block[r] = the page holding p (from the

@@ -5,6 +5,7 @@
 #include "harness_backend.h"
 #include <miniprefix/engine.h>
 
+#include <algorithm>
 #include <cstdio>
 #include <cstring>
 #include <string>
@@ -274,6 +275,23 @@ int mpx_runner_sequence(const void* runner, const char* id, int32_t* blocks, int
         if (count) *count = static_cast<int32_t>(b.size());
         if (used) *used = u;
         for (std::size_t i = 0; i < b.size() && static_cast<int32_t>(i) < capacity; ++i) blocks[i] = b[i];
+    });
+}
+
+int mpx_runner_keep_logits(void* runner, int32_t enabled) {
+    return guarded([&] {
+        if (!mpx::keep_logits(runner_of(runner), enabled != 0))
+            throw std::logic_error("runner does not keep logits");
+    });
+}
+
+int mpx_runner_kept_logits(const void* runner, const char* id, float* logits, size_t capacity, size_t* count) {
+    return guarded([&] {
+        const std::vector<float>* kept = nullptr;
+        if (!mpx::kept_logits(runner_of(runner), id, &kept)) throw std::logic_error("runner does not keep logits");
+        if (!kept) throw std::out_of_range("no kept logits for this sequence");
+        if (count) *count = kept->size();
+        if (logits) std::memcpy(logits, kept->data(), std::min(capacity, kept->size()) * sizeof(float));
     });
 }
 

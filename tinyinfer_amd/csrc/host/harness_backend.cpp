@@ -8,6 +8,8 @@
 namespace miniprefix {
 bool hip_runner_sequence(const ModelRunner& runner, const RequestId& id, const PagedSequence** out);
 void* hip_runner_device(ModelRunner& runner);
+bool hip_runner_keep_logits(ModelRunner& runner, bool enabled);
+bool hip_runner_kept_logits(const ModelRunner& runner, const RequestId& id, const std::vector<float>** out);
 }
 
 namespace mpx {
@@ -57,5 +59,13 @@ bool sequence_of(const miniprefix::ModelRunner& runner, const std::string& id, s
 }
 
 void* device_of(miniprefix::ModelRunner& runner) { return miniprefix::hip_runner_device(runner); }
+
+bool keep_logits(miniprefix::ModelRunner& runner, bool enabled) {
+    return miniprefix::hip_runner_keep_logits(runner, enabled);
+}
+
+bool kept_logits(const miniprefix::ModelRunner& runner, const std::string& id, const std::vector<float>** out) {
+    return miniprefix::hip_runner_kept_logits(runner, id, out);
+}
 
 }  // namespace mpx

@@ -24,5 +24,10 @@ void set_batching(miniprefix::Engine& engine, bool enabled);
 bool sequence_of(const miniprefix::ModelRunner& runner, const std::string& id, std::vector<int>* blocks, int* used);
 // The runner's device context, or nullptr.
 void* device_of(miniprefix::ModelRunner& runner);
+// Logit keeping (HipRunner::keep_logits); false when the runner lacks it.
+bool keep_logits(miniprefix::ModelRunner& runner, bool enabled);
+// The kept logits of sequence `id` (*out null if none); false when the
+// runner lacks logit keeping.
+bool kept_logits(const miniprefix::ModelRunner& runner, const std::string& id, const std::vector<float>** out);
 
 }  // namespace mpx

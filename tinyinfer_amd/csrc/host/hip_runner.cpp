@@ -74,6 +74,7 @@ public:
         if (kv_.contains(id)) throw std::invalid_argument("sequence already exists");
         if (free_slots_.empty()) throw std::runtime_error("HIP block table arena exhausted");
         kv_.create(id);
+        kept_.erase(id);
         tables_[id] = Table{free_slots_.back(), false};
         free_slots_.pop_back();
     }
@@ -123,6 +124,7 @@ public:
         }
         tx.commit();
         table.dirty = false;
+        if (keep_logits_) kept_[id] = logits;
         return logits;
     }
 
@@ -155,21 +157,32 @@ public:
         tx.commit();
         table.dirty = false;
         staged_.push_back({table.slot, used, static_cast<std::int32_t>(tokens.size())});
+        staged_ids_.push_back(id);
         staged_tokens_.insert(staged_tokens_.end(), tokens.begin(), tokens.end());
     }
     std::vector<StagedResult> run_staged() override {
         std::vector<StagedResult> results(staged_.size());
         if (staged_.empty()) return results;
         std::vector<std::int32_t> argmax(staged_.size()), nonfinite(staged_.size());
+        // Logits travel to the host only when they are kept (keep_logits).
+        const std::size_t vocab = static_cast<std::size_t>(config().vocabulary);
+        std::vector<float> logits(keep_logits_ ? staged_.size() * vocab : 0);
+        const std::vector<RequestId> ids = staged_ids_;
         const int status = mp_hip_forward(device_, staged_.data(), static_cast<std::int32_t>(staged_.size()),
-                                          staged_tokens_.data(), nullptr, argmax.data(), nonfinite.data());
+                                          staged_tokens_.data(), keep_logits_ ? logits.data() : nullptr,
+                                          argmax.data(), nonfinite.data());
         discard_staged();
         if (status != MP_OK && status != MP_NONFINITE) check(status, "model forward");
         for (std::size_t i = 0; i < results.size(); ++i) results[i] = {argmax[i], nonfinite[i] == 0};
+        if (keep_logits_)
+            for (std::size_t i = 0; i < ids.size(); ++i)
+                kept_[ids[i]].assign(logits.begin() + static_cast<std::ptrdiff_t>(i * vocab),
+                                     logits.begin() + static_cast<std::ptrdiff_t>((i + 1) * vocab));
         return results;
     }
     void discard_staged() noexcept override {
         staged_.clear();
+        staged_ids_.clear();
         staged_tokens_.clear();
         for (const int block : written_) staged_writes_[static_cast<std::size_t>(block)] = 0;
         written_.clear();
@@ -192,6 +205,7 @@ public:
         kv_.clear();
         for (auto& t : tables_) free_slots_.push_back(t.second.slot);
         tables_.clear();
+        kept_.clear();
     }
     RunnerStats stats() const override {
         RunnerStats r;
@@ -213,6 +227,22 @@ public:
     // Committed page table of a sequence (tests compare it with the reference's).
     const PagedSequence& sequence(const RequestId& id) const { return kv_.sequence(id); }
     mp_hip* device() { return device_; }
+
+    // Logit keeping (no counterpart in the reference, whose append returns
+    // the logits to its caller): while enabled, every forward's last-row
+    // logits of each sequence, append or batched, are kept on the host until
+    // the next forward of that sequence (also after its release, which the
+    // Engine performs in the step that emits its last token; until the id is
+    // created again or the runner cleared), so a caller of the batched
+    // Engine (which downloads only the argmax otherwise) can read them.
+    void keep_logits(bool enabled) {
+        keep_logits_ = enabled;
+        if (!enabled) kept_.clear();
+    }
+    const std::vector<float>* kept_logits(const RequestId& id) const {
+        const auto it = kept_.find(id);
+        return it == kept_.end() ? nullptr : &it->second;
+    }
 
 private:
     static constexpr int kMaxSequences = 1024;
@@ -287,11 +317,14 @@ private:
     std::map<RequestId, Table> tables_;
     std::vector<int> free_slots_;
     std::vector<mp_seq_step> staged_;
+    std::vector<RequestId> staged_ids_;
     std::vector<TokenId> staged_tokens_;
     std::vector<char> staged_writes_;  // per block: written by a queued forward
     std::vector<int> written_;         // the blocks marked in staged_writes_
     CostStats costs_;
     bool cost_timing_ = false;
+    bool keep_logits_ = false;
+    std::map<RequestId, std::vector<float>> kept_;
 };
 
 }  // namespace
@@ -312,6 +345,20 @@ bool hip_runner_sequence(const ModelRunner& runner, const RequestId& id, const P
     const auto* hip = dynamic_cast<const HipRunner*>(&runner);
     if (!hip) return false;
     *out = &hip->sequence(id);
+    return true;
+}
+
+// Logit keeping of runners built by make_hip_runner (HipRunner::keep_logits).
+bool hip_runner_keep_logits(ModelRunner& runner, bool enabled) {
+    auto* hip = dynamic_cast<HipRunner*>(&runner);
+    if (!hip) return false;
+    hip->keep_logits(enabled);
+    return true;
+}
+bool hip_runner_kept_logits(const ModelRunner& runner, const RequestId& id, const std::vector<float>** out) {
+    const auto* hip = dynamic_cast<const HipRunner*>(&runner);
+    if (!hip) return false;
+    *out = hip->kept_logits(id);
     return true;
 }
 

@@ -81,6 +81,8 @@ def bind(lib: ctypes.CDLL) -> ctypes.CDLL:
         "mpx_runner_set_cost_timing": ([vp, i32], ctypes.c_int),
         "mpx_runner_sequence": ([vp, c, I32P, i32, I32P, I32P], ctypes.c_int),
         "mpx_runner_device": ([vp], vp),
+        "mpx_runner_keep_logits": ([vp, i32], ctypes.c_int),
+        "mpx_runner_kept_logits": ([vp, c, F32P, sz, ctypes.POINTER(sz)], ctypes.c_int),
         "mpx_engine_create": ([vp, i32, i32, i32, i32], vp),
         "mpx_engine_free": ([vp], None),
         "mpx_engine_set_batching": ([vp, i32], ctypes.c_int),
@@ -243,6 +245,20 @@ class Runner:
 
     def set_cost_timing(self, enabled: bool):
         _check(self.lib, self.lib.mpx_runner_set_cost_timing(self.handle, int(enabled)))
+
+    def keep_logits(self, enabled: bool = True):
+        """Keep every forward's last-row logits per sequence on the host (also
+        in the batched Engine step, which otherwise downloads only the argmax)."""
+        _check(self.lib, self.lib.mpx_runner_keep_logits(self.handle, int(enabled)))
+
+    def kept_logits(self, rid: str) -> np.ndarray:
+        """The last-row logits of sequence rid's latest forward (keep_logits)."""
+        out = np.empty(self.vocabulary, dtype=np.float32)
+        n = ctypes.c_size_t()
+        _check(self.lib, self.lib.mpx_runner_kept_logits(self.handle, _b(rid), out.ctypes.data_as(F32P), out.size,
+                                                         ctypes.byref(n)))
+        assert n.value == out.size
+        return out
 
     def device(self) -> int | None:
         """The runner's device context (mp_hip*), or None."""
