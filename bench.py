@@ -22,14 +22,19 @@ against the reference's in the GPU tests); --arithmetic exact selects the
 bit-exact one.
 
 Prefill runs first (untimed); `--warmup` pure-decode steps follow, then
-exactly `--steps` timed steps between two device synchronisations. Each
-forward call ends with a device synchronisation of its own (the runner
+exactly `--steps` timed steps between two device synchronisations (`value`).
+Each forward call ends with a device synchronisation of its own (the runner
 returns argmax results to the host), so host time over the steps is the
-whole job's time.
+whole job's time. The timed window sits early in the decode, where the
+contexts are shorter than the decode's mean: `timed_window` states its mean
+context against the whole decode's, and `whole_decode` is the rate over
+every decode step but the roofline pass (each step timed on the host).
 
-roofline: one layer per step (rotating through the layers) has its
-attention and its four projections timed with HIP events on the runner's
-stream. Attention algorithmic bytes per launch = sum over sequences of
+roofline: after the timed window, a pass of up to 30 decode steps has one
+layer per step (rotating through the layers) with its attention and its four
+projections timed with HIP events on the runner's stream (timing keeps
+these steps on direct launches). Attention algorithmic bytes per launch =
+sum over sequences of
 T*kv_width*4*2 (K and V of every attended token, read once) +
 rows*hidden*4*2 (q in, context out). Projection algorithmic bytes per layer
 = the layer's weights (q|k|v, o, gate, up, down) + the activations they read
@@ -44,10 +49,14 @@ of known size that --traffic-probe runs).
 
 cpu_baseline: the reference CPU runner (the reference's own CpuRunner,
 Engine and KVManager compiled from its sources into oracle/_ref) on one
-pinned host core: the prefill of one request's first prompt chunk, then
-single-token decode steps for about --cpu-seconds; prefill and decode rates
-are reported separately. Without oracle/_ref the oracle (a C restatement of
-the reference CPU path, bit-identical to it) stands in, labelled "port".
+pinned host core, in a process of its own started before the GPU is
+touched and run beside the GPU leg on another core: the prefill of a prompt
+as long as the workload's mean decode context (capped at 1,300 tokens; the
+prefix of the workload's longest prompt, in the workload's prefill chunks),
+then single-token decode steps for about --cpu-seconds; prefill and decode
+rates are reported separately. Without oracle/_ref the oracle (a C
+restatement of the reference CPU path, bit-identical to it) stands in,
+labelled "port".
 """
 from __future__ import annotations
 
@@ -57,6 +66,7 @@ import gc
 import json
 import os
 import platform
+import subprocess
 import sys
 import time
 from collections import defaultdict
@@ -75,7 +85,9 @@ METRICS = {
     "config5a": "decode tok/s (B=8, 16384-token prompts, SmolLM2-135M-shape FP32); paged-attn HBM GB/s % peak",
     "config5b": "decode tok/s (B=256, 1024-token contexts, SmolLM2-135M-shape FP32); paged-attn HBM GB/s % peak",
 }
-DEFAULT_STEPS = {"config3": (96, 8), "config2": (96, 8), "config4": (48, 8), "config5a": (64, 8), "config5b": (40, 6)}
+DEFAULT_STEPS = {"config3": (64, 8), "config2": (64, 8), "config4": (24, 6), "config5a": (96, 8), "config5b": (24, 6)}
+ROOFLINE_STEPS = 30  # decode steps of the roofline pass (fewer if the decode ends first)
+CPU_CONTEXT_CAP = 1300  # tokens of the CPU baseline's prefill
 HBM_PEAK_GBS = 8000.0
 FP32_MATRIX_PEAK_TFLOPS = 157.3
 PROBE_BYTES = 128 << 20  # --traffic-probe: one copy of 128 MiB (read and written)
@@ -160,31 +172,44 @@ def gpu_leg(args, wl):
             raise RuntimeError("prefill did not finish")
     log(f"prefill: {setup_steps} + {prefill_steps} steps, {time.perf_counter() - t:.1f}s")
     remaining = min(r.max_new_tokens for r in active) - max(generated[i] for i in ids)
-    if args.warmup + args.steps > remaining:
-        raise SystemExit(f"--warmup + --steps must leave every request decoding: at most {remaining} steps remain")
+    if args.warmup + args.steps + 1 > remaining:
+        raise SystemExit(f"--warmup + --steps must leave every request decoding for one more step: "
+                         f"{remaining} decode steps remain")
     batch = len(ids)
-    for _ in range(args.warmup):
+    used0 = {rid: engine.runner.sequence(rid)[1] for rid in ids}  # committed tokens before the first decode step
+    clean = []  # (decode step index, host seconds) of the steps outside the roofline pass
+
+    def decode_step(index):
+        t = time.perf_counter()
         s = step()
+        clean.append((index, time.perf_counter() - t))
         assert s["decode_tokens"] == batch and s["prefill_tokens"] == 0, s
-    used = {rid: engine.runner.sequence(rid)[1] for rid in ids}
-    # One layer per step (rotating) has its attention and projections timed,
-    # so that timing costs the measured throughput almost nothing;
-    # --all-kernels times every launch and the LM head.
-    classes = TIME_ATTENTION | TIME_PROJECTION | (TIME_HEAD if args.all_kernels else TIME_SAMPLED)
-    set_timing(device, classes)
+
+    for i in range(args.warmup):
+        decode_step(i)
     if args.cost_timing:
         runner.set_cost_timing(True)
     costs0 = runner.cost_stats()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
-        s = step()
-        assert s["decode_tokens"] == batch and s["prefill_tokens"] == 0, s
+    for i in range(args.warmup, args.warmup + args.steps):
+        decode_step(i)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    times = kernel_times(device)
+    costs = {k: v - costs0.get(k, 0) for k, v in runner.cost_stats().items()}  # the timed steps
     for rid in ids:
-        assert engine.runner.sequence(rid)[1] == used[rid] + args.steps
+        assert engine.runner.sequence(rid)[1] == used0[rid] + args.warmup + args.steps
+    # Roofline pass: one layer per step (rotating) has its attention and
+    # projections timed; --all-kernels times every layer and the LM head.
+    first_rof = args.warmup + args.steps
+    rof_steps = min(ROOFLINE_STEPS, remaining - first_rof)
+    classes = TIME_ATTENTION | TIME_PROJECTION | (TIME_HEAD if args.all_kernels else TIME_SAMPLED)
+    set_timing(device, classes)
+    for _ in range(rof_steps):
+        s = step()
+        assert s["decode_tokens"] == batch and s["prefill_tokens"] == 0, s
+    times = kernel_times(device)
+    set_timing(device, 0)
     if args.traffic_probe:
         # A copy of known size for the counter calibration (--summarise-counters).
         src = torch.ones(PROBE_BYTES // 4, dtype=torch.float32, device="cuda")
@@ -192,26 +217,36 @@ def gpu_leg(args, wl):
         for _ in range(2):
             dst.copy_(src)
         torch.cuda.synchronize()
-    costs = {k: v - costs0.get(k, 0) for k, v in runner.cost_stats().items()}  # the timed steps
+    # The rest of the decode, step by step, for the whole-decode rate.
+    for i in range(first_rof + rof_steps, remaining):
+        decode_step(i)
     engine.shutdown()
     engine.close()
 
-    K = args.steps
-    sum_t = sum(K * u + K * (K + 1) // 2 for u in used.values())  # attended tokens over the timed steps
+    def attended(first, count):  # attended tokens of every sequence over decode steps first..first+count-1
+        return sum(count * u + count * first + count * (count + 1) // 2 for u in used0.values())
+
+    K, R = args.steps, rof_steps
+    sum_t = attended(first_rof, R)  # the roofline pass
     kvw, layer_floats, act_floats = layer_shape(cfg)
     timed_layers = cfg["layers"] if args.all_kernels else 1  # per step
     att_launches = times["attention_launches"]
-    assert att_launches == K * timed_layers, times
+    assert att_launches == R * timed_layers, times
     att_bytes = timed_layers * (sum_t * kvw * 4 * 2) + att_launches * batch * cfg["hidden"] * 4 * 2
     att_s = times["attention_ns"] * 1e-9
     proj_layers = times["projection_launches"] // 4
-    assert proj_layers == K * timed_layers, times
+    assert proj_layers == R * timed_layers, times
     proj_bytes_layer = 4 * (layer_floats + batch * act_floats)
     proj_flops_layer = 2 * batch * layer_floats
     proj_s = times["projection_ns"] * 1e-9
+    whole_s = sum(t for _, t in clean)
+    whole_ctx = sum(attended(i, 1) for i, _ in clean) / (len(clean) * batch)
     return dict(
         value=batch * K / elapsed, ms_per_step=elapsed / K * 1e3, batch=batch, prefill_steps=setup_steps + prefill_steps,
-        mean_context=sum_t / (K * batch), times=times, cow=costs,
+        mean_context=attended(args.warmup, K) / (K * batch), decode_steps=remaining, roofline_steps=R,
+        roofline_context=sum_t / (R * batch), times=times, cow=costs,
+        whole=dict(value=round(batch * len(clean) / whole_s, 2), steps=len(clean),
+                   ms_per_step=round(whole_s / len(clean) * 1e3, 4), mean_context=round(whole_ctx, 1)),
         attention=dict(us=att_s / att_launches * 1e6, bytes=att_bytes / att_launches, gbs=att_bytes / att_s / 1e9),
         projections=dict(us=proj_s / proj_layers * 1e6, bytes=proj_bytes_layer, flops=proj_flops_layer,
                          gbs=proj_bytes_layer * proj_layers / proj_s / 1e9,
@@ -234,19 +269,32 @@ def host_info():
     return dict(host_nproc=os.cpu_count(), host_cpus_available=avail, cpu_model=model)
 
 
+def cpu_prompt(wl):
+    """The CPU baseline's prompt: the prefix of the workload's longest prompt
+    as long as the mean context of its decode steps, capped at
+    CPU_CONTEXT_CAP tokens."""
+    last = max(r.phase for r in wl.requests)
+    active = [r for r in wl.requests if r.phase == last]
+    mean_context = sum(len(r.prompt) + r.max_new_tokens / 2 for r in active) / len(active)
+    longest = max(active, key=lambda r: len(r.prompt)).prompt
+    n = min(int(round(mean_context)), CPU_CONTEXT_CAP, len(longest))
+    return np.asarray(longest[:n], dtype=np.int32), mean_context
+
+
 def cpu_leg(args, wl):
-    """The reference CPU path on one pinned core: one request's first prompt
-    chunk, then single-token decode steps (the reference CPU runner serves
-    one sequence per call, so this is its throughput)."""
+    """The reference CPU path on one pinned core: a prompt as long as the
+    workload's mean decode context, prefilled in the workload's chunks, then
+    single-token decode steps (the reference CPU runner serves one sequence
+    per call, so this is its throughput)."""
     from oracle import ref_library
 
     info = host_info()
     try:
-        os.sched_setaffinity(0, {sorted(os.sched_getaffinity(0))[0]})
+        os.sched_setaffinity(0, {sorted(os.sched_getaffinity(0))[-1]})
     except (AttributeError, OSError):
         pass
     cfg = wl.config()
-    prompt = np.asarray(wl.requests[-1].prompt[:wl.prefill_chunk], dtype=np.int32)
+    prompt, mean_context = cpu_prompt(wl)
     ref = ref_library()
     if ref is None:
         return oracle_cpu_leg(args, wl, cfg, prompt, info)
@@ -254,12 +302,14 @@ def cpu_leg(args, wl):
 
     w = Weights.synthetic(cfg, seed=wl.weight_seed, stddev=0.02, library=ref)
     pages = -(-(len(prompt) + 256) // 16)
+    chunk = min(wl.prefill_chunk, len(prompt))
     runner = Runner(w, context=cfg["context"], kind=0, block_tokens=16, max_blocks=pages, prefix_cache_blocks=0)
-    engine = Engine(runner, max_batch_size=1, token_budget=len(prompt), prefill_chunk=len(prompt),
-                    context=cfg["context"])
+    engine = Engine(runner, max_batch_size=1, token_budget=chunk, prefill_chunk=chunk, context=cfg["context"])
     engine.submit("cpu", prompt, max_new_tokens=256, eos_token_id=None)
     t = time.perf_counter()
-    engine.step()  # the whole prompt in one chunk, and its first token
+    prefill_steps = -(-len(prompt) // chunk)
+    for _ in range(prefill_steps):  # the prompt in the workload's chunks, and its first token
+        engine.step()
     prefill_s = time.perf_counter() - t
     decoded, spent = 0, 0.0
     while spent < args.cpu_seconds or decoded < 2:
@@ -275,10 +325,11 @@ def cpu_leg(args, wl):
     engine.close()
     return dict(value=round(decoded / spent, 3), unit="tok/s", cores=1, kind="reference",
                 prefill_tok_s=round(len(prompt) / prefill_s, 2), prefill_s=round(prefill_s, 2),
-                sample=f"reference CpuRunner + Engine (oracle/_ref, built from the reference sources), 1 pinned core: "
-                       f"prefill of a {len(prompt)}-token prompt chunk of the same workload ({prefill_s:.1f}s), then "
-                       f"{decoded} single-token decode steps at contexts {len(prompt) + 1}..{len(prompt) + decoded} "
-                       f"({spent:.1f}s)", **info)
+                sample=f"reference CpuRunner + Engine (oracle/_ref, built from the reference sources), 1 pinned core, "
+                       f"beside the GPU leg: prefill of a {len(prompt)}-token prompt of the same workload in "
+                       f"{chunk}-token chunks ({prefill_s:.1f}s), then {decoded} single-token decode steps at contexts "
+                       f"{len(prompt) + 1}..{len(prompt) + decoded} ({spent:.1f}s); the workload's decode averages "
+                       f"{mean_context:.0f} tokens of context", **info)
 
 
 def oracle_cpu_leg(args, wl, cfg, prompt, info):
@@ -304,8 +355,9 @@ def oracle_cpu_leg(args, wl, cfg, prompt, info):
         token = int(np.argmax(logits))
     return dict(value=round(decoded / spent, 3), unit="tok/s", cores=1, kind="port",
                 prefill_tok_s=round(len(prompt) / prefill_s, 2), prefill_s=round(prefill_s, 2),
-                sample=f"oracle (C restatement of the reference CPU runner, bit-identical to it), 1 pinned core: "
-                       f"{len(prompt)}-token prefill ({prefill_s:.1f}s), {decoded} decode steps ({spent:.1f}s)", **info)
+                sample=f"oracle (C restatement of the reference CPU runner, bit-identical to it), 1 pinned core, beside "
+                       f"the GPU leg: {len(prompt)}-token prefill ({prefill_s:.1f}s), {decoded} decode steps at contexts "
+                       f"{len(prompt) + 1}..{len(prompt) + decoded} ({spent:.1f}s)", **info)
 
 
 def roofline(kind: str, g: dict, rec: dict | None):
@@ -316,7 +368,9 @@ def roofline(kind: str, g: dict, rec: dict | None):
                 "achieved": round(a["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(a["gbs"] / HBM_PEAK_GBS, 4),
                 "traffic": int(round(ratio * a["bytes"])) if ratio else None, "traffic_ratio": ratio,
-                "algorithmic_bytes_per_launch": int(a["bytes"]), "us_per_launch": round(a["us"], 2)}
+                "algorithmic_bytes_per_launch": int(a["bytes"]), "us_per_launch": round(a["us"], 2),
+                "measured_over": f"{g['roofline_steps']} decode steps after the timed window (one layer per step), "
+                                 f"mean context {g['roofline_context']:.1f}"}
     p = g["projections"]
     ratio = rec.get("projection_ratio") if rec else None
     return {"bound": "hbm", "kernel": "projections (one layer: q|k|v+RoPE, o, gate/up+SwiGLU, down)",
@@ -519,6 +573,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--cpu-seconds", type=float, default=8.0, help="decode time of the CPU baseline")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-leg", action="store_true", help=argparse.SUPPRESS)  # the CPU baseline's own process
     ap.add_argument("--all-kernels", action="store_true", help="time every layer and the LM head")
     ap.add_argument("--arithmetic", choices=["fast", "exact"], default="fast")
     ap.add_argument("--traffic-probe", action="store_true", help="run a copy of known size after the timed steps")
@@ -546,13 +601,34 @@ def main():
     from tinyinfer_amd import workloads
 
     wl = getattr(workloads, args.workload)()
+    if args.cpu_leg:
+        print(json.dumps(cpu_leg(args, wl)), flush=True)
+        return
     steps, warmup = DEFAULT_STEPS[args.workload]
     args.steps = steps if args.steps is None else args.steps
     args.warmup = warmup if args.warmup is None else args.warmup
     if args.steps < 1 or args.warmup < 0:
         raise SystemExit("--steps must be >= 1 and --warmup >= 0")
+    # The CPU baseline runs in a process of its own, started before this one
+    # touches the GPU, on the last host core; this process keeps the others.
+    child = None
+    if not args.no_cpu_baseline:
+        child = subprocess.Popen([sys.executable, str(Path(__file__).resolve()), "--cpu-leg", "--workload",
+                                  args.workload, "--cpu-seconds", str(args.cpu_seconds)],
+                                 stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True)
+        try:
+            cores = sorted(os.sched_getaffinity(0))
+            if len(cores) > 1:
+                os.sched_setaffinity(0, set(cores[:-1]))
+        except (AttributeError, OSError):
+            pass
     g = gpu_leg(args, wl)
-    cpu = None if args.no_cpu_baseline else cpu_leg(args, wl)
+    cpu = None
+    if child is not None:
+        out, err = child.communicate(timeout=900)
+        if child.returncode != 0:
+            raise SystemExit(f"CPU baseline failed ({child.returncode}): {err[-2000:]}")
+        cpu = json.loads(out.strip().splitlines()[-1])
     rec = None
     tf = traffic_file(args.workload)
     if tf.exists():
@@ -573,8 +649,16 @@ def main():
                    "batch": g["batch"], "page_tokens": 16, "prefill_chunk": wl.prefill_chunk,
                    "token_budget": wl.token_budget, "seed": wl.weight_seed, "arithmetic": args.arithmetic,
                    "mean_context": round(g["mean_context"], 1),
-                   "timed_window": f"decode steps {args.warmup + 1}..{args.warmup + args.steps} after prefill "
-                                   f"({g['prefill_steps']} prefill steps untimed)"},
+                   "timed_window": f"decode steps {args.warmup + 1}..{args.warmup + args.steps} of "
+                                   f"{g['decode_steps']} after prefill ({g['prefill_steps']} prefill steps untimed); "
+                                   f"mean context {g['mean_context']:.1f} against {g['whole']['mean_context']:.1f} "
+                                   f"over the decode, so the window attends "
+                                   f"{g['mean_context'] / g['whole']['mean_context']:.3f}x the decode's mean KV bytes "
+                                   f"per step"},
+        "whole_decode": {"value": g["whole"]["value"], "unit": "tok/s", "steps": g["whole"]["steps"],
+                         "ms_per_step": g["whole"]["ms_per_step"], "mean_context": g["whole"]["mean_context"],
+                         "note": f"every decode step but the {g['roofline_steps']} of the roofline pass, each timed "
+                                 f"on the host"},
         "roofline": roofline(dominant, g, rec),
         "roofline_other": roofline(other, g, rec),
         "cpu_baseline": cpu,

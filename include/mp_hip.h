@@ -232,6 +232,19 @@ typedef struct mp_hip_timing_totals {
 int mp_hip_set_timing(mp_hip* h, uint32_t classes);
 int mp_hip_kernel_times(const mp_hip* h, mp_hip_timing_totals* out);
 
+/* Graph replay of fast-arithmetic decode steps (no counterpart in the
+ * reference, which launches every kernel of every step): a decode step
+ * (every sequence one token) of up to 16 sequences and of a shape seen in
+ * the previous call -- the same number of sequences, logits wanted or not,
+ * rows longer and shorter than 256 tokens present or not -- is captured
+ * once as a HIP graph of its launches and replayed at later steps of that
+ * shape, with the step's metadata uploaded before the replay; results are
+ * bit-identical to direct launches. On by default; off while kernel timing
+ * (mp_hip_set_timing) is on. mp_hip_set_graphs(h, 0) switches it off (and retires the graphs);
+ * mp_hip_graphs_captured reports how many graphs the context holds. */
+int mp_hip_set_graphs(mp_hip* h, int32_t enabled);
+int mp_hip_graphs_captured(const mp_hip* h, int32_t* count);
+
 #ifdef __cplusplus
 }
 #endif

@@ -77,6 +77,8 @@ def _bind(lib):
     lib.mp_hip_stream.restype = vp
     lib.mp_hip_set_timing.argtypes = [vp, ctypes.c_uint32]
     lib.mp_hip_kernel_times.argtypes = [vp, ctypes.POINTER(KernelTimes)]
+    lib.mp_hip_set_graphs.argtypes = [vp, ctypes.c_int32]
+    lib.mp_hip_graphs_captured.argtypes = [vp, I32P]
     lib._mp_bound = True
     return lib
 
@@ -172,6 +174,21 @@ def set_timing(handle: int, classes: int):
     status = lib().mp_hip_set_timing(handle, classes)
     if status:
         raise BackendError(status, lib().mp_hip_last_error(handle).decode())
+
+
+def set_graphs(handle: int, enabled: bool):
+    """Graph replay of decode steps on a device context (mp_hip*)."""
+    status = lib().mp_hip_set_graphs(handle, int(enabled))
+    if status:
+        raise BackendError(status, "mp_hip_set_graphs failed")
+
+
+def graphs_captured(handle: int) -> int:
+    n = np.zeros(1, dtype=np.int32)
+    status = lib().mp_hip_graphs_captured(handle, n.ctypes.data_as(I32P))
+    if status:
+        raise BackendError(status, "mp_hip_graphs_captured failed")
+    return int(n[0])
 
 
 def kernel_times(handle: int) -> dict:

@@ -230,14 +230,18 @@ __global__ __launch_bounds__(kItemsPerGroup * 64) void fast_attention_kernel(con
     __shared__ float p_s[kItemsPerGroup][G][kPage];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int index = blockIdx.x * kItemsPerGroup + wave;
-    if (index >= w.items_count) {
+    // The item (within the list's capacity) and the count are loaded
+    // together; the count lives in device memory so that a captured launch
+    // of capacity-sized grids serves every step.
+    int4 item = {0, 0, 0, 0};
+    if (index < w.items_capacity) item = reinterpret_cast<const int4*>(w.items)[index];
+    if (index >= w.counts[0]) {
         // A wavefront past the items (batches with few splits) only touches
         // its slice of the weights to prefetch.
         const float touched = touch_weights(w, (uint64_t)index, lane);
         asm volatile("" ::"v"(touched));
         return;
     }
-    const int4 item = reinterpret_cast<const int4*>(w.items)[index];
     const int row = item.x, kvh = item.y % w.kv_heads, seq = item.z;
     const int n = item.w & 0x1FF, sp = (item.w >> 9) & 0x7FFF, t0 = sp << (item.w >> 24);
     const int32_t* table = kv.tables + (size_t)(item.y / w.kv_heads) * kv.table_stride;
@@ -270,16 +274,18 @@ __global__ __launch_bounds__(kSplitPages * 64) void fast_attention_short_kernel(
     __shared__ float p_s[kSplitPages][G][kPage];
     __shared__ float part_ml[kSplitPages][G][2];
     __shared__ float part_acc[kSplitPages][G][kDim];
-    if (blockIdx.x >= w.short_count) {
+    // (row, slot * kv_heads + KV head, tokens): the length rides in the item,
+    // one dependent load fewer before the pages; loaded together with the
+    // count.
+    int4 item = {0, 0, 1, 0};
+    if ((int)blockIdx.x < w.short_capacity) item = reinterpret_cast<const int4*>(w.short_items)[blockIdx.x];
+    if ((int)blockIdx.x >= w.counts[1]) {
         // A work-group past the items (small batches, whose items leave
         // most CUs idle) only touches its slices of the weights to prefetch.
         const float touched = touch_weights(w, (uint64_t)blockIdx.x * kSplitPages + wave, lane);
         asm volatile("" ::"v"(touched));
         return;
     }
-    // (row, slot * kv_heads + KV head, tokens): the length rides in the item,
-    // one dependent load fewer before the pages.
-    const int4 item = reinterpret_cast<const int4*>(w.short_items)[blockIdx.x];
     const int row = item.x, kvh = item.y % w.kv_heads, length = item.z;
     const int32_t* table = kv.tables + (size_t)(item.y / w.kv_heads) * kv.table_stride;
     const int split = fast_attention_split(length);
@@ -338,8 +344,9 @@ __global__ __launch_bounds__(256) void fast_attention_merge_kernel(int heads, in
                                                                    int ldo) {
     const int lane = threadIdx.x & 63;
     const int pair = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (pair >= w.merge_count * heads) return;
-    const int2 rs = reinterpret_cast<const int2*>(w.merge_rows)[pair / heads];
+    int2 rs = {0, 0};
+    if (pair / heads < w.merge_capacity) rs = reinterpret_cast<const int2*>(w.merge_rows)[pair / heads];
+    if (pair >= w.counts[2] * heads) return;
     const int row = rs.x, h = pair % heads;
     const int G = heads / kv_heads, kvh = h / G, hg = h % G;
     const int grp = lane >> 4, c = lane & 15;
@@ -381,7 +388,7 @@ __global__ __launch_bounds__(256) void fast_attention_merge_kernel(int heads, in
         }
         gm = rm;
     };
-    load(0, w.max_splits);  // bounded by the batch's longest long row until the row's own count is known
+    load(0, w.split_stride);  // bounded by the most splits a row can have until the row's own count is known
     // The row's position is first needed here, after the loads above are in flight.
     __builtin_amdgcn_sched_barrier(0);
     asm volatile("" : "+v"(pos));
@@ -409,6 +416,10 @@ __global__ __launch_bounds__(256) void fast_attention_merge_kernel(int heads, in
     if (grp == 0) *reinterpret_cast<f4*>(out + act_index<PLAIN>(row, h * kDim + 4 * c, ldo)) = num / den;
 }
 
+// Grids: the step's counts, or with w.capacity_grids the capacities of the
+// lists this step uses (a launch captured once for the steps of one shape,
+// whose lists are empty or not alike; the kernels read each step's counts
+// from w.counts).
 template <int G, bool PLAIN>
 void launch_items(hipStream_t s, const float* qkv, int ldq, const RowMeta& meta, const PagedKv& kv, int layer,
                   const FastAttentionWork& w, float* out, int ldo) {
@@ -416,16 +427,18 @@ void launch_items(hipStream_t s, const float* qkv, int ldq, const RowMeta& meta,
     uint64_t bytes = 0;
     for (int r = 0; r < FastAttentionWork::kPrefetchRanges; ++r) bytes += w.prefetch_bytes[r];
     const uint64_t slices = (bytes + 64 * 128 - 1) / (64 * 128);
-    if (w.short_count > 0) {
+    const int items = w.capacity_grids && w.items_count > 0 ? w.items_capacity : w.items_count;
+    const int shorts = w.capacity_grids && w.short_count > 0 ? w.short_capacity : w.short_count;
+    if (shorts > 0) {
         // Without split items (whose launch covers the slices), enough
         // work-groups for every slice.
-        int groups = w.short_count;
-        if (w.items_count <= 0)
+        int groups = shorts;
+        if (items <= 0)
             groups = (int)std::max<uint64_t>((uint64_t)groups, (slices + kSplitPages - 1) / kSplitPages);
         fast_attention_short_kernel<G, PLAIN><<<groups, kSplitPages * 64, 0, s>>>(qkv, ldq, meta, kv, layer, w, out, ldo);
     }
-    if (w.items_count > 0) {
-        const uint64_t waves = std::max<uint64_t>((uint64_t)w.items_count, slices);
+    if (items > 0) {
+        const uint64_t waves = std::max<uint64_t>((uint64_t)items, slices);
         fast_attention_kernel<G, PLAIN><<<(int)((waves + kItemsPerGroup - 1) / kItemsPerGroup), kItemsPerGroup * 64, 0,
                                    s>>>(qkv, ldq, meta, kv, layer, w, out, ldo);
     }
@@ -441,9 +454,9 @@ hipError_t launch_all(hipStream_t s, const float* qkv, int ldq, int heads, int k
     default: launch_items<4, PLAIN>(s, qkv, ldq, meta, kv, layer, w, out, ldo); break;
     }
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess || w.items_count <= 0 || w.merge_count <= 0) return e;
-    fast_attention_merge_kernel<PLAIN>
-        <<<(w.merge_count * heads + 3) / 4, 256, 0, s>>>(heads, kv_heads, meta, w, out, ldo);
+    const int merges = w.capacity_grids && w.merge_count > 0 ? w.merge_capacity : w.merge_count;
+    if (e != hipSuccess || w.items_count <= 0 || merges <= 0) return e;
+    fast_attention_merge_kernel<PLAIN><<<(merges * heads + 3) / 4, 256, 0, s>>>(heads, kv_heads, meta, w, out, ldo);
     return hipGetLastError();
 }
 
@@ -455,7 +468,9 @@ hipError_t launch_fast_attention(hipStream_t s, const float* qkv, int ldq, int r
     const int G = heads / kv_heads;
     if (rows <= 0) return hipSuccess;
     if (kv.block_tokens != kPage || kv.kv_width != kv_heads * kDim || G > kMaxGroup || G < 1 ||
-        G * kv_heads != heads || w.kv_heads != kv_heads || (w.items_count > 0 && w.split_stride < w.max_splits))
+        G * kv_heads != heads || w.kv_heads != kv_heads || (w.items_count > 0 && w.split_stride < w.max_splits) ||
+        !w.counts || w.items_count > w.items_capacity || w.short_count > w.short_capacity ||
+        w.merge_count > w.merge_capacity)
         return hipErrorInvalidValue;
     return plain ? launch_all<true>(s, qkv, ldq, heads, kv_heads, meta, kv, layer, out, ldo, w)
                  : launch_all<false>(s, qkv, ldq, heads, kv_heads, meta, kv, layer, out, ldo, w);

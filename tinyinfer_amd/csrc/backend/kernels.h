@@ -173,23 +173,29 @@ inline int fast_attention_item_w(int tokens, int split_index, int split_tokens) 
     return tokens | (split_index << 9) | (lg << 24);
 }
 struct FastAttentionWork {
+    // The lists' lengths as the kernels read them: device int32 [3] = split
+    // items, short items, merged rows (equal to the host counts below).
+    const int32_t* counts;
     // splits of the rows longer than 256 tokens (fast_attention_item_w), in
     // any order (the forward puts every row's whole splits before the
     // shorter last ones)
     const int32_t* items;
-    int items_count;
+    int items_count, items_capacity;
     // per row of up to 256 tokens and KV head (int4): row, table slot *
     // kv_heads + KV head, tokens, 0
     const int32_t* short_items;
-    int short_count;
+    int short_count, short_capacity;
     // the rows whose splits the merge kernel combines (the one-token rows
     // longer than 256 tokens), as (row, sequence) int32 pairs
     const int32_t* merge_rows;
-    int merge_count;
+    int merge_count, merge_capacity;
+    // Grids sized by the capacities instead of the counts (a launch that a
+    // graph replays for several steps).
+    bool capacity_grids;
     // Splits of the longest row (of those longer than 256 tokens; 0 if
-    // none), the bound of the merge's first round of loads; the partial
-    // results of (sequence, KV head, split) sit at slot (sequence *
-    // kv_heads + KV head) * split_stride + split, split_stride >= max_splits.
+    // none); the partial results of (sequence, KV head, split) sit at slot
+    // (sequence * kv_heads + KV head) * split_stride + split, split_stride >=
+    // max_splits (the merge's first round of loads is bounded by it).
     int max_splits;
     int split_stride;
     float* partial_out;  // [slot][G][64]
