@@ -452,23 +452,36 @@ def summarise_counters(fetch_csv: str, write_csv: str, bench_json: str, out: str
 
 def summarise_trace(trace_csv: str, steps: str, out: str, command: str):
     """Markdown table of a rocprofv3 --kernel-trace run of bench.py: every
-    kernel of the last `steps` engine steps (a step ends with the LM head's
-    argmax kernel), its launches, average and minimum duration and time per
-    step, then the kernels of one layer in launch order."""
+    kernel of `steps` engine steps (a step ends with the LM head's argmax
+    kernel: "N" for the last N steps, "N+F" for N steps from engine step F,
+    prefill steps included in the count), its launches, average and minimum
+    duration and time per step, then the kernels of one layer in launch
+    order."""
+    first = None
+    if "+" in steps:
+        steps, first = steps.split("+")
+        first = int(first)
     steps = int(steps)
     rows = sorted(csv.DictReader(open(trace_csv)), key=lambda r: int(r["Start_Timestamp"]))
     name = lambda r: r["Kernel_Name"].replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0]
     dur = lambda r: int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
     ends = [i for i, r in enumerate(rows) if "head_argmax_kernel" in name(r)]
-    if len(ends) < steps + 1:
-        raise SystemExit(f"{trace_csv}: {len(ends) - 1} complete steps, {steps} asked for")
-    window = rows[ends[-steps - 1] + 1:ends[-1] + 1]
+    if first is None:
+        if len(ends) < steps + 1:
+            raise SystemExit(f"{trace_csv}: {len(ends) - 1} complete steps, {steps} asked for")
+        window = rows[ends[-steps - 1] + 1:ends[-1] + 1]
+    else:
+        if first < 1 or len(ends) < first + steps:
+            raise SystemExit(f"{trace_csv}: {len(ends)} steps, steps {first}..{first + steps - 1} asked for")
+        window = rows[ends[first - 1] + 1:ends[first + steps - 1] + 1]
+        steps_text = f"steps {first}..{first + steps - 1}"
     span = int(window[-1]["End_Timestamp"]) - int(window[0]["Start_Timestamp"])
     busy = sum(dur(r) for r in window)
     per = defaultdict(list)
     for r in window:
         per[(name(r), r["Grid_Size_X"], r["Workgroup_Size_X"])].append(dur(r))
-    lines = [f"# Kernel trace: last {steps} steps", "", f"Command: `{command}`", "",
+    title = f"last {steps} steps" if first is None else f"{steps} engine {steps_text} (0-based, prefill included)"
+    lines = [f"# Kernel trace: {title}", "", f"Command: `{command}`", "",
              f"Trace: {steps} steps in {span / 1e6:.3f} ms on the GPU clock ({span / 1e3 / steps:.1f} us per step "
              f"under the profiler); kernels busy {busy / 1e6:.3f} ms ({busy / 1e3 / steps:.1f} us per step).", "",
              "| kernel | grid (threads) | work-group | launches | avg us | min us | us per step | % of busy |",
@@ -583,7 +596,8 @@ def main():
     ap.add_argument("--summarise-sq", nargs=4, metavar=("COUNTER_CSV", "TRACE_CSV", "OUT", "COMMAND"),
                     help="markdown summary of a rocprofv3 --pmc run of this script with the SQ counters")
     ap.add_argument("--summarise-trace", nargs=4, metavar=("TRACE_CSV", "STEPS", "OUT", "COMMAND"),
-                    help="markdown summary of a rocprofv3 --kernel-trace run of this script")
+                    help="markdown summary of a rocprofv3 --kernel-trace run of this script (STEPS: N, the last N "
+                         "engine steps, or N+F, N steps from engine step F)")
     args = ap.parse_args()
     if args.summarise_sq:
         summarise_sq(*args.summarise_sq)

@@ -46,6 +46,11 @@ struct mp_hip {
     float* head = nullptr;           // [vocab, hidden]: the embedding when tied
     float* final_norm = nullptr;     // [hidden]
     std::vector<float*> input_norm, post_norm, qkv, o, gate, up, down;
+    // Fast arithmetic: the projections also row-major [out][in] (q|k|v in
+    // natural column order) for the one-sequence decode steps' GEMV
+    // (fast_gemv.hip), where the shape allows.
+    bool gemv = false;
+    std::vector<float*> qkv_rows, o_rows, gate_rows, up_rows, down_rows;
     std::vector<unsigned char> uploaded;  // per (layer, slot) + model tensors
     // paged KV
     float* keys = nullptr;
@@ -493,6 +498,10 @@ int mp_hip_create(const mp_model_desc* model, const mp_kv_desc* kv, mp_hip** out
     if (c.tied) h->head = h->embedding;
     else alloc_weights(&h->head, (size_t)c.vocabulary * hd);
     alloc_weights(&h->final_norm, hd);
+    h->gemv = h->fast && kv->block_tokens == 16 && c.heads / c.kv_heads <= 4 &&
+              mphip::gemv_fits(c.hidden, c.intermediate, c.heads, c.kv_heads);
+    for (auto* v : {&h->qkv_rows, &h->o_rows, &h->gate_rows, &h->up_rows, &h->down_rows})
+        v->assign(h->gemv ? c.layers : 0, nullptr);
     for (int l = 0; l < c.layers; ++l) {
         alloc_weights(&h->input_norm[l], hd);
         alloc_weights(&h->post_norm[l], hd);
@@ -501,6 +510,13 @@ int mp_hip_create(const mp_model_desc* model, const mp_kv_desc* kv, mp_hip** out
         alloc_weights(&h->gate[l], hd * c.intermediate);
         alloc_weights(&h->up[l], hd * c.intermediate);
         alloc_weights(&h->down[l], hd * c.intermediate);
+        if (h->gemv) {
+            alloc_weights(&h->qkv_rows[l], hd * qkv_width(c));
+            alloc_weights(&h->o_rows[l], hd * hd);
+            alloc_weights(&h->gate_rows[l], hd * c.intermediate);
+            alloc_weights(&h->up_rows[l], hd * c.intermediate);
+            alloc_weights(&h->down_rows[l], hd * c.intermediate);
+        }
     }
     // Pools: [block][layer][slot][kv_width] (miniprefix/src/kv/paged_kv.cpp:53-56).
     h->pool_elements = (size_t)kv->max_blocks * c.layers * kv->block_tokens * kv_width(c);
@@ -583,11 +599,17 @@ int mp_hip_upload_tensor(mp_hip* h, int32_t layer, int32_t slot, const float* da
     // Fast mode with 64-wide heads: q and k pair-permuted for the RoPE
     // projection (fast_rope_column).
     const bool rope = h->fast && c.hidden / c.heads == 64 && (slot == MP_TENSOR_Q || slot == MP_TENSOR_K);
-    auto transposed = [&](float* dst, int rows, int cols) -> hipError_t {
+    // `rows_dst`: the row-major copy of the GEMV path (fast mode), or null.
+    auto transposed = [&](float* dst, int rows, int cols, float* rows_dst = nullptr) -> hipError_t {
         hipError_t r = staged();
         if (r != hipSuccess) return r;
-        return h->fast ? mphip::launch_to_fragments(h->stream, h->staging, dst, cols, rows, true, layer >= 0 && rope)
-                       : mphip::launch_transpose(h->stream, h->staging, dst, rows, cols, rows);
+        r = h->fast ? mphip::launch_to_fragments(h->stream, h->staging, dst, cols, rows, true, layer >= 0 && rope)
+                    : mphip::launch_transpose(h->stream, h->staging, dst, rows, cols, rows);
+        if (r == hipSuccess && rows_dst) r = mphip::launch_transpose(h->stream, h->staging, rows_dst, rows, cols, rows);
+        return r;
+    };
+    auto row_copy = [&](const std::vector<float*>& v, size_t offset) -> float* {
+        return h->gemv ? v[layer] + offset : nullptr;
     };
     if (layer < 0) {
         if (slot == MP_TENSOR_EMBEDDING) {
@@ -608,13 +630,15 @@ int mp_hip_upload_tensor(mp_hip* h, int32_t layer, int32_t slot, const float* da
         switch (slot) {
         case MP_TENSOR_INPUT_NORM: e = hipMemcpyAsync(h->input_norm[layer], data, bytes, h2d, h->stream); break;
         case MP_TENSOR_POST_NORM: e = hipMemcpyAsync(h->post_norm[layer], data, bytes, h2d, h->stream); break;
-        case MP_TENSOR_Q: e = transposed(qkv, hd, hd); break;
-        case MP_TENSOR_K: e = transposed(qkv + (size_t)hd * hd, hd, kvw); break;
-        case MP_TENSOR_V: e = transposed(qkv + (size_t)(hd + kvw) * hd, hd, kvw); break;
-        case MP_TENSOR_O: e = transposed(h->o[layer], hd, hd); break;
-        case MP_TENSOR_GATE: e = transposed(h->gate[layer], hd, in); break;
-        case MP_TENSOR_UP: e = transposed(h->up[layer], hd, in); break;
-        case MP_TENSOR_DOWN: e = transposed(h->down[layer], in, hd); break;
+        case MP_TENSOR_Q: e = transposed(qkv, hd, hd, row_copy(h->qkv_rows, 0)); break;
+        case MP_TENSOR_K: e = transposed(qkv + (size_t)hd * hd, hd, kvw, row_copy(h->qkv_rows, (size_t)hd * hd)); break;
+        case MP_TENSOR_V:
+            e = transposed(qkv + (size_t)(hd + kvw) * hd, hd, kvw, row_copy(h->qkv_rows, (size_t)(hd + kvw) * hd));
+            break;
+        case MP_TENSOR_O: e = transposed(h->o[layer], hd, hd, row_copy(h->o_rows, 0)); break;
+        case MP_TENSOR_GATE: e = transposed(h->gate[layer], hd, in, row_copy(h->gate_rows, 0)); break;
+        case MP_TENSOR_UP: e = transposed(h->up[layer], hd, in, row_copy(h->up_rows, 0)); break;
+        case MP_TENSOR_DOWN: e = transposed(h->down[layer], in, hd, row_copy(h->down_rows, 0)); break;
         }
     }
     int status = check(h, e, "upload weights");
@@ -1022,6 +1046,30 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
     // graph_grids the attention grids are sized by the lists' capacities, for
     // a capture that later steps of the same shape replay.
     bool graph_grids = false;
+    // A decode step of one sequence runs its projections as GEMV
+    // (fast_gemv.hip) over the row-major weights; RMSNorm is then computed
+    // inside the q|k|v and gate/up projections, and the sums of squares the
+    // LM head's folded norm reads are taken after the last layer.
+    const bool gemv_rows = h->gemv && fast_decode && nseq == 1;
+    auto gemv = [&](mphip::Epilogue epi, const float* x, int inner, const float* w, const float* w2, int columns,
+                    float* out, const float* norm, int layer) {
+        mphip::GemvArgs a{};
+        a.x = x;
+        a.w = w;
+        a.w2 = w2;
+        a.out = out;
+        a.norm = norm;
+        a.eps = eps;
+        a.inner = inner;
+        a.columns = columns;
+        a.heads = c.heads;
+        a.layer = layer;
+        a.kv = kv;
+        a.meta = meta;
+        a.row_block = h->row_block;
+        a.row_rope = h->row_rope;
+        return mphip::launch_gemv(s, epi, a);
+    };
     auto launch_fast_forward = [&]() -> hipError_t {
         hipError_t e = launch_embedding();
         // Matrix-core projections; RMSNorm folded into the next projection
@@ -1048,7 +1096,7 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
             return mphip::launch_fast_gemm(s, epi, a);
         };
         mphip::FastAttentionWork fw{};
-        fw.counts = h->meta + fast_at;
+        fw.counts = graph_grids ? h->meta + fast_at : nullptr;
         fw.items = h->meta + items_at;
         fw.items_count = (int)fast_items;
         fw.items_capacity = (int)items_capacity;
@@ -1065,9 +1113,12 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
         fw.partial_ml = h->fast_partials + (size_t)h->workspace_seqs * c.kv_heads * split_stride * group_ * 64;
         fw.kv_heads = c.kv_heads;
         auto set_prefetch = [&](int l) {
-            // This layer's remaining projections, then the next layer's q|k|v.
-            const float* ranges[] = {h->o[l], h->gate[l], h->up[l], h->down[l],
-                                     l + 1 < c.layers ? h->qkv[l + 1] : nullptr};
+            // This layer's remaining projections, then the next layer's q|k|v
+            // (the copies the step's projections read).
+            const bool g = gemv_rows;
+            const float* ranges[] = {g ? h->o_rows[l] : h->o[l], g ? h->gate_rows[l] : h->gate[l],
+                                     g ? h->up_rows[l] : h->up[l], g ? h->down_rows[l] : h->down[l],
+                                     l + 1 < c.layers ? (g ? h->qkv_rows[l + 1] : h->qkv[l + 1]) : nullptr};
             const uint64_t bytes[] = {sizeof(float) * hd * hd, sizeof(float) * hd * in, sizeof(float) * hd * in,
                                       sizeof(float) * hd * in,
                                       l + 1 < c.layers ? sizeof(float) * hd * (uint64_t)qw : 0};
@@ -1076,10 +1127,12 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
                 fw.prefetch_bytes[r] = r < 5 && ranges[r] ? bytes[r] : 0;
             }
         };
-        if (e == hipSuccess) e = mphip::launch_fast_ssq(s, h->x, R, hd, h->ssq, ssq_stride);
+        if (e == hipSuccess && !gemv_rows) e = mphip::launch_fast_ssq(s, h->x, R, hd, h->ssq, ssq_stride);
         for (int l = 0; l < c.layers && e == hipSuccess; ++l) {
             layer_now = l;
-            if (fast_decode) {
+            if (gemv_rows) {
+                e = timed(P, [&] { return gemv(mphip::kRope, h->x, hd, h->qkv_rows[l], nullptr, qw, h->qkv_out, h->input_norm[l], l); });
+            } else if (fast_decode) {
                 // q|k|v with RoPE and the KV append in the epilogue.
                 e = timed(P, [&] {
                     mphip::FastGemmArgs a{};
@@ -1132,11 +1185,21 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
                                                 attention_events());
                 }
             }
+            if (gemv_rows) {
+                if (e == hipSuccess) e = timed(P, [&] { return gemv(mphip::kResidual, h->ctx, hd, h->o_rows[l], nullptr, hd, h->x, nullptr, l); });
+                if (e == hipSuccess)
+                    e = timed(P, [&] { return gemv(mphip::kSwiglu, h->x, hd, h->gate_rows[l], h->up_rows[l], in, h->ffn, h->post_norm[l], l); });
+                if (e == hipSuccess) e = timed(P, [&] { return gemv(mphip::kResidual, h->ffn, in, h->down_rows[l], nullptr, hd, h->x, nullptr, l); });
+                continue;
+            }
             if (e == hipSuccess) e = timed(P, [&] { return fast(mphip::kResidual, h->ctx, hd, h->o[l], nullptr, hd, h->x, nullptr); });
             if (e == hipSuccess)
                 e = timed(P, [&] { return fast(mphip::kSwiglu, h->x, hd, h->gate[l], h->up[l], in, h->ffn, h->post_norm[l]); });
             if (e == hipSuccess) e = timed(P, [&] { return fast(mphip::kResidual, h->ffn, in, h->down[l], nullptr, hd, h->x, nullptr); });
         }
+        // The LM head's folded norm reads per-16-column sums of squares, which
+        // the GEMV projections do not write.
+        if (e == hipSuccess && gemv_rows) e = mphip::launch_fast_ssq(s, h->x, R, hd, h->ssq, ssq_stride);
         layer_now = sampled ? -2 : -1;
         if (e == hipSuccess) e = timed(MP_TIME_HEAD, [&] {
             mphip::FastGemmArgs a{};
@@ -1382,7 +1445,6 @@ int mp_hip_paged_attention_decode_fast(const float* q, const float* keys, const 
     int32_t* const dev = reinterpret_cast<int32_t*>(buffer);
     e = hipMemcpyAsync(dev, host.data(), ints * sizeof(int32_t), hipMemcpyHostToDevice, s);
     mphip::FastAttentionWork w{};
-    w.counts = dev;
     w.items = dev + counts.size();
     w.items_count = w.items_capacity = counts[0];
     w.short_items = w.items + split_items.size();

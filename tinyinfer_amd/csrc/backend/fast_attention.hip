@@ -230,12 +230,11 @@ __global__ __launch_bounds__(kItemsPerGroup * 64) void fast_attention_kernel(con
     __shared__ float p_s[kItemsPerGroup][G][kPage];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int index = blockIdx.x * kItemsPerGroup + wave;
-    // The item (within the list's capacity) and the count are loaded
-    // together; the count lives in device memory so that a captured launch
-    // of capacity-sized grids serves every step.
+    // The item (within the list's capacity) and, for a launch that a graph
+    // replays, the step's count from device memory are loaded together.
     int4 item = {0, 0, 0, 0};
     if (index < w.items_capacity) item = reinterpret_cast<const int4*>(w.items)[index];
-    if (index >= w.counts[0]) {
+    if (index >= (w.counts ? w.counts[0] : w.items_count)) {
         // A wavefront past the items (batches with few splits) only touches
         // its slice of the weights to prefetch.
         const float touched = touch_weights(w, (uint64_t)index, lane);
@@ -279,7 +278,7 @@ __global__ __launch_bounds__(kSplitPages * 64) void fast_attention_short_kernel(
     // count.
     int4 item = {0, 0, 1, 0};
     if ((int)blockIdx.x < w.short_capacity) item = reinterpret_cast<const int4*>(w.short_items)[blockIdx.x];
-    if ((int)blockIdx.x >= w.counts[1]) {
+    if ((int)blockIdx.x >= (w.counts ? w.counts[1] : w.short_count)) {
         // A work-group past the items (small batches, whose items leave
         // most CUs idle) only touches its slices of the weights to prefetch.
         const float touched = touch_weights(w, (uint64_t)blockIdx.x * kSplitPages + wave, lane);
@@ -346,7 +345,7 @@ __global__ __launch_bounds__(256) void fast_attention_merge_kernel(int heads, in
     const int pair = blockIdx.x * 4 + (threadIdx.x >> 6);
     int2 rs = {0, 0};
     if (pair / heads < w.merge_capacity) rs = reinterpret_cast<const int2*>(w.merge_rows)[pair / heads];
-    if (pair >= w.counts[2] * heads) return;
+    if (pair >= (w.counts ? w.counts[2] : w.merge_count) * heads) return;
     const int row = rs.x, h = pair % heads;
     const int G = heads / kv_heads, kvh = h / G, hg = h % G;
     const int grp = lane >> 4, c = lane & 15;
@@ -469,7 +468,7 @@ hipError_t launch_fast_attention(hipStream_t s, const float* qkv, int ldq, int r
     if (rows <= 0) return hipSuccess;
     if (kv.block_tokens != kPage || kv.kv_width != kv_heads * kDim || G > kMaxGroup || G < 1 ||
         G * kv_heads != heads || w.kv_heads != kv_heads || (w.items_count > 0 && w.split_stride < w.max_splits) ||
-        !w.counts || w.items_count > w.items_capacity || w.short_count > w.short_capacity ||
+        (w.capacity_grids && !w.counts) || w.items_count > w.items_capacity || w.short_count > w.short_capacity ||
         w.merge_count > w.merge_capacity)
         return hipErrorInvalidValue;
     return plain ? launch_all<true>(s, qkv, ldq, heads, kv_heads, meta, kv, layer, out, ldo, w)

@@ -132,6 +132,32 @@ hipError_t launch_fast_gemm(hipStream_t s, Epilogue epilogue, const FastGemmArgs
 // into ssq[p*stride + row], for the first RMSNorm after the embedding.
 hipError_t launch_fast_ssq(hipStream_t s, const float* x, int rows, int width, float* ssq, int stride);
 
+// Fast-mode projections of a decode step of one sequence (fast_gemv.hip):
+// GEMV on the vector ALU over row-major [columns][inner] weights, one
+// wavefront per output (per RoPE pair for kRope). x and out are row 0 of
+// quad-layout matrices (`inner` and `columns` wide). kRope: RMSNorm (weights
+// `norm`, eps) then q|k|v of `heads` query and kv.kv_width/64 KV heads in
+// natural column order, RoPE at the row's position (meta.row_pos[0],
+// row_rope[0], page row_block[0]), q into out, K and V into the pools of
+// `kv` at `layer`; kResidual: out += x W^T (no norm); kSwiglu: RMSNorm then
+// the SwiGLU of the w (gate) and w2 (up) rows. Shapes: inner 576 (kRope,
+// kSwiglu, kResidual) or 1536 (kResidual), head dim 64.
+struct GemvArgs {
+    const float* x;
+    const float* w;
+    const float* w2;
+    float* out;
+    const float* norm;
+    float eps;
+    int inner, columns, heads, layer;
+    PagedKv kv;
+    RowMeta meta;
+    const int32_t* row_block;
+    const float* row_rope;
+};
+bool gemv_fits(int hidden, int intermediate, int heads, int kv_heads);
+hipError_t launch_gemv(hipStream_t s, Epilogue epilogue, const GemvArgs& args);
+
 // Fast-mode decode attention (fast_attention.hip): every row is one new
 // token (already rotated q, its K/V already in the pools). Flash-decoding
 // split over the context: work item (row, KV head, split of
@@ -173,8 +199,9 @@ inline int fast_attention_item_w(int tokens, int split_index, int split_tokens) 
     return tokens | (split_index << 9) | (lg << 24);
 }
 struct FastAttentionWork {
-    // The lists' lengths as the kernels read them: device int32 [3] = split
-    // items, short items, merged rows (equal to the host counts below).
+    // With capacity_grids, the lists' lengths as the kernels read them:
+    // device int32 [3] = split items, short items, merged rows (equal to the
+    // host counts below); null otherwise (the kernels take the host counts).
     const int32_t* counts;
     // splits of the rows longer than 256 tokens (fast_attention_item_w), in
     // any order (the forward puts every row's whole splits before the
