@@ -181,40 +181,47 @@ def test_fast_long_rows_merge_many_splits(torch_cuda, key_scale):
 def test_fast_decode_rows_same_in_mixed_steps(torch_cuda):
     """A decoding row's logits are bit-identical whether its step only
     decodes or also prefills another sequence: one-token rows take the
-    decode attention in both (rows of 120 tokens: one work-group; 700
-    tokens: splits and merge), the prefilling rows the row-block kernels.
-    In the mixed step every row is also checked against the oracle."""
+    decode attention in both (rows of 64, 119 and 200 tokens: one
+    work-group; 450 and 699 tokens: splits and merge), the prefilling rows
+    the matrix-core prefill kernel, and with five decoding sequences both
+    steps run the matrix-core projections (steps of up to four decoding
+    sequences run the GEMV projections instead, which sum in another
+    order). In the mixed step every row is also checked against the
+    oracle."""
     cfg = smollm_config(layers=2, context=1024, vocabulary=4096)
     model = OracleModel(cfg, seed=53)
     bt, o = 16, Oracle()
-    lengths = [119, 699, 300]
+    lengths = [119, 699, 200, 450, 64, 300]  # the last one prefills in the mixed step
+    dec = len(lengths) - 1
     prompts = [[int(t) for t in o.fill_tokens(L, 53, 9500 + i, cfg["vocabulary"])] for i, L in enumerate(lengths)]
-    tables = [np.arange(60 * i, 60 * i + 60, dtype=np.int32) for i in range(3)]
+    tables = [np.arange(60 * i, 60 * i + 60, dtype=np.int32) for i in range(len(lengths))]
+    blocks = 60 * len(lengths)
 
     def run(mixed):
-        backend = HipBackend(cfg, block_tokens=bt, max_blocks=180, max_sequences=3, arithmetic=ARITHMETIC_FAST)
+        backend = HipBackend(cfg, block_tokens=bt, max_blocks=blocks, max_sequences=len(lengths),
+                             arithmetic=ARITHMETIC_FAST)
         upload_model(backend, model)
         for i, t in enumerate(tables):
             backend.table_write(i, 0, t)
-        am, _ = backend.forward([(0, 0, lengths[0]), (1, 0, lengths[1])], prompts[0] + prompts[1])
-        nxt = [int(am[0]), int(am[1])]
-        steps = [(0, lengths[0], 1), (1, lengths[1], 1)] + ([(2, 0, lengths[2])] if mixed else [])
-        _, got = backend.forward(steps, nxt + (prompts[2] if mixed else []))
+        am, _ = backend.forward([(i, 0, lengths[i]) for i in range(dec)], [t for p in prompts[:dec] for t in p])
+        nxt = [int(a) for a in am]
+        steps = [(i, lengths[i], 1) for i in range(dec)] + ([(dec, 0, lengths[dec])] if mixed else [])
+        _, got = backend.forward(steps, nxt + (prompts[dec] if mixed else []))
         backend.close()
         return nxt, got
 
     nxt, alone = run(False)
     nxt_mixed, mixed = run(True)
     assert nxt == nxt_mixed
-    for i in range(2):
+    for i in range(dec):
         assert np.array_equal(alone[i].view(np.uint32), mixed[i].view(np.uint32)), f"row {i}"
-    n = pool_elements(cfg, bt, 180)
+    n = pool_elements(cfg, bt, blocks)
     keys, values = np.zeros(n, dtype=np.float32), np.zeros(n, dtype=np.float32)
-    for i in range(2):
+    for i in range(dec):
         model.append(keys, values, bt, tables[i], 0, prompts[i])
-    want = [model.append(keys, values, bt, tables[i], lengths[i], [nxt[i]]) for i in range(2)]
-    want.append(model.append(keys, values, bt, tables[2], 0, prompts[2]))
-    for i in range(3):
+    want = [model.append(keys, values, bt, tables[i], lengths[i], [nxt[i]]) for i in range(dec)]
+    want.append(model.append(keys, values, bt, tables[dec], 0, prompts[dec]))
+    for i in range(len(lengths)):
         assert rel_inf(mixed[i], want[i]) <= 1e-3, f"row {i}: relative error {rel_inf(mixed[i], want[i]):.3e}"
 
 
@@ -294,47 +301,54 @@ def test_fast_prefill_climbing_scores(torch_cuda):
     assert np.array_equal(one[-1].view(np.uint32), three[-1].view(np.uint32))
 
 
-def test_fast_single_sequence_decode_gemv(torch_cuda):
-    """Decode steps of one sequence take the GEMV projections (row-major
-    weights, RMSNorm computed inside the projections): 90 teacher-forced
-    steps from a 200-token prompt, crossing from the short-row attention
-    to the splits at 256 tokens, each within 1e-3 relative of the oracle
-    with the oracle's greedy token; the same row decoded beside two others
-    (matrix-core projections) stays within 1e-3 of the oracle too."""
+def test_fast_small_batch_decode_gemv(torch_cuda):
+    """Decode steps of up to four sequences take the GEMV projections
+    (row-major weights, RMSNorm computed inside the projections): 90
+    teacher-forced steps of one sequence from a 200-token prompt, crossing
+    from the short-row attention to the splits at 256 tokens, each within
+    1e-3 relative of the oracle with the oracle's greedy token; the same row
+    decoded beside two others gives bit-identical logits (each row's sums
+    are its own), and beside five others (matrix-core projections) it stays
+    within 1e-3 of the oracle too."""
     cfg = smollm_config(layers=2, context=512, vocabulary=4096)
     model = OracleModel(cfg, seed=97)
     o = Oracle()
     bt = 16
     prompt = [int(t) for t in o.fill_tokens(200, 97, 9990, cfg["vocabulary"])]
-    others = [[int(t) for t in o.fill_tokens(n, 97, 9991 + i, cfg["vocabulary"])] for i, n in enumerate((90, 300))]
-    n = pool_elements(cfg, bt, 96)
+    lengths = (90, 300, 40, 120, 230)
+    others = [[int(t) for t in o.fill_tokens(n, 97, 9991 + i, cfg["vocabulary"])] for i, n in enumerate(lengths)]
+    n = pool_elements(cfg, bt, 192)
     keys, values = np.zeros(n, np.float32), np.zeros(n, np.float32)
     table = np.arange(32, dtype=np.int32)
     want = model.append(keys, values, bt, table, 0, prompt)
-    solo = HipBackend(cfg, block_tokens=bt, max_blocks=96, max_sequences=3, arithmetic=ARITHMETIC_FAST)
-    batch = HipBackend(cfg, block_tokens=bt, max_blocks=96, max_sequences=3, arithmetic=ARITHMETIC_FAST)
-    for backend in (solo, batch):
+    sizes = (1, 3, 6)  # GEMV alone and beside two others; matrix cores beside five
+    backends = [HipBackend(cfg, block_tokens=bt, max_blocks=192, max_sequences=6, arithmetic=ARITHMETIC_FAST)
+                for _ in sizes]
+    for backend, size in zip(backends, sizes):
         upload_model(backend, model)
-        for i in range(3):
+        for i in range(6):
             backend.table_write(i, 0, np.arange(32 * i, 32 * i + 32, dtype=np.int32))
-    solo.forward([(0, 0, 200)], prompt)
-    batch.forward([(0, 0, 200), (1, 0, 90), (2, 0, 300)], prompt + others[0] + others[1])
-    used = [200, 90, 300]
-    nxt_others = [0, 0]
+        backend.forward([(0, 0, 200)] + [(i + 1, 0, lengths[i]) for i in range(size - 1)],
+                        prompt + [t for p in others[:size - 1] for t in p])
+    used = [200] + list(lengths)
+    nxt = [0] * 6
     worst = 0.0
     for step in range(90):
         token = int(np.argmax(want))
-        am, got = solo.forward([(0, used[0], 1)], [token])
-        _, got3 = batch.forward([(0, used[0], 1), (1, used[1], 1), (2, used[2], 1)], [token] + nxt_others)
-        nxt_others = [int(np.argmax(got3[1])), int(np.argmax(got3[2]))]
+        outs = []
+        for backend, size in zip(backends, sizes):
+            am, got = backend.forward([(i, used[i], 1) for i in range(size)], [token] + nxt[1:size])
+            assert am[0] == int(np.argmax(got[0]))
+            outs.append(got)
+        nxt[1:] = [int(np.argmax(g)) for g in outs[2][1:]]
         want = model.append(keys, values, bt, table, used[0], [token])
-        for label, g in (("alone", got[0]), ("in a batch", got3[0])):
+        assert np.array_equal(outs[0][0].view(np.uint32), outs[1][0].view(np.uint32)), f"step {step}"
+        for label, g in (("alone", outs[0][0]), ("beside five", outs[2][0])):
             err = rel_inf(g, want)
             worst = max(worst, err)
             assert err <= 1e-3, f"step {step} ({label}): relative error {err:.3e}"
             assert int(np.argmax(g)) == int(np.argmax(want)) or margin(want) < 1e-5, f"step {step} ({label})"
-        assert am[0] == int(np.argmax(got[0]))
         used = [u + 1 for u in used]
-    solo.close()
-    batch.close()
+    for backend in backends:
+        backend.close()
     print(f"max relative logit error {worst:.3e}")

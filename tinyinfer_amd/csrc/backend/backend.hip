@@ -47,8 +47,8 @@ struct mp_hip {
     float* final_norm = nullptr;     // [hidden]
     std::vector<float*> input_norm, post_norm, qkv, o, gate, up, down;
     // Fast arithmetic: the projections also row-major [out][in] (q|k|v in
-    // natural column order) for the one-sequence decode steps' GEMV
-    // (fast_gemv.hip), where the shape allows.
+    // natural column order) for the GEMV of decode steps of up to four
+    // sequences (fast_gemv.hip), where the shape allows.
     bool gemv = false;
     std::vector<float*> qkv_rows, o_rows, gate_rows, up_rows, down_rows;
     std::vector<unsigned char> uploaded;  // per (layer, slot) + model tensors
@@ -1046,14 +1046,15 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
     // graph_grids the attention grids are sized by the lists' capacities, for
     // a capture that later steps of the same shape replay.
     bool graph_grids = false;
-    // A decode step of one sequence runs its projections as GEMV
+    // A decode step of up to four sequences runs its projections as GEMV
     // (fast_gemv.hip) over the row-major weights; RMSNorm is then computed
     // inside the q|k|v and gate/up projections, and the sums of squares the
     // LM head's folded norm reads are taken after the last layer.
-    const bool gemv_rows = h->gemv && fast_decode && nseq == 1;
+    const bool gemv_rows = h->gemv && fast_decode && nseq <= mphip::kGemvRows;
     auto gemv = [&](mphip::Epilogue epi, const float* x, int inner, const float* w, const float* w2, int columns,
                     float* out, const float* norm, int layer) {
         mphip::GemvArgs a{};
+        a.rows = R;
         a.x = x;
         a.w = w;
         a.w2 = w2;

@@ -132,16 +132,17 @@ hipError_t launch_fast_gemm(hipStream_t s, Epilogue epilogue, const FastGemmArgs
 // into ssq[p*stride + row], for the first RMSNorm after the embedding.
 hipError_t launch_fast_ssq(hipStream_t s, const float* x, int rows, int width, float* ssq, int stride);
 
-// Fast-mode projections of a decode step of one sequence (fast_gemv.hip):
-// GEMV on the vector ALU over row-major [columns][inner] weights, one
-// wavefront per output (per RoPE pair for kRope). x and out are row 0 of
-// quad-layout matrices (`inner` and `columns` wide). kRope: RMSNorm (weights
-// `norm`, eps) then q|k|v of `heads` query and kv.kv_width/64 KV heads in
-// natural column order, RoPE at the row's position (meta.row_pos[0],
-// row_rope[0], page row_block[0]), q into out, K and V into the pools of
-// `kv` at `layer`; kResidual: out += x W^T (no norm); kSwiglu: RMSNorm then
-// the SwiGLU of the w (gate) and w2 (up) rows. Shapes: inner 576 (kRope,
-// kSwiglu, kResidual) or 1536 (kResidual), head dim 64.
+// Fast-mode projections of a decode step of up to four sequences
+// (fast_gemv.hip): GEMV on the vector ALU over row-major [columns][inner]
+// weights, one wavefront per output (per RoPE pair for kRope). x and out are
+// rows 0..rows-1 of quad-layout matrices (`inner` and `columns` wide).
+// kRope: RMSNorm (weights `norm`, eps) then q|k|v of `heads` query and
+// kv.kv_width/64 KV heads in natural column order, RoPE at each row's
+// position (meta.row_pos[r], row_rope[r], page row_block[r]), q into out, K
+// and V into the pools of `kv` at `layer`; kResidual: out += x W^T (no
+// norm); kSwiglu: RMSNorm then the SwiGLU of the w (gate) and w2 (up) rows.
+// Shapes: inner 576 (kRope, kSwiglu, kResidual) or 1536 (kResidual), head
+// dim 64, rows 1..4. A row's result does not depend on the other rows.
 struct GemvArgs {
     const float* x;
     const float* w;
@@ -149,12 +150,13 @@ struct GemvArgs {
     float* out;
     const float* norm;
     float eps;
-    int inner, columns, heads, layer;
+    int rows, inner, columns, heads, layer;
     PagedKv kv;
     RowMeta meta;
     const int32_t* row_block;
     const float* row_rope;
 };
+constexpr int kGemvRows = 4;
 bool gemv_fits(int hidden, int intermediate, int heads, int kv_heads);
 hipError_t launch_gemv(hipStream_t s, Epilogue epilogue, const GemvArgs& args);
 
