@@ -75,8 +75,12 @@ def test_fast_prefill_and_decode_track_the_oracle(torch_cuda, shape):
 
 
 def test_fast_rows_do_not_depend_on_the_batch(torch_cuda):
-    """70 sequences (two row tiles) decoded together and in small groups give
-    bit-identical logits: no row's sums depend on the other rows."""
+    """70 sequences (two row tiles) decoded together and in groups of 10
+    give bit-identical logits on the matrix cores, and decoded in groups of
+    4 and one by one bit-identical logits on the GEMV projections: no row's
+    sums depend on the other rows of its step. (Decode steps of up to four
+    sequences take the GEMV projections, larger ones the matrix cores, whose
+    summation orders differ; both are held to the oracle elsewhere.)"""
     cfg = smollm_config(layers=1, context=512, vocabulary=4096)
     model = OracleModel(cfg, seed=43)
     bt, count = 16, 70
@@ -84,8 +88,11 @@ def test_fast_rows_do_not_depend_on_the_batch(torch_cuda):
     lengths = [int(x) for x in 5 + o.fill_tokens(count, 43, 9200, 120)]
     prompts = [[int(t) for t in o.fill_tokens(L, 43, 9300 + i, cfg["vocabulary"])] for i, L in enumerate(lengths)]
     results = {}
-    for label, groups in (("together", [list(range(count))]), ("apart", [list(range(i, min(i + 7, count)))
-                                                                         for i in range(0, count, 7)])):
+    def split(size):
+        return [list(range(i, min(i + size, count))) for i in range(0, count, size)]
+
+    for label, groups in (("together", [list(range(count))]), ("tens", split(10)), ("fours", split(4)),
+                          ("ones", split(1))):
         backend = HipBackend(cfg, block_tokens=bt, max_blocks=count * 10, max_sequences=count,
                              arithmetic=ARITHMETIC_FAST)
         upload_model(backend, model)
@@ -105,7 +112,13 @@ def test_fast_rows_do_not_depend_on_the_batch(torch_cuda):
         results[label] = out
         backend.close()
     for key, v in results["together"].items():
-        assert np.array_equal(v.view(np.uint32), results["apart"][key].view(np.uint32)), key
+        if key[1] == 0:
+            continue  # prefill steps run the same kernels whatever the grouping; compared below too
+        assert np.array_equal(v.view(np.uint32), results["tens"][key].view(np.uint32)), key
+        assert np.array_equal(results["fours"][key].view(np.uint32), results["ones"][key].view(np.uint32)), key
+    for key, v in results["together"].items():
+        if key[1] == 0:
+            assert np.array_equal(v.view(np.uint32), results["ones"][key].view(np.uint32)), key
 
 
 
@@ -181,17 +194,16 @@ def test_fast_long_rows_merge_many_splits(torch_cuda, key_scale):
 def test_fast_decode_rows_same_in_mixed_steps(torch_cuda):
     """A decoding row's logits are bit-identical whether its step only
     decodes or also prefills another sequence: one-token rows take the
-    decode attention in both (rows of 64, 119 and 200 tokens: one
-    work-group; 450 and 699 tokens: splits and merge), the prefilling rows
-    the matrix-core prefill kernel, and with five decoding sequences both
-    steps run the matrix-core projections (steps of up to four decoding
-    sequences run the GEMV projections instead, which sum in another
-    order). In the mixed step every row is also checked against the
-    oracle."""
+    decode attention in both (rows of 33 to 200 tokens: one work-group;
+    300 to 699 tokens: splits and merge), the prefilling rows the
+    matrix-core prefill kernel, and with nine decoding sequences both steps
+    run the matrix-core projections (steps of up to four decoding sequences
+    run the GEMV projections instead, which sum in another order). In the
+    mixed step every row is also checked against the oracle."""
     cfg = smollm_config(layers=2, context=1024, vocabulary=4096)
     model = OracleModel(cfg, seed=53)
     bt, o = 16, Oracle()
-    lengths = [119, 699, 200, 450, 64, 300]  # the last one prefills in the mixed step
+    lengths = [119, 699, 200, 450, 64, 80, 330, 520, 33, 300]  # the last one prefills in the mixed step
     dec = len(lengths) - 1
     prompts = [[int(t) for t in o.fill_tokens(L, 53, 9500 + i, cfg["vocabulary"])] for i, L in enumerate(lengths)]
     tables = [np.arange(60 * i, 60 * i + 60, dtype=np.int32) for i in range(len(lengths))]

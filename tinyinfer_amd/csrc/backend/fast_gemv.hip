@@ -7,7 +7,10 @@
 // shapes, one long MFMA chain per wavefront); here every projection spreads
 // over 480 to 1,536 single-wavefront work-groups, and each wavefront issues
 // all its loads at once (down projection 3.0 vs 5.4 us at B = 1, measured in
-// isolation).
+// isolation). Whole decode steps measured faster up to four sequences
+// (0.82 vs 1.01 ms at B = 1, 0.99 vs 1.05 at B = 4) and slower from six
+// (1.12 vs 1.07 ms at B = 6, 1.25 vs 1.07 at B = 8), where each
+// wavefront's loads of every row's activations outweigh the tiles' waste.
 //
 // Lane l takes the float4s l, l + 64, ... of the inner dimension; the
 // products are summed per lane, then over the 64 lanes in a fixed order
