@@ -88,6 +88,9 @@ struct mp_hip {
     // block id): applied on the device at the start of the next forward
     // (or sync), uploaded with that call's metadata.
     std::unordered_map<int32_t, int32_t> pending_tables;
+    // Host copy of the whole table arena (every entry written so far), from
+    // which the forward puts short rows' page ids into their work items.
+    std::vector<int32_t> host_tables;
     // Copies-on-write queued since the last flush, in call order; launched
     // as one kernel at the start of the next forward (or sync), before any
     // kernel reads or writes the pools. No queued copy touches a page
@@ -529,6 +532,7 @@ int mp_hip_create(const mp_model_desc* model, const mp_kv_desc* kv, mp_hip** out
     if (!status) status = device_alloc(h, (void**)&h->tables, table_bytes, "allocate block tables");
     if (!status) status = check(h, hipMemsetAsync(h->tables, 0, table_bytes, h->stream), "clear block tables");
     h->stats.block_table_device_bytes = table_bytes;
+    h->host_tables.assign((size_t)kv->max_sequences * kv->max_sequence_blocks, 0);
     if (!status) {
         std::vector<float> cs, sn;
         rope_tables(c, cs, sn);
@@ -676,7 +680,10 @@ int mp_hip_table_write(mp_hip* h, int32_t slot, int32_t first, const int32_t* bl
     // Queued; the next forward (or sync) uploads the entries with its own
     // metadata and applies them before any kernel reads a table.
     const int32_t base = slot * h->kv.max_sequence_blocks + first;
-    for (int32_t i = 0; i < count; ++i) h->pending_tables[base + i] = blocks[i];
+    for (int32_t i = 0; i < count; ++i) {
+        h->pending_tables[base + i] = blocks[i];
+        h->host_tables[(size_t)base + i] = blocks[i];
+    }
     h->stats.block_table_uploaded_bytes += sizeof(int32_t) * count;
     return MP_OK;
 }
@@ -828,7 +835,7 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
     const size_t fast_at = align4(base_entries);
     const size_t merge_at = fast_at + 4;
     const size_t short_at = merge_at + align4(2 * (size_t)nseq);
-    const size_t items_at = short_at + 4 * (size_t)nseq * c.kv_heads;
+    const size_t items_at = short_at + (size_t)mphip::kShortItemInts * nseq * c.kv_heads;
     const size_t pre_at = fast_rows ? align4(items_at + 4 * fast_items) : fast_at;
     const size_t tables_at = pre_at + 4 * fast_pre;
     const size_t copies_at = tables_at + 2 * table_pairs;
@@ -842,7 +849,8 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
     const size_t chunks_limit = (size_t)score_chunks(c.context);
     const size_t bound = 3 * (size_t)R + 2 * (size_t)nseq + 2 * (size_t)R * (1 + chunks_limit) + 16 +
                          2 * table_pairs + 3 * copies +
-                         (fast_rows ? 4 + 2 * (size_t)nseq + 4 * (size_t)nseq * c.kv_heads + 4 * items_capacity +
+                         (fast_rows ? 4 + 2 * (size_t)nseq + (size_t)mphip::kShortItemInts * nseq * c.kv_heads +
+                                          4 * items_capacity +
                                           4 * ((size_t)R / 16 + (size_t)nseq) * c.kv_heads
                                     : 0);
     if ((status = ensure_call_buffers(h, std::max(entries, bound)))) return status;
@@ -920,11 +928,15 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
                 ++mr;
                 continue;
             }
+            const int length = steps[q].used + 1, pages = (length + 15) / 16;
+            const int32_t* row_table = h->host_tables.data() + (size_t)steps[q].table_slot * h->kv.max_sequence_blocks;
             for (int kvh = 0; kvh < c.kv_heads; ++kvh, ++r) {
-                m_short[4 * r] = m_last[q];
-                m_short[4 * r + 1] = steps[q].table_slot * c.kv_heads + kvh;
-                m_short[4 * r + 2] = steps[q].used + 1;
-                m_short[4 * r + 3] = 0;
+                int32_t* item = m_short + (size_t)mphip::kShortItemInts * r;
+                item[0] = m_last[q];
+                item[1] = steps[q].table_slot * c.kv_heads + kvh;
+                item[2] = length;
+                item[3] = 0;
+                for (int k = 0; k < mphip::kShortItemInts - 4; ++k) item[4 + k] = row_table[std::min(k, pages - 1)];
             }
         }
         // Prefill: (first row, slot * kv_heads + KV head, position, rows) per
@@ -1114,18 +1126,19 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
         fw.partial_ml = h->fast_partials + (size_t)h->workspace_seqs * c.kv_heads * split_stride * group_ * 64;
         fw.kv_heads = c.kv_heads;
         auto set_prefetch = [&](int l) {
-            // This layer's remaining projections, then the next layer's q|k|v
-            // (the copies the step's projections read).
+            // This layer's remaining projections, then the next layer's q|k|v.
+            // Not for the GEMV projections, whose many wavefronts keep their
+            // own loads in flight: at B=1 the prefetch-only work-groups cost
+            // the attention more than they saved (1,346 vs 1,400 tok/s).
             const bool g = gemv_rows;
-            const float* ranges[] = {g ? h->o_rows[l] : h->o[l], g ? h->gate_rows[l] : h->gate[l],
-                                     g ? h->up_rows[l] : h->up[l], g ? h->down_rows[l] : h->down[l],
-                                     l + 1 < c.layers ? (g ? h->qkv_rows[l + 1] : h->qkv[l + 1]) : nullptr};
+            const float* ranges[] = {h->o[l], h->gate[l], h->up[l], h->down[l],
+                                     l + 1 < c.layers ? h->qkv[l + 1] : nullptr};
             const uint64_t bytes[] = {sizeof(float) * hd * hd, sizeof(float) * hd * in, sizeof(float) * hd * in,
                                       sizeof(float) * hd * in,
                                       l + 1 < c.layers ? sizeof(float) * hd * (uint64_t)qw : 0};
             for (int r = 0; r < mphip::FastAttentionWork::kPrefetchRanges; ++r) {
-                fw.prefetch[r] = r < 5 ? ranges[r] : nullptr;
-                fw.prefetch_bytes[r] = r < 5 && ranges[r] ? bytes[r] : 0;
+                fw.prefetch[r] = r < 5 && !g ? ranges[r] : nullptr;
+                fw.prefetch_bytes[r] = r < 5 && !g && ranges[r] ? bytes[r] : 0;
             }
         };
         if (e == hipSuccess && !gemv_rows) e = mphip::launch_fast_ssq(s, h->x, R, hd, h->ssq, ssq_stride);
@@ -1391,6 +1404,9 @@ int mp_hip_paged_attention_decode_fast(const float* q, const float* keys, const 
     // rows as splits (whole splits first) merged afterwards.
     std::vector<int32_t> split_items, short_items, merge_rows, positions(rows);
     int max_splits = 0, longest = 1;
+    // The short rows' page ids go into their items: a host copy of their
+    // table rows.
+    std::vector<int32_t> host_table;
     for (int r = 0; r < rows; ++r) {
         const int length = lengths[r];
         if (length < 1 || (length + 15) / 16 > table_stride) {
@@ -1400,8 +1416,18 @@ int mp_hip_paged_attention_decode_fast(const float* q, const float* keys, const 
         positions[r] = length - 1;
         longest = std::max(longest, length);
         if (mphip::fast_attention_short(length)) {
-            for (int kvh = 0; kvh < kv_heads; ++kvh)
+            const int pages = (length + 15) / 16;
+            host_table.resize(pages);
+            if (hipMemcpy(host_table.data(), tables + (size_t)r * table_stride, sizeof(int32_t) * pages,
+                          hipMemcpyDeviceToHost) != hipSuccess) {
+                mphip::set_free_error("fast paged attention: reading a page table");
+                return MP_DEVICE_ERROR;
+            }
+            for (int kvh = 0; kvh < kv_heads; ++kvh) {
                 short_items.insert(short_items.end(), {r, r * kv_heads + kvh, length, 0});
+                for (int k = 0; k < mphip::kShortItemInts - 4; ++k)
+                    short_items.push_back(host_table[std::min(k, pages - 1)]);
+            }
             continue;
         }
         const int split = mphip::fast_attention_split(length), splits = (length + split - 1) / split;
@@ -1423,7 +1449,8 @@ int mp_hip_paged_attention_decode_fast(const float* q, const float* keys, const 
         }
     // One device buffer: the counts and int32 lists (16-byte aligned), then
     // the partials.
-    const std::vector<int32_t> counts = {(int32_t)(split_items.size() / 4), (int32_t)(short_items.size() / 4),
+    const std::vector<int32_t> counts = {(int32_t)(split_items.size() / 4),
+                                         (int32_t)(short_items.size() / mphip::kShortItemInts),
                                          (int32_t)(merge_rows.size() / 2), 0};
     const size_t ints = counts.size() + split_items.size() + short_items.size() + merge_rows.size() + positions.size();
     const size_t int_bytes = (ints * sizeof(int32_t) + 255) / 256 * 256;

@@ -85,7 +85,8 @@ __device__ __forceinline__ float touch_weights(const FastAttentionWork& w, uint6
 }
 
 // One split: tokens t0..t0+n-1 (t0 page-aligned, at most kMaxPages pages)
-// of the row whose page table is `table`, for the G query heads of KV head
+// of the row whose page ids are `table` (its page table, or the page ids a
+// short item carries), for the G query heads of KV head
 // kvh. Gives per head the reference maximum m, the denominator l and lane
 // d's weighted sum acc (not yet divided). `touch` numbers this wavefront's
 // 8 KB slice of the weight prefetch; p_s is the wavefront's own LDS.
@@ -273,11 +274,12 @@ __global__ __launch_bounds__(kSplitPages * 64) void fast_attention_short_kernel(
     __shared__ float p_s[kSplitPages][G][kPage];
     __shared__ float part_ml[kSplitPages][G][2];
     __shared__ float part_acc[kSplitPages][G][kDim];
-    // (row, slot * kv_heads + KV head, tokens): the length rides in the item,
-    // one dependent load fewer before the pages; loaded together with the
-    // count.
-    int4 item = {0, 0, 1, 0};
-    if ((int)blockIdx.x < w.short_capacity) item = reinterpret_cast<const int4*>(w.short_items)[blockIdx.x];
+    // (row, slot * kv_heads + KV head, tokens, 0, page ids): the length and
+    // the pages ride in the item, loaded together with the count, so the
+    // pages' loads depend on one load only.
+    const int32_t* it = w.short_items + (size_t)min((int)blockIdx.x, w.short_capacity - 1) * kShortItemInts;
+    int4 item = reinterpret_cast<const int4*>(it)[0];
+    if ((int)blockIdx.x >= w.short_capacity) item = {0, 0, 1, 0};
     if ((int)blockIdx.x >= (w.counts ? w.counts[1] : w.short_count)) {
         // A work-group past the items (small batches, whose items leave
         // most CUs idle) only touches its slices of the weights to prefetch.
@@ -286,7 +288,7 @@ __global__ __launch_bounds__(kSplitPages * 64) void fast_attention_short_kernel(
         return;
     }
     const int row = item.x, kvh = item.y % w.kv_heads, length = item.z;
-    const int32_t* table = kv.tables + (size_t)(item.y / w.kv_heads) * kv.table_stride;
+    const int32_t* table = it + 4;
     const int split = fast_attention_split(length);
     const int splits = (length + split - 1) / split;  // 1..kSplitPages
     if (wave < splits) {

@@ -182,6 +182,7 @@ __host__ __device__ inline int fast_attention_split(int length) {
 // Rows of up to 256 tokens (at most 8 splits) are combined inside one
 // work-group; longer rows through the partials and the merge kernel.
 __host__ __device__ inline bool fast_attention_short(int length) { return (length + 15) / 16 <= 16; }
+constexpr int kShortItemInts = 20;
 // The most splits a row that is not short has, over every length up to
 // `length` (0 when every such row is short): the stride of the partial
 // results per (sequence, KV head), fixed by the context limit so that the
@@ -210,8 +211,10 @@ struct FastAttentionWork {
     // shorter last ones)
     const int32_t* items;
     int items_count, items_capacity;
-    // per row of up to 256 tokens and KV head (int4): row, table slot *
-    // kv_heads + KV head, tokens, 0
+    // per row of up to 256 tokens and KV head, kShortItemInts int32: row,
+    // table slot * kv_heads + KV head, tokens, 0, then the row's page ids
+    // (16; past the row's last page, its last page again), so that the
+    // pages are found without a dependent load of the table
     const int32_t* short_items;
     int short_count, short_capacity;
     // the rows whose splits the merge kernel combines (the one-token rows
