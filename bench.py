@@ -490,8 +490,11 @@ def summarise_trace(trace_csv: str, steps: str, out: str, command: str):
         lines.append(f"| `{k}` | {grid} | {wg} | {len(v)} | {np.mean(v) / 1e3:.2f} | {min(v) / 1e3:.2f} | "
                      f"{sum(v) / 1e3 / steps:.2f} | {100 * sum(v) / busy:.1f} |")
     # One layer in launch order: the kernels from one launch of the layer's
-    # first projection (the step's first matrix kernel) to the next.
-    starter = next(name(r) for r in window if "gemm" in name(r))
+    # first projection (q|k|v with RoPE: the GEMV kernel of small steps, the
+    # kRope = 4 matrix kernel otherwise) to the next.
+    names = [name(r) for r in window]
+    starters = [n for n in names if "gemv_rope" in n or "fast_gemm_kernel<4," in n]
+    starter = starters[0] if starters else next(n for n in names if "gemm" in n)
     order, layer, instances = defaultdict(list), [], 0
     for r in window:
         if name(r) == starter and layer:

@@ -452,6 +452,186 @@ __global__ __launch_bounds__(kWaves * 64, CH == 1 ? 4 : 1) void fast_gemm_kernel
     }
 }
 
+// LM head over the tied embedding for hidden size K. The tiles above cut K
+// into eight per work-group and sum eight partial tiles through LDS; for the
+// head (768 groups of 64 columns, 36 steps each) that took 50.5 us at 64
+// rows and 25 us at 1 row. Here one work-group per CU holds the rows of a
+// pass (up to 64, times the RMSNorm weights, in fragment order) in LDS, and
+// each of its kHeadWaves wavefronts streams the weights of one 16-column
+// block from HBM through a ring of kHeadRing steps in flight: one MFMA chain
+// per output over the 16-k steps in order, the row blocks' MFMAs of a
+// sub-step issued together (41.7 us at 64 rows, 20.5 us at 16, measured in
+// isolation). The order depends on K only, so a row's logits do not depend
+// on the batch or on the rows sharing its pass; rows beyond 64 take further
+// passes over the same columns. Epilogue as above: the row's 1/sqrt(mean
+// square + eps) (its per-16-column partials summed in a fixed order), logits
+// on request, and per row and 64-column group the first maximum and a
+// non-finite flag, the four wavefronts of a group combined through LDS.
+constexpr int kHeadWaves = 12;  // 16-column blocks per work-group: 3 groups of 64
+constexpr int kHeadRing = 12;   // weight steps in flight per wavefront
+
+template <int K, int RB>
+__global__ __launch_bounds__(kHeadWaves * 64, 1) void fast_head_kernel(FastGemmArgs a) {
+    constexpr int S = K / 16;
+    constexpr int R = RB * 16;
+    constexpr int kThreads = kHeadWaves * 64;
+    constexpr int kFill = (RB * S * 64 + kThreads - 1) / kThreads;
+    constexpr int kParts = S / 4;  // RMSNorm partials per quarter
+    static_assert(K % 16 == 0 && S % kHeadRing == 0 && S % 4 == 0, "whole rings of steps, quarters of partials");
+    __shared__ f4 a_s[RB * S * 64];
+    __shared__ f4 g_s[S][4];
+    __shared__ uint64_t key_s[kHeadWaves][R];
+    __shared__ int32_t bad_s[kHeadWaves][R];
+    __shared__ float ssq_s[4][R];
+    __shared__ float inv_s[R];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nblocks = a.columns >> 4;
+    const int cb = blockIdx.x * kHeadWaves + wave;
+    const bool active = cb < nblocks;
+    // Lane l's float4 of fragment (cb, s): W[16cb + l%16][16s + 4(l/16) .. +3].
+    const float* wb = a.w + (size_t)min(cb, nblocks - 1) * S * 256 + (size_t)lane * 4;
+    for (int r0 = 0; r0 < a.rows; r0 += R) {
+        // The thread index, opaque to the compiler in each pass: otherwise
+        // it keeps every fill address live across the passes (spilled).
+        int tid = threadIdx.x;
+        asm volatile("" : "+v"(tid));
+        // The pass's rows (gathered, clamped to the last row), the RMSNorm
+        // weights and the first ring of weights, all loads issued before the
+        // first wait.
+        f4 xv[kFill], gv = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int u = 0; u < kFill; ++u) {
+            const int i = min(tid + u * kThreads, RB * S * 64 - 1);
+            const int l = i & 63, s = (i >> 6) % S, rb = (i >> 6) / S;
+            const int r = min(r0 + rb * 16 + (l & 15), a.rows - 1);
+            const int xrow = a.row_map ? a.row_map[r] : r;
+            xv[u] = ld4(a.x + ((size_t)(xrow >> 6) * (K / 4) * 64 + (xrow & 63)) * 4 + (size_t)(4 * s + (l >> 4)) * 256);
+        }
+        if (r0 == 0 && tid < S * 4) gv = ld4(a.norm + 4 * tid);
+        // The row's S per-16-column sums of squares: quarter q (partials
+        // qS/4 .. (q+1)S/4 - 1, in order) by thread qR + row.
+        float ss = 0.0f;
+        if (tid < 4 * R) {
+            const int q = tid / R;
+            const int r = min(r0 + tid % R, a.rows - 1);
+            const int pr = a.row_map ? a.row_map[r] : r;
+            float part[kParts];
+#pragma unroll
+            for (int p = 0; p < kParts; ++p) part[p] = a.ssq_in[(size_t)(q * kParts + p) * a.ssq_stride + pr];
+#pragma unroll
+            for (int p = 0; p < kParts; ++p) ss += part[p];
+        }
+        f4 ring[kHeadRing];
+#pragma unroll
+        for (int j = 0; j < kHeadRing; ++j)
+            ring[j] = __builtin_nontemporal_load(reinterpret_cast<const f4*>(wb + (size_t)j * 256));
+        if (r0 == 0 && tid < S * 4) g_s[tid / 4][tid % 4] = gv;
+        if (tid < 4 * R) ssq_s[tid / R][tid % R] = ss;
+        __syncthreads();
+        // The rows times the RMSNorm weights (so that the MFMA loop has no
+        // multiplies).
+#pragma unroll
+        for (int u = 0; u < kFill; ++u) {
+            const int i = tid + u * kThreads;
+            if (i < RB * S * 64) a_s[i] = xv[u] * g_s[(i >> 6) % S][(i >> 4) & 3];
+        }
+        __syncthreads();
+        if (tid < R) {
+            const float* u = &ssq_s[0][tid];
+            inv_s[tid] = 1.0f / sqrtf(((u[0] + u[R]) + (u[2 * R] + u[3 * R])) / (float)K + a.eps);
+        }
+        f4 acc[RB];
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) acc[rb] = f4{0.f, 0.f, 0.f, 0.f};
+        // Rounds of kHeadRing steps (a loop), each step's ring slot reloaded
+        // with the step kHeadRing ahead once consumed, and the next step's
+        // rows read from LDS before this step's MFMAs (the scheduling
+        // barriers keep the compiler from hoisting more of them). The MFMAs
+        // of a step go sub-step by sub-step across the row blocks, so that
+        // consecutive ones are independent.
+        f4 xc[RB];
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) xc[rb] = a_s[rb * S * 64 + lane];
+#pragma unroll 1
+        for (int s0 = 0; s0 < S; s0 += kHeadRing) {
+#pragma unroll
+            for (int j = 0; j < kHeadRing; ++j) {
+                const int s = s0 + j;
+                const f4 b = ring[j];
+                // (The last round re-reads the last step: no branch.)
+                ring[j] = __builtin_nontemporal_load(
+                    reinterpret_cast<const f4*>(wb + (size_t)min(s + kHeadRing, S - 1) * 256));
+                const int sn = min(s + 1, S - 1);
+                f4 xn[RB];
+#pragma unroll
+                for (int rb = 0; rb < RB; ++rb) xn[rb] = a_s[(rb * S + sn) * 64 + lane];
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int rb = 0; rb < RB; ++rb) acc[rb] = __builtin_amdgcn_mfma_f32_16x16x4f32(xc[rb].x, b.x, acc[rb], 0, 0, 0);
+#pragma unroll
+                for (int rb = 0; rb < RB; ++rb) acc[rb] = __builtin_amdgcn_mfma_f32_16x16x4f32(xc[rb].y, b.y, acc[rb], 0, 0, 0);
+#pragma unroll
+                for (int rb = 0; rb < RB; ++rb) acc[rb] = __builtin_amdgcn_mfma_f32_16x16x4f32(xc[rb].z, b.z, acc[rb], 0, 0, 0);
+#pragma unroll
+                for (int rb = 0; rb < RB; ++rb) acc[rb] = __builtin_amdgcn_mfma_f32_16x16x4f32(xc[rb].w, b.w, acc[rb], 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int rb = 0; rb < RB; ++rb) xc[rb] = xn[rb];
+            }
+        }
+        __syncthreads();  // inv_s
+        // Lane l, register i: row r0 + 16rb + 4(l/16) + i, column 16cb + l%16.
+        // (A transpose through LDS, each lane then scanning one row's 16
+        // columns, measured slower: 45.9 vs 41.7 us at 64 rows.)
+        const int N = a.columns;
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int rl = rb * 16 + 4 * (lane >> 4) + i;
+                const int row = r0 + rl;
+                const bool live = active && row < a.rows;
+                const float x = acc[rb][i] * inv_s[rl];
+                const int col = cb * 16 + (lane & 15);
+                if (live && a.logits) a.logits[(size_t)row * N + col] = x;
+                const bool finite = __builtin_isfinite(x);
+                uint64_t key = live && finite ? argmax_key(x, col) : 0;
+                key = max_key<kDppQuadXor1>(key);
+                key = max_key<kDppQuadXor2>(key);
+                key = max_key<kDppRowRor4>(key);
+                key = max_key<kDppRowRor8>(key);
+                const uint64_t bads = __ballot(live && !finite);
+                if ((lane & 15) == 0) {
+                    key_s[wave][rl] = key;
+                    bad_s[wave][rl] = ((bads >> (lane & 48)) & 0xFFFFull) != 0;
+                }
+            }
+        }
+        __syncthreads();
+        // Per row and 64-column group: the first maximum of its four blocks.
+        if (tid < (kHeadWaves / 4) * R) {
+            const int gl = tid / R, rl = tid % R;
+            const int cg = blockIdx.x * (kHeadWaves / 4) + gl, row = r0 + rl;
+            if (4 * cg < nblocks && row < a.rows) {
+                uint64_t key = 0;
+                int32_t bad = 0;
+#pragma unroll
+                for (int w = 0; w < 4; ++w) {
+                    const uint64_t k = key_s[4 * gl + w][rl];
+                    key = k > key ? k : key;
+                    bad |= bad_s[4 * gl + w][rl];
+                }
+                const size_t at = (size_t)row * a.groups + cg;
+                a.best_value[at] = key ? key_value(key) : -__builtin_inff();
+                a.best_index[at] = key ? (int)(0xFFFFFFFFu - (uint32_t)key) : -1;
+                a.bad[at] = bad;
+            }
+        }
+        __syncthreads();  // the next pass rewrites a_s, key_s and bad_s
+    }
+}
+
 // x rows' per-16-column sums of squares (the partials a NORM projection
 // reads), for x written by something other than a residual projection.
 __global__ __launch_bounds__(256) void fast_ssq_kernel(const float* __restrict__ x, int rows, int width,
@@ -499,6 +679,13 @@ template <int EPI, bool NORM, bool GATHER>
 hipError_t launch_sized(hipStream_t s, const FastGemmArgs& a) {
     constexpr int M = EPI == kSwiglu ? 2 : 1;
     if constexpr (EPI == kHead) {
+        if (a.inner == 576 && a.ssq_parts == 576 / 16 && head_wide(a.columns) && a.norm && a.ssq_in) {
+            const int blocks = (a.columns / 16 + kHeadWaves - 1) / kHeadWaves;
+            if (a.rows <= 16) fast_head_kernel<576, 1><<<blocks, kHeadWaves * 64, 0, s>>>(a);
+            else if (a.rows <= 32) fast_head_kernel<576, 2><<<blocks, kHeadWaves * 64, 0, s>>>(a);
+            else fast_head_kernel<576, 4><<<blocks, kHeadWaves * 64, 0, s>>>(a);
+            return hipGetLastError();
+        }
         if (head_wide(a.columns)) {
             // Row blocks as the batch needs them (B=1: 24.6 instead of 52.4
             // us; B=32: 35.0 instead of 48.6), 64-column groups throughout.
