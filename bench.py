@@ -172,9 +172,9 @@ def gpu_leg(args, wl):
             raise RuntimeError("prefill did not finish")
     log(f"prefill: {setup_steps} + {prefill_steps} steps, {time.perf_counter() - t:.1f}s")
     remaining = min(r.max_new_tokens for r in active) - max(generated[i] for i in ids)
-    if args.warmup + args.steps + 1 > remaining:
-        raise SystemExit(f"--warmup + --steps must leave every request decoding for one more step: "
-                         f"{remaining} decode steps remain")
+    if args.warmup + args.steps + 2 > remaining:
+        raise SystemExit(f"--warmup + --steps must leave every request decoding for two more steps (the roofline "
+                         f"pass and the first requests' last token): {remaining} decode steps remain")
     batch = len(ids)
     used0 = {rid: engine.runner.sequence(rid)[1] for rid in ids}  # committed tokens before the first decode step
     clean = []  # (decode step index, host seconds) of the steps outside the roofline pass
@@ -202,7 +202,11 @@ def gpu_leg(args, wl):
     # Roofline pass: one layer per step (rotating) has its attention and
     # projections timed; --all-kernels times every layer and the LM head.
     first_rof = args.warmup + args.steps
-    rof_steps = min(ROOFLINE_STEPS, remaining - first_rof)
+    # It ends before the decode step in which the first requests emit their
+    # last token (their releases may split that step's batch).
+    rof_steps = min(ROOFLINE_STEPS, remaining - 1 - first_rof)
+    if rof_steps < 1:
+        raise SystemExit(f"--warmup + --steps leave no decode step for the roofline pass ({remaining} remain)")
     classes = TIME_ATTENTION | TIME_PROJECTION | (TIME_HEAD if args.all_kernels else TIME_SAMPLED)
     set_timing(device, classes)
     for _ in range(rof_steps):
@@ -383,12 +387,19 @@ def roofline(kind: str, g: dict, rec: dict | None):
 
 
 def decode_dispatches(rows: list, steps: int, path: str) -> range:
-    """Dispatch ids of the last `steps` engine steps of a rocprofv3 --pmc
-    run of this script (each step ends with the LM head's argmax kernel; the
-    pure decode steps, warmup and timed, run last). Counting by step, not by
-    kernel name or grid, keeps out the prefill steps, which run the same
-    instantiations for their one-token rows and short chunks."""
-    ends = sorted({int(r["Dispatch_Id"]) for r in rows if "head_argmax_kernel" in r["Kernel_Name"]})
+    """Dispatch ids of the roofline pass of a rocprofv3 --pmc run of this
+    script with --traffic-probe: the last `steps` engine steps before the
+    probe's copy of PROBE_BYTES (each step ends with the LM head's argmax
+    kernel). Counting by step, not by kernel name or grid, keeps out the
+    prefill steps, which run the same instantiations for their one-token
+    rows and short chunks, and the probe places the window at the contexts
+    whose algorithmic bytes the bench line reports."""
+    probe = [int(r["Dispatch_Id"]) for r in rows
+             if r["Kernel_Name"].startswith("__amd_rocclr_copyBuffer") and int(r["Grid_Size"]) * 16 >= PROBE_BYTES // 4]
+    if not probe:
+        raise SystemExit(f"{path}: no probe copy found (run bench.py with --traffic-probe)")
+    ends = sorted({int(r["Dispatch_Id"]) for r in rows
+                   if "head_argmax_kernel" in r["Kernel_Name"] and int(r["Dispatch_Id"]) < min(probe)})
     if len(ends) < steps + 1:
         raise SystemExit(f"{path}: {len(ends) - 1} complete steps, {steps} asked for")
     return range(ends[-steps - 1] + 1, ends[-1] + 1)
@@ -409,7 +420,7 @@ def summarise_counters(fetch_csv: str, write_csv: str, bench_json: str, out: str
 
     def read(path):
         rows = list(csv.DictReader(open(path)))
-        window = decode_dispatches(rows, line["warmup"] + line["steps"], path)
+        window = decode_dispatches(rows, line["kernel_times_ns"]["attention_launches"], path)
         per = defaultdict(list)  # name -> KiB per decode launch
         probe = []
         for r in rows:
@@ -422,7 +433,7 @@ def summarise_counters(fetch_csv: str, write_csv: str, bench_json: str, out: str
         return per, probe
 
     result = {"workload": line["config"]["workload"], "seed": line["config"]["seed"],
-              "arithmetic": line["config"].get("arithmetic"), "mean_context": line["config"]["mean_context"],
+              "arithmetic": line["config"].get("arithmetic"), "window": line["roofline"]["measured_over"],
               "steps": line["steps"], "warmup": line["warmup"]}
     for counter, path in (("fetch", fetch_csv), ("write", write_csv)):
         per, probe = read(path)
@@ -450,6 +461,27 @@ def summarise_counters(fetch_csv: str, write_csv: str, bench_json: str, out: str
     print(json.dumps(result, indent=1))
 
 
+def trace_window(trace_csv: str, steps: str):
+    """The dispatches of a rocprofv3 --kernel-trace run of bench.py in time
+    order over `steps` engine steps (a step ends with the LM head's argmax
+    kernel): "N" for the last N steps, "N+F" for N steps from engine step F
+    (0-based, prefill steps included). Returns (rows, N, F or None)."""
+    first = None
+    if "+" in steps:
+        steps, first = steps.split("+")
+        first = int(first)
+    steps = int(steps)
+    rows = sorted(csv.DictReader(open(trace_csv)), key=lambda r: int(r["Start_Timestamp"]))
+    ends = [i for i, r in enumerate(rows) if "head_argmax_kernel" in r["Kernel_Name"]]
+    if first is None:
+        if len(ends) < steps + 1:
+            raise SystemExit(f"{trace_csv}: {len(ends) - 1} complete steps, {steps} asked for")
+        return rows[ends[-steps - 1] + 1:ends[-1] + 1], steps, None
+    if first < 1 or len(ends) < first + steps:
+        raise SystemExit(f"{trace_csv}: {len(ends)} steps, steps {first}..{first + steps - 1} asked for")
+    return rows[ends[first - 1] + 1:ends[first + steps - 1] + 1], steps, first
+
+
 def summarise_trace(trace_csv: str, steps: str, out: str, command: str):
     """Markdown table of a rocprofv3 --kernel-trace run of bench.py: every
     kernel of `steps` engine steps (a step ends with the LM head's argmax
@@ -457,24 +489,11 @@ def summarise_trace(trace_csv: str, steps: str, out: str, command: str):
     prefill steps included in the count), its launches, average and minimum
     duration and time per step, then the kernels of one layer in launch
     order."""
-    first = None
-    if "+" in steps:
-        steps, first = steps.split("+")
-        first = int(first)
-    steps = int(steps)
-    rows = sorted(csv.DictReader(open(trace_csv)), key=lambda r: int(r["Start_Timestamp"]))
+    window, steps, first = trace_window(trace_csv, steps)
+    if first is not None:
+        steps_text = f"steps {first}..{first + steps - 1}"
     name = lambda r: r["Kernel_Name"].replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0]
     dur = lambda r: int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
-    ends = [i for i, r in enumerate(rows) if "head_argmax_kernel" in name(r)]
-    if first is None:
-        if len(ends) < steps + 1:
-            raise SystemExit(f"{trace_csv}: {len(ends) - 1} complete steps, {steps} asked for")
-        window = rows[ends[-steps - 1] + 1:ends[-1] + 1]
-    else:
-        if first < 1 or len(ends) < first + steps:
-            raise SystemExit(f"{trace_csv}: {len(ends)} steps, steps {first}..{first + steps - 1} asked for")
-        window = rows[ends[first - 1] + 1:ends[first + steps - 1] + 1]
-        steps_text = f"steps {first}..{first + steps - 1}"
     span = int(window[-1]["End_Timestamp"]) - int(window[0]["Start_Timestamp"])
     busy = sum(dur(r) for r in window)
     per = defaultdict(list)
@@ -516,7 +535,7 @@ def summarise_trace(trace_csv: str, steps: str, out: str, command: str):
     print("\n".join(lines))
 
 
-def summarise_sq(counter_csv: str, trace_csv: str, out: str, command: str):
+def summarise_sq(counter_csv: str, trace_csv: str, trace_steps: str, out: str, command: str):
     """Markdown table of a rocprofv3 --pmc run of bench.py with the SQ
     counters SQ_WAVE_CYCLES SQ_BUSY_CYCLES SQ_ACTIVE_INST_VALU SQ_INSTS_VALU
     SQ_INSTS_MFMA SQ_VALU_MFMA_BUSY_CYCLES SQ_INSTS_VALU_MFMA_MOPS_F32
@@ -529,14 +548,12 @@ def summarise_sq(counter_csv: str, trace_csv: str, out: str, command: str):
     clean = lambda n: n.replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0]
     decode = ("fast_attention_kernel<", "fast_attention_merge_kernel", "fast_gemm_kernel<4, true, false, 1, 1, 12>",
               "fast_gemm_kernel<1, false, false, 1, 1, 12>", "fast_gemm_kernel<2, true, false, 2, 1, 6>",
-              "fast_gemm_kernel<3, true, true, 4, 4, ")
+              "fast_head_kernel<576, 4>")
     pick = lambda n: next((k for k in decode if k in n), None)
-    # The pure decode steps only (warmup and timed, from the command line):
+    # The roofline pass's decode steps only (the run has --traffic-probe):
     # prefill steps run the same instantiations on other shapes.
-    opt = lambda flag, default: int(command.split(flag)[1].split()[0]) if flag in command else default
-    counted = opt("--warmup", 4) + opt("--steps", 20)
     rows = list(csv.DictReader(open(counter_csv)))
-    window = decode_dispatches(rows, counted, counter_csv)
+    window = decode_dispatches(rows, ROOFLINE_STEPS, counter_csv)
     per, meta = defaultdict(dict), {}
     for r in rows:
         k = pick(clean(r["Kernel_Name"]))
@@ -545,11 +562,9 @@ def summarise_sq(counter_csv: str, trace_csv: str, out: str, command: str):
             continue
         per[d][r["Counter_Name"]] = float(r["Counter_Value"])
         meta[d] = k
-    # Durations: every launch of the trace's last 24 decode steps.
-    trace = sorted(csv.DictReader(open(trace_csv)), key=lambda r: int(r["Start_Timestamp"]))
-    ends = [i for i, r in enumerate(trace) if "head_argmax_kernel" in r["Kernel_Name"]]
+    # Durations: every launch of the trace's window.
     durations = defaultdict(list)
-    for r in trace[ends[-25] + 1 if len(ends) > 24 else 0:ends[-1] + 1]:
+    for r in trace_window(trace_csv, trace_steps)[0]:
         k = pick(clean(r["Kernel_Name"]))
         if k:
             durations[k].append(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
@@ -560,7 +575,8 @@ def summarise_sq(counter_csv: str, trace_csv: str, out: str, command: str):
             agg[meta[d]][k] += v
     simds, clock = 256 * 4, 2.4e9
     lines = ["# SQ counters of the decode kernels (fast arithmetic)", "", f"Counters: `{command}`", "",
-             "Durations: the --kernel-trace summary of the same workload (decode_config3_fast_kernels.md). "
+             f"Durations: the --kernel-trace run of the same workload, engine steps {trace_steps} "
+             "(decode_config3_fast_kernels.md). Counters: the 30 steps of the roofline pass. "
              "Matrix-core utilisation = SQ_VALU_MFMA_BUSY_CYCLES per launch / (1,024 SIMDs x average duration x "
              "2.4 GHz); VALU active and waiting = SQ_ACTIVE_INST_VALU and SQ_WAIT_INST_ANY over SQ_WAVE_CYCLES.", "",
              "| kernel | launches | avg us | MFMA instr per launch | MFMA busy cycles per launch | matrix-core "
@@ -596,7 +612,7 @@ def main():
     ap.add_argument("--cost-timing", action="store_true",
                     help="time the host prefix-cache lookups/publications and the COW copies of the timed steps")
     ap.add_argument("--summarise-counters", nargs=4, metavar=("FETCH_CSV", "WRITE_CSV", "BENCH_JSON", "OUT"))
-    ap.add_argument("--summarise-sq", nargs=4, metavar=("COUNTER_CSV", "TRACE_CSV", "OUT", "COMMAND"),
+    ap.add_argument("--summarise-sq", nargs=5, metavar=("COUNTER_CSV", "TRACE_CSV", "TRACE_STEPS", "OUT", "COMMAND"),
                     help="markdown summary of a rocprofv3 --pmc run of this script with the SQ counters")
     ap.add_argument("--summarise-trace", nargs=4, metavar=("TRACE_CSV", "STEPS", "OUT", "COMMAND"),
                     help="markdown summary of a rocprofv3 --kernel-trace run of this script (STEPS: N, the last N "

@@ -61,7 +61,10 @@ public:
         kv_.create(id);
         live_.insert(id);
     }
-    void fork_sequence(const RequestId& s, const RequestId& t) override { kv_.fork_sequence(s, t); }
+    void fork_sequence(const RequestId& s, const RequestId& t) override {
+        kv_.fork_sequence(s, t);
+        forked_ = true;
+    }
     std::size_t reuse_prefix(const RequestId& id, const std::vector<TokenId>& p) override { return kv_.reuse_prefix(id, p); }
     void cache_prefix(const RequestId& id) override { kv_.cache_prefix(id); }
     void clear_prefix_cache() override { kv_.clear_prefix_cache(); }
@@ -103,6 +106,7 @@ public:
         tx.commit();
     }
     std::vector<StagedResult> run_staged() override {
+        ++passes_;
         const std::vector<int> before = pool_;  // what every forward of the batch reads
         std::vector<StagedResult> results;
         for (const Forward& f : queue_) results.push_back({run(f, before), true});
@@ -112,6 +116,15 @@ public:
     void discard_staged() noexcept override {
         queue_.clear();
         std::fill(writes_.begin(), writes_.end(), 0);
+    }
+    // As the HIP runner decides it (hip_runner.cpp).
+    bool stage_touches_pool(const RequestId& id, std::size_t tokens, bool publishes) const override {
+        const PagedSequence& s = kv_.sequence(id);
+        const std::size_t bt = static_cast<std::size_t>(bt_), used = static_cast<std::size_t>(s.used);
+        const bool caches = kv_.config().prefix_cache_blocks > 0;
+        if ((used + tokens + bt - 1) / bt > s.blocks.size()) return true;
+        if (used % bt != 0 && (caches || forked_)) return true;
+        return publishes && caches;
     }
     bool shares_staged_pages(const RequestId& id) const override {
         if (!kv_.contains(id)) return false;
@@ -166,6 +179,10 @@ private:
     std::vector<char> writes_;  // per block: written by a queued forward
     std::vector<Forward> queue_;
     std::set<RequestId> live_;
+    bool forked_ = false;
+
+public:
+    int passes_ = 0;  // run_staged() calls
 };
 
 struct Submit {
@@ -175,7 +192,8 @@ struct Submit {
 
 // Runs the submissions through an engine and returns a transcript of every
 // step's events and page tables.
-std::string transcript(KvCacheConfig kv, EngineConfig ec, const std::vector<Submit>& submits, bool batching) {
+std::string transcript(KvCacheConfig kv, EngineConfig ec, const std::vector<Submit>& submits, bool batching,
+                       std::vector<int>* passes = nullptr) {
     auto owned = std::make_unique<PayloadRunner>(kv);
     PayloadRunner* runner = owned.get();
     Engine engine(std::move(owned), ec);
@@ -195,6 +213,8 @@ std::string transcript(KvCacheConfig kv, EngineConfig ec, const std::vector<Subm
         }
         out << "| " << runner->tables() << "\n";
         CHECK(!engine.failed());
+        if (passes) passes->push_back(runner->passes_);
+        runner->passes_ = 0;
     }
     CHECK(engine.idle());
     return out.str();
@@ -248,7 +268,7 @@ void concurrent_fork() {
 // Many requests over shared prompt prefixes, small pools (evictions,
 // waiting admissions, capacity errors), EOS, budgets and chunks.
 void randomized() {
-    for (unsigned seed = 1; seed <= 60; ++seed) {
+    for (unsigned seed = 1; seed <= 400; ++seed) {
         std::mt19937 rng(seed);
         auto pick = [&](int lo, int hi) { return std::uniform_int_distribution<int>(lo, hi)(rng); };
         const int bt = pick(2, 5);
@@ -276,11 +296,32 @@ void randomized() {
     }
 }
 
+// Requests that finish in a step (by length, or by an EOS that only their
+// result decides) no longer run their forwards alone: the appends after them
+// join the same device pass unless they take pages from the pool. Here no
+// decode step crosses a page, so every decode step is one pass; the prefill
+// step, whose appends each take a first page, runs a pass before each
+// append that follows one that may finish.
+void finishing_requests_share_a_batch() {
+    const KvCacheConfig kv{16, 64, 0};
+    const EngineConfig ec{8, 64, 16, 128};
+    std::vector<Submit> submits;
+    for (int i = 0; i < 8; ++i)
+        submits.push_back({0, request("f" + std::to_string(i), iota(1 + i, 3), static_cast<unsigned>(2 + i % 3),
+                                      i % 2 ? std::optional<TokenId>(5) : std::nullopt)});
+    same(kv, ec, submits, "finishing_requests_share_a_batch");
+    std::vector<int> passes;
+    transcript(kv, ec, submits, true, &passes);
+    CHECK(passes.size() >= 2);
+    for (std::size_t step = 1; step < passes.size(); ++step) CHECK(passes[step] <= 1);
+}
+
 }  // namespace
 
 int main() {
     same_step_publish_and_reuse();
     concurrent_fork();
+    finishing_requests_share_a_batch();
     randomized();
     std::puts("staged engine tests passed");
     return 0;

@@ -56,13 +56,21 @@ public:
         ModelRunner& runner = *engine_.runner_;
         const RequestId& id = job.request.id;
         if (staged_) {
+            // A queued item that may finish in this step (EOS possible, or
+            // its last token) releases its sequence when the queue runs. In
+            // the per-request order that release precedes every later append
+            // of the step; it changes what a later append gets only if that
+            // append takes pages from the pool or publishes into a prefix
+            // cache, so only such an append runs the queue first.
+            const bool samples =
+                !prefill || job.prefilled + input.size() >= job.request.prompt_token_ids.size();
+            if (may_release_ && staged_->stage_touches_pool(id, input.size(), samples)) run_queue();
             staged_->stage(id, input);
             engine_.account(job, input.size(), prefill);
-            const bool samples = prompt_done(job);
             queue_.push_back({&job, samples});
             if (!samples) return;
             runner.cache_prefix(id);
-            if (may_finish(job)) run_queue();
+            if (may_finish(job)) may_release_ = true;
             return;
         }
         const std::vector<float> logits = runner.append(id, input);
@@ -78,6 +86,7 @@ public:
     }
 
     void run_queue() {
+        may_release_ = false;  // the queue's finishes release in order below
         if (queue_.empty()) return;
         const std::vector<StagedResult> results = staged_->run_staged();
         std::vector<Queued> batch;
@@ -103,6 +112,7 @@ private:
     Engine& engine_;
     StagedRunner* staged_;
     std::vector<Queued> queue_;
+    bool may_release_ = false;  // a queued item may finish when the queue runs
 };
 
 Engine::Engine(std::unique_ptr<ModelRunner> runner, EngineConfig config)

@@ -81,6 +81,7 @@ public:
     void fork_sequence(const RequestId& source, const RequestId& target) override {
         sync("fork completion");
         kv_.fork_sequence(source, target);
+        forked_ = true;
         tables_.at(target).dirty = true;  // written whole by the next append
     }
     std::size_t reuse_prefix(const RequestId& id, const std::vector<TokenId>& prompt) override {
@@ -186,6 +187,18 @@ public:
         staged_tokens_.clear();
         for (const int block : written_) staged_writes_[static_cast<std::size_t>(block)] = 0;
         written_.clear();
+    }
+    // New pages, or (conservatively) a tail page that a prefix cache or a
+    // fork may share and a copy-on-write would replace; or a publication
+    // into a prefix cache.
+    bool stage_touches_pool(const RequestId& id, std::size_t tokens, bool publishes) const override {
+        const PagedSequence& s = kv_.sequence(id);
+        const std::size_t bt = static_cast<std::size_t>(kv_.config().block_tokens);
+        const std::size_t used = static_cast<std::size_t>(s.used);
+        const bool caches = kv_.config().prefix_cache_blocks > 0;
+        if ((used + tokens + bt - 1) / bt > s.blocks.size()) return true;
+        if (used % bt != 0 && (caches || forked_)) return true;
+        return publishes && caches;
     }
     bool shares_staged_pages(const RequestId& id) const override {
         if (written_.empty() || !kv_.contains(id)) return false;
@@ -324,6 +337,7 @@ private:
     CostStats costs_;
     bool cost_timing_ = false;
     bool keep_logits_ = false;
+    bool forked_ = false;  // a fork_sequence() made shared tails possible
     std::map<RequestId, std::vector<float>> kept_;
 };
 

@@ -33,6 +33,13 @@ public:
     virtual void discard_staged() noexcept = 0;
     // True when sequence `id` references a block that a queued forward writes.
     virtual bool shares_staged_pages(const RequestId& id) const = 0;
+    // True when staging `tokens` more for sequence `id` would take pages
+    // from the pool (new pages or a copy-on-write target) or, with
+    // `publishes`, publish into a prefix cache, whose evictions return pages
+    // to the pool. A caller whose queued items may release their sequences
+    // once their results are known runs the queue before such a stage, so
+    // that the pool sees the releases first.
+    virtual bool stage_touches_pool(const RequestId& id, std::size_t tokens, bool publishes) const = 0;
 };
 
 }  // namespace miniprefix
