@@ -394,8 +394,10 @@ def decode_dispatches(rows: list, steps: int, path: str) -> range:
     prefill steps, which run the same instantiations for their one-token
     rows and short chunks, and the probe places the window at the contexts
     whose algorithmic bytes the bench line reports."""
+    # (The runtime's copy kernel moves about 1 KiB per work-item: the probe's
+    # 128 MiB is a grid of 131,072, a step's metadata upload one of 512.)
     probe = [int(r["Dispatch_Id"]) for r in rows
-             if r["Kernel_Name"].startswith("__amd_rocclr_copyBuffer") and int(r["Grid_Size"]) * 16 >= PROBE_BYTES // 4]
+             if r["Kernel_Name"].startswith("__amd_rocclr_copyBuffer") and int(r["Grid_Size"]) * 1024 >= PROBE_BYTES // 2]
     if not probe:
         raise SystemExit(f"{path}: no probe copy found (run bench.py with --traffic-probe)")
     ends = sorted({int(r["Dispatch_Id"]) for r in rows
@@ -575,8 +577,8 @@ def summarise_sq(counter_csv: str, trace_csv: str, trace_steps: str, out: str, c
             agg[meta[d]][k] += v
     simds, clock = 256 * 4, 2.4e9
     lines = ["# SQ counters of the decode kernels (fast arithmetic)", "", f"Counters: `{command}`", "",
-             f"Durations: the --kernel-trace run of the same workload, engine steps {trace_steps} "
-             "(decode_config3_fast_kernels.md). Counters: the 30 steps of the roofline pass. "
+             f"Durations: the --kernel-trace run of the same workload over the same steps, the roofline pass "
+             f"(engine steps {trace_steps}: decode_config3_fast_kernels_roofline_pass.md). "
              "Matrix-core utilisation = SQ_VALU_MFMA_BUSY_CYCLES per launch / (1,024 SIMDs x average duration x "
              "2.4 GHz); VALU active and waiting = SQ_ACTIVE_INST_VALU and SQ_WAIT_INST_ANY over SQ_WAVE_CYCLES.", "",
              "| kernel | launches | avg us | MFMA instr per launch | MFMA busy cycles per launch | matrix-core "
