@@ -389,7 +389,9 @@ __global__ __launch_bounds__(256) void fast_attention_merge_kernel(int heads, in
         }
         gm = rm;
     };
-    load(0, w.split_stride);  // bounded by the most splits a row can have until the row's own count is known
+    // Bounded, until the row's own count is known, by the step's most splits
+    // (a launch that a graph replays: by the most any row can have).
+    load(0, w.counts ? w.split_stride : w.max_splits);
     // The row's position is first needed here, after the loads above are in flight.
     __builtin_amdgcn_sched_barrier(0);
     asm volatile("" : "+v"(pos));
