@@ -90,7 +90,12 @@ __device__ __forceinline__ float touch_weights(const FastAttentionWork& w, uint6
 // kvh. Gives per head the reference maximum m, the denominator l and lane
 // d's weighted sum acc (not yet divided). `touch` numbers this wavefront's
 // 8 KB slice of the weight prefetch; p_s is the wavefront's own LDS.
-template <int G, bool PLAIN>
+// NP > 0: the split is NP whole pages (n == NP * kPage), so the ring loads
+// exactly its pages. NP == 0: any split; the ring's loads are unconditional
+// (so that each page's wait counts a fixed number of later loads), and those
+// past the split's last page re-read it -- two page loads per wavefront that
+// the whole-page variants avoid.
+template <int G, bool PLAIN, int NP = 0>
 __device__ __forceinline__ void attend_split(const float* __restrict__ qkv, int ldq, const PagedKv& kv, int layer,
                                              const FastAttentionWork& w, const int32_t* table, int row, int kvh,
                                              int t0, int n, uint64_t touch, float (&p_s)[G][kPage], float (&m)[G],
@@ -99,10 +104,12 @@ __device__ __forceinline__ void attend_split(const float* __restrict__ qkv, int 
     const int t = lane >> 2, dq = lane & 3;
     const int end = t0 + n;           // tokens t0..end-1 (t0 page-aligned)
     const int first = t0 / kPage;     // the split's first page
-    const int np = (end + kPage - 1) / kPage - first;  // 1..kMaxPages
+    static_assert(NP >= 0 && NP <= kMaxPages && (NP == 0 || NP >= kRing), "whole-page splits fill the ring");
+    constexpr int kPages = NP > 0 ? NP : kMaxPages;  // iterations of the page loop
+    const int np = NP > 0 ? NP : (end + kPage - 1) / kPage - first;  // 1..kMaxPages
     int page_id[kMaxPages];
 #pragma unroll
-    for (int k = 0; k < kMaxPages; ++k) page_id[k] = table[first + min(k, np - 1)];
+    for (int k = 0; k < kPages; ++k) page_id[k] = table[first + (NP > 0 ? k : min(k, np - 1))];
     const size_t head_base = (size_t)kvh * kPage * kDim;  // floats into a page-layer span
     f4 kb[kRing][4], vb[kRing][4];
     auto load = [&](int k, f4 (&kk)[4], f4 (&vv)[4]) {
@@ -144,8 +151,8 @@ __device__ __forceinline__ void attend_split(const float* __restrict__ qkv, int 
         acc[h] = 0.0f;
     }
 #pragma unroll
-    for (int k = 0; k < kMaxPages; ++k) {
-        if (k > 0 && k >= np) break;  // np >= 1
+    for (int k = 0; k < kPages; ++k) {
+        if (NP == 0 && k > 0 && k >= np) break;  // np >= 1
         f4(&kc)[4] = kb[k % kRing];
         f4(&vc)[4] = vb[k % kRing];
         const int tok0 = (first + k) * kPage;
@@ -213,7 +220,7 @@ __device__ __forceinline__ void attend_split(const float* __restrict__ qkv, int 
         }
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_sched_barrier(0);
-        if (k + kRing < kMaxPages) load(k + kRing, kb[k % kRing], vb[k % kRing]);
+        if (k + kRing < kPages) load(k + kRing, kb[k % kRing], vb[k % kRing]);
         __builtin_amdgcn_sched_barrier(0);
     }
     asm volatile("" ::"v"(touched));  // the prefetch's value is not used
@@ -246,7 +253,15 @@ __global__ __launch_bounds__(kItemsPerGroup * 64) void fast_attention_kernel(con
     const int n = item.w & 0x1FF, sp = (item.w >> 9) & 0x7FFF, t0 = sp << (item.w >> 24);
     const int32_t* table = kv.tables + (size_t)(item.y / w.kv_heads) * kv.table_stride;
     float m[G], l[G], acc[G];
-    attend_split<G, PLAIN>(qkv, ldq, kv, layer, w, table, row, kvh, t0, n, (uint64_t)index, p_s[wave], m, l, acc);
+    // Whole 128- and 256-token splits (all but each row's last) take the
+    // variants that load exactly their pages.
+    const int pages = __builtin_amdgcn_readfirstlane(n == 8 * kPage ? 8 : n == 16 * kPage ? 16 : 0);
+    if (pages == 8)
+        attend_split<G, PLAIN, 8>(qkv, ldq, kv, layer, w, table, row, kvh, t0, n, (uint64_t)index, p_s[wave], m, l, acc);
+    else if (pages == 16)
+        attend_split<G, PLAIN, 16>(qkv, ldq, kv, layer, w, table, row, kvh, t0, n, (uint64_t)index, p_s[wave], m, l, acc);
+    else
+        attend_split<G, PLAIN>(qkv, ldq, kv, layer, w, table, row, kvh, t0, n, (uint64_t)index, p_s[wave], m, l, acc);
     const size_t slot = ((size_t)seq * w.kv_heads + kvh) * w.split_stride + sp;
 #pragma unroll
     for (int h = 0; h < G; ++h) {
@@ -294,8 +309,12 @@ __global__ __launch_bounds__(kSplitPages * 64) void fast_attention_short_kernel(
     if (wave < splits) {
         float m[G], l[G], acc[G];
         const int t0 = wave * split;
-        attend_split<G, PLAIN>(qkv, ldq, kv, layer, w, table, row, kvh, t0, min(split, length - t0),
-                        (uint64_t)blockIdx.x * kSplitPages + wave, p_s[wave], m, l, acc);
+        const int n = min(split, length - t0);
+        const uint64_t touch = (uint64_t)blockIdx.x * kSplitPages + wave;
+        if (n == 2 * kPage)  // whole 32-token splits: exactly their two pages
+            attend_split<G, PLAIN, 2>(qkv, ldq, kv, layer, w, table, row, kvh, t0, n, touch, p_s[wave], m, l, acc);
+        else
+            attend_split<G, PLAIN>(qkv, ldq, kv, layer, w, table, row, kvh, t0, n, touch, p_s[wave], m, l, acc);
 #pragma unroll
         for (int h = 0; h < G; ++h) {
             part_acc[wave][h][lane] = acc[h];
