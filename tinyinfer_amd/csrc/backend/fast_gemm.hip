@@ -48,6 +48,8 @@
 // RMSNorm on the input (NORM): a[r][k] = x[r][k] * g[k], and the result is
 // scaled by 1/sqrt(sum_k x[r][k]^2 / K + eps), the sum assembled from the
 // producer's per-block partials.
+#include <type_traits>
+
 #include "kernels.h"
 #include "lanes.h"
 #include "layout.h"
@@ -544,24 +546,24 @@ __global__ __launch_bounds__(kHeadWaves * 64, 1) void fast_head_kernel(FastGemmA
         f4 acc[RB];
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) acc[rb] = f4{0.f, 0.f, 0.f, 0.f};
-        // Rounds of kHeadRing steps (a loop), each step's ring slot reloaded
-        // with the step kHeadRing ahead once consumed, and the next step's
-        // rows read from LDS before this step's MFMAs (the scheduling
+        // Rounds of kHeadRing steps (a loop, then the last round on its own),
+        // each step's ring slot reloaded with the step kHeadRing ahead once
+        // consumed (but in the last round, which would only re-read the
+        // last step: 12 KB of surplus loads per wavefront), and the next
+        // step's rows read from LDS before this step's MFMAs (the scheduling
         // barriers keep the compiler from hoisting more of them). The MFMAs
         // of a step go sub-step by sub-step across the row blocks, so that
         // consecutive ones are independent.
         f4 xc[RB];
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) xc[rb] = a_s[rb * S * 64 + lane];
-#pragma unroll 1
-        for (int s0 = 0; s0 < S; s0 += kHeadRing) {
+        auto round = [&](int s0, auto reload) {
 #pragma unroll
             for (int j = 0; j < kHeadRing; ++j) {
                 const int s = s0 + j;
                 const f4 b = ring[j];
-                // (The last round re-reads the last step: no branch.)
-                ring[j] = __builtin_nontemporal_load(
-                    reinterpret_cast<const f4*>(wb + (size_t)min(s + kHeadRing, S - 1) * 256));
+                if constexpr (decltype(reload)::value)
+                    ring[j] = __builtin_nontemporal_load(reinterpret_cast<const f4*>(wb + (size_t)(s + kHeadRing) * 256));
                 const int sn = min(s + 1, S - 1);
                 f4 xn[RB];
 #pragma unroll
@@ -579,7 +581,10 @@ __global__ __launch_bounds__(kHeadWaves * 64, 1) void fast_head_kernel(FastGemmA
 #pragma unroll
                 for (int rb = 0; rb < RB; ++rb) xc[rb] = xn[rb];
             }
-        }
+        };
+#pragma unroll 1
+        for (int s0 = 0; s0 + kHeadRing < S; s0 += kHeadRing) round(s0, std::true_type{});
+        round(S - kHeadRing, std::false_type{});
         __syncthreads();  // inv_s
         // Lane l, register i: row r0 + 16rb + 4(l/16) + i, column 16cb + l%16.
         // (A transpose through LDS, each lane then scanning one row's 16
