@@ -15,6 +15,13 @@ pages within one step and across steps, partial tails are shared and
 copied, and decoding requests copy their republished tail every step
 (miniprefix/src/engine/engine.cpp:98, prefix_cache.cpp:147-148).
 
+Two more variants set an EOS token (the token the scenario emits most often
+without one, which ends a request early, in a step where others go on),
+with the prefix cache on and off: a request that may finish releases
+its sequence only once its result is known, and the batched Engine keeps the
+appends after it in the same device pass unless they take pages from the
+pool or publish into the cache.
+
 A CPU variant runs the reference Engine over the reference CpuRunner against
 the oracle-KV runner (tokens and events only), which checks the scenario
 itself without a GPU."""
@@ -45,13 +52,13 @@ def scenario(vocabulary: int):
     ]
 
 
-def transcript(engine: Engine, runner: Runner | None, submits, steps: int = 40):
+def transcript(engine: Engine, runner: Runner | None, submits, steps: int = 40, eos: int | None = None):
     out, live = [], set()
     pending = sorted(submits, key=lambda s: s[0])
     for step in range(steps):
         while pending and pending[0][0] <= step:
             _, rid, prompt, n = pending.pop(0)
-            engine.submit(rid, prompt, max_new_tokens=n, eos_token_id=None)
+            engine.submit(rid, prompt, max_new_tokens=n, eos_token_id=eos)
             live.add(rid)
         engine.step()
         events = engine.poll_events()
@@ -75,19 +82,38 @@ def transcript(engine: Engine, runner: Runner | None, submits, steps: int = 40):
 CONFIG = dict(smollm_config(layers=2, context=512))
 KV = dict(block_tokens=16, max_blocks=96, prefix_cache_blocks=48)
 ENGINE = dict(max_batch_size=4, token_budget=96, prefill_chunk=24, context=512)
+# (prefix cache pages, EOS from the scenario's own tokens)
+VARIANTS = {"cache": (48, False), "cache_eos": (48, True), "no_cache_eos": (0, True)}
 
 
-def reference_run(kind: int):
+def frequent_token(t) -> int:
+    """The token the transcript's events carry most often (ties: smallest)."""
+    counts = {}
+    for _, _, events, _ in t:
+        for e in events:
+            if e.get("token") is not None:
+                counts[e["token"]] = counts.get(e["token"], 0) + 1
+    return min(counts, key=lambda k: (-counts[k], k))
+
+
+def reference_run(kind: int, variant: str = "cache"):
+    """The reference Engine's transcript and COW counters, and the EOS token
+    the variant uses (None for none)."""
     ref = reference_library()
     if ref is None:
         pytest.skip("oracle/_ref not built")
+    cache, with_eos = VARIANTS[variant]
+    eos = None
+    if with_eos:
+        base, _, _ = reference_run(kind, "cache")
+        eos = frequent_token(base)
     w = Weights.synthetic(CONFIG, seed=SEED, stddev=0.02, library=ref)
-    runner = Runner(w, context=512, kind=kind, **KV)
+    runner = Runner(w, context=512, kind=kind, **dict(KV, prefix_cache_blocks=cache))
     engine = Engine(runner, **ENGINE)
-    t = transcript(engine, runner if kind == 1 else None, scenario(CONFIG["vocabulary"]))
+    t = transcript(engine, runner if kind == 1 else None, scenario(CONFIG["vocabulary"]), eos=eos)
     costs = runner.cost_stats()
     engine.shutdown()
-    return t, costs
+    return t, costs, eos
 
 
 def strip_tables(t):
@@ -98,24 +124,28 @@ def test_scenario_on_reference_runners():
     """CPU: the reference Engine over the reference CpuRunner and over the
     oracle-KV runner emit the same events (the oracle forward is the
     reference's arithmetic)."""
-    cpu, _ = reference_run(0)
-    okv, costs = reference_run(1)
+    cpu, _, _ = reference_run(0)
+    okv, costs, _ = reference_run(1)
     assert strip_tables(cpu) == strip_tables(okv)
     assert costs["cow_pages"] > 0  # the scenario exercises copy-on-write
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("variant", sorted(VARIANTS))
 @pytest.mark.parametrize("kind", [0, 2], ids=["exact", "fast"])
 @pytest.mark.parametrize("batching", [True, False])
-def test_hip_engine_matches_reference_engine(torch_cuda, batching, kind):
+def test_hip_engine_matches_reference_engine(torch_cuda, batching, kind, variant):
     """Exact arithmetic (kind 0) and fast arithmetic (kind 2) alike: the same
     events, tokens and page tables as the reference engine at every step."""
-    want, want_costs = reference_run(1)
+    want, want_costs, eos = reference_run(1, variant)
+    if eos is not None:
+        # The EOS token ends some requests early: the variant tests what it says.
+        assert any(e.get("finish") == "eos" for _, _, events, _ in want for e in events), eos
     w = Weights.synthetic(CONFIG, seed=SEED, stddev=0.02)
-    runner = Runner(w, context=512, kind=kind, **KV)
+    runner = Runner(w, context=512, kind=kind, **dict(KV, prefix_cache_blocks=VARIANTS[variant][0]))
     engine = Engine(runner, **ENGINE)
     engine.set_batching(batching)
-    got = transcript(engine, runner, scenario(CONFIG["vocabulary"]))
+    got = transcript(engine, runner, scenario(CONFIG["vocabulary"]), eos=eos)
     costs = runner.cost_stats()
     engine.shutdown()
     for g, r in zip(got, want):
