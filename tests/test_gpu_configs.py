@@ -3,8 +3,7 @@ written from the reference's own MiniPrefix (tests/golden/make_fixtures.py).
 
 Each workload (tinyinfer_amd/workloads.py: configs 2, 3, 4, 5A, 5B) runs
 through this repository's Engine with batched steps over the HIP runner in
-the fast arithmetic, as bench.py runs it (configs 2 and 4 also in the exact
-arithmetic). After every engine step the digest of every resident
+the fast arithmetic, as bench.py runs it, and in the exact arithmetic. After every engine step the digest of every resident
 sequence's committed page table and the step's token counts must equal the
 reference Engine's; the copy-on-write counters must equal its counts at the
 end; and the greedy tokens of the fixture's requests must equal the
@@ -112,8 +111,7 @@ def run_workload(name, kind, check=None):
     return wl, tokens, digests, np.array(stats), costs
 
 
-CASES = [(name, 2) for name in ("config2", "config3", "config4", "config5b", "config5a")] + \
-        [("config2", 0), ("config4", 0)]
+CASES = [(name, kind) for kind in (2, 0) for name in ("config2", "config3", "config4", "config5b", "config5a")]
 
 
 @pytest.mark.parametrize("name,kind", CASES, ids=[f"{n}-{'fast' if k == 2 else 'exact'}" for n, k in CASES])

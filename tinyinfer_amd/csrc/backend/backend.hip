@@ -834,7 +834,7 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
     const size_t base_entries = 3 * (size_t)R + 2 * (size_t)nseq + 2 * nblocks + 2 * items;
     const size_t fast_at = align4(base_entries);
     const size_t merge_at = fast_at + 4;
-    const size_t short_at = merge_at + align4(2 * (size_t)nseq);
+    const size_t short_at = merge_at + 4 * (size_t)nseq;
     const size_t items_at = short_at + (size_t)mphip::kShortItemInts * nseq * c.kv_heads;
     const size_t pre_at = fast_rows ? align4(items_at + 4 * fast_items) : fast_at;
     const size_t tables_at = pre_at + 4 * fast_pre;
@@ -849,7 +849,7 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
     const size_t chunks_limit = (size_t)score_chunks(c.context);
     const size_t bound = 3 * (size_t)R + 2 * (size_t)nseq + 2 * (size_t)R * (1 + chunks_limit) + 16 +
                          2 * table_pairs + 3 * copies +
-                         (fast_rows ? 4 + 2 * (size_t)nseq + (size_t)mphip::kShortItemInts * nseq * c.kv_heads +
+                         (fast_rows ? 4 + 4 * (size_t)nseq + (size_t)mphip::kShortItemInts * nseq * c.kv_heads +
                                           4 * items_capacity +
                                           4 * ((size_t)R / 16 + (size_t)nseq) * c.kv_heads
                                     : 0);
@@ -923,8 +923,11 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
         for (int q = 0; q < nseq; ++q) {
             if (steps[q].count != 1) continue;
             if (!mphip::fast_attention_short(steps[q].used + 1)) {
-                m_merge[2 * mr] = m_last[q];
-                m_merge[2 * mr + 1] = q;
+                const int length = steps[q].used + 1, split = mphip::fast_attention_split(length);
+                m_merge[4 * mr] = m_last[q];
+                m_merge[4 * mr + 1] = q;
+                m_merge[4 * mr + 2] = (length + split - 1) / split;
+                m_merge[4 * mr + 3] = 0;
                 ++mr;
                 continue;
             }
@@ -1432,7 +1435,7 @@ int mp_hip_paged_attention_decode_fast(const float* q, const float* keys, const 
         }
         const int split = mphip::fast_attention_split(length), splits = (length + split - 1) / split;
         max_splits = std::max(max_splits, splits);
-        merge_rows.insert(merge_rows.end(), {r, r});
+        merge_rows.insert(merge_rows.end(), {r, r, splits, 0});
     }
     for (int pass = 0; pass < 2; ++pass)
         for (int r = 0; r < rows; ++r) {
@@ -1451,7 +1454,7 @@ int mp_hip_paged_attention_decode_fast(const float* q, const float* keys, const 
     // the partials.
     const std::vector<int32_t> counts = {(int32_t)(split_items.size() / 4),
                                          (int32_t)(short_items.size() / mphip::kShortItemInts),
-                                         (int32_t)(merge_rows.size() / 2), 0};
+                                         (int32_t)(merge_rows.size() / 4), 0};
     const size_t ints = counts.size() + split_items.size() + short_items.size() + merge_rows.size() + positions.size();
     const size_t int_bytes = (ints * sizeof(int32_t) + 255) / 256 * 256;
     const size_t partial_floats = (size_t)rows * kv_heads * max_splits * group * (64 + 2);

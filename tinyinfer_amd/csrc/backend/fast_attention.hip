@@ -356,23 +356,23 @@ __global__ __launch_bounds__(kSplitPages * 64) void fast_attention_short_kernel(
 // 16k tokens in 256-token splits, takes one round of loads). The four
 // groups are then rescaled to the common maximum and summed as
 // (g0 + g1) + (g2 + g3). The order depends on nothing but the row's split
-// count. The partials sit at a fixed stride per (sequence, KV head), so the
-// first round is issued together with the load of the row's position.
+// count. The row's list entry carries its split count, so the first round
+// of loads depends on that one load only and reads no slot past the row's
+// splits.
 template <bool PLAIN>
 __global__ __launch_bounds__(256) void fast_attention_merge_kernel(int heads, int kv_heads, RowMeta meta,
                                                                    FastAttentionWork w, float* __restrict__ out,
                                                                    int ldo) {
     const int lane = threadIdx.x & 63;
     const int pair = blockIdx.x * 4 + (threadIdx.x >> 6);
-    int2 rs = {0, 0};
-    if (pair / heads < w.merge_capacity) rs = reinterpret_cast<const int2*>(w.merge_rows)[pair / heads];
+    int4 rs = {0, 0, 1, 0};  // row, sequence, splits
+    if (pair / heads < w.merge_capacity) rs = reinterpret_cast<const int4*>(w.merge_rows)[pair / heads];
     if (pair >= (w.counts ? w.counts[2] : w.merge_count) * heads) return;
-    const int row = rs.x, h = pair % heads;
+    const int row = rs.x, h = pair % heads, splits = rs.z;
     const int G = heads / kv_heads, kvh = h / G, hg = h % G;
     const int grp = lane >> 4, c = lane & 15;
     const size_t slot0 = ((size_t)rs.y * kv_heads + kvh) * w.split_stride;  // split 0 of (sequence, kvh)
     auto at = [&](int sp) { return (slot0 + sp) * G + hg; };
-    int pos = meta.row_pos[row];
     float gm = -__builtin_inff(), gl = 0.0f;
     f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
     float mv[kMergeHeld] = {}, lv[kMergeHeld] = {};
@@ -408,15 +408,7 @@ __global__ __launch_bounds__(256) void fast_attention_merge_kernel(int heads, in
         }
         gm = rm;
     };
-    // Bounded, until the row's own count is known, by the step's most splits
-    // (a launch that a graph replays: by the most any row can have).
-    load(0, w.counts ? w.split_stride : w.max_splits);
-    // The row's position is first needed here, after the loads above are in flight.
-    __builtin_amdgcn_sched_barrier(0);
-    asm volatile("" : "+v"(pos));
-    if (fast_attention_short(pos + 1)) return;  // written by the short-row kernel
-    const int split = fast_attention_split(pos + 1);
-    const int splits = (pos + split) / split;  // ceil((pos + 1) / split)
+    load(0, splits);
     combine(0, splits);
     for (int r = 1; 4 * r * kMergeHeld < splits; ++r) {
         load(r, splits);

@@ -218,7 +218,7 @@ struct FastAttentionWork {
     const int32_t* short_items;
     int short_count, short_capacity;
     // the rows whose splits the merge kernel combines (the one-token rows
-    // longer than 256 tokens), as (row, sequence) int32 pairs
+    // longer than 256 tokens), as (row, sequence, splits, 0) int4s
     const int32_t* merge_rows;
     int merge_count, merge_capacity;
     // Grids sized by the capacities instead of the counts (a launch that a
