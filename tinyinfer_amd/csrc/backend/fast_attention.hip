@@ -30,11 +30,13 @@
 // keeps a reference maximum per head that is raised only when a score
 // exceeds it by more than 16 (probabilities then stay below e^16 and the
 // sums are rescaled), so most pages need no cross-lane maximum.
-// Loads past the split's last page re-read that page (a cache hit) so that
-// every load is unconditional and the waits stay exact. Rows of up to 256
-// tokens (at most 8 splits) run as one work-group per (row, KV head) that
-// combines its splits in LDS; the splits of longer rows write partials that
-// a merge kernel combines.
+// Whole splits (8 or 16 pages; 2 for a short row's 32-token splits) run the
+// page loop compiled for their page count, which loads exactly their pages.
+// A row's last split, of any length, keeps every load unconditional, so that
+// each page's wait counts a fixed number of later loads: its loads past the
+// last page re-read that page. Rows of up to 256 tokens (at most 8 splits)
+// run as one work-group per (row, KV head) that combines its splits in LDS;
+// the splits of longer rows write partials that a merge kernel combines.
 // (Combining in the last split to finish costs each split a store
 // completion and an atomic round trip at its end, more than the extra
 // launch; with a device-scope release fence it would also write back the
