@@ -6,6 +6,9 @@
   both builds must pass the same assertions.
 - tests/native/staged_engine_tests.cpp (this runtime only) checks that the
   batched engine path gives the per-request path's events and page tables.
+- The three restatements also run on this runtime built with
+  AddressSanitizer and UndefinedBehaviorSanitizer (host code only), where
+  any report fails the run.
 - The reference's own host test files (miniprefix/tests/*_test.cpp that need
   no model runner) are compiled against both runtimes and must behave
   identically. engine_history_test.cpp stops at its line 55 on both (the
@@ -15,6 +18,7 @@
 
 Reference builds go to oracle/_ref/host (never committed, never shipped to
 run on a GPU)."""
+import os
 import shutil
 import subprocess
 from pathlib import Path
@@ -48,14 +52,17 @@ def reference_includes():
     return [REFERENCE / "miniprefix" / "include", REFERENCE / "include", REFERENCE / "src"]
 
 
-def _archive(out_dir: Path, name: str, includes, sources) -> Path:
+SANITIZE = ["-g", "-fno-omit-frame-pointer", "-fsanitize=address,undefined", "-fno-sanitize-recover=undefined"]
+
+
+def _archive(out_dir: Path, name: str, includes, sources, flags=()) -> Path:
     """Compiles a runtime's sources once into a static archive."""
     out_dir.mkdir(parents=True, exist_ok=True)
     objects = []
     for i, src in enumerate(sources):
         obj = out_dir / f"{name}_{i}_{src.stem}.o"
-        subprocess.run([GXX, "-std=c++17", "-O1", "-w", "-UNDEBUG", *[f"-I{p}" for p in includes], "-c", str(src),
-                        "-o", str(obj)], check=True, capture_output=True, text=True, timeout=300)
+        subprocess.run([GXX, "-std=c++17", "-O1", "-w", "-UNDEBUG", *flags, *[f"-I{p}" for p in includes], "-c",
+                        str(src), "-o", str(obj)], check=True, capture_output=True, text=True, timeout=300)
         objects.append(str(obj))
     lib = out_dir / f"lib{name}.a"
     lib.unlink(missing_ok=True)
@@ -63,9 +70,9 @@ def _archive(out_dir: Path, name: str, includes, sources) -> Path:
     return lib
 
 
-def _build(out_dir: Path, exe: str, test_source: Path, includes, archive: Path) -> Path:
+def _build(out_dir: Path, exe: str, test_source: Path, includes, archive: Path, flags=()) -> Path:
     path = out_dir / exe
-    proc = subprocess.run([GXX, "-std=c++17", "-O1", "-w", "-UNDEBUG", *[f"-I{p}" for p in includes],
+    proc = subprocess.run([GXX, "-std=c++17", "-O1", "-w", "-UNDEBUG", *flags, *[f"-I{p}" for p in includes],
                            str(test_source), str(archive), "-o", str(path)], capture_output=True, text=True,
                           timeout=300)
     assert proc.returncode == 0, proc.stderr[-4000:]
@@ -83,6 +90,16 @@ def mine(tmp_path_factory):
 
 
 @pytest.fixture(scope="module")
+def mine_sanitized(tmp_path_factory):
+    out = tmp_path_factory.mktemp("host_mine_sanitized")
+    probe = subprocess.run([GXX, *SANITIZE, "-x", "c++", "-", "-o", str(out / "probe")], input="int main(){}",
+                           capture_output=True, text=True, timeout=120)
+    if probe.returncode != 0:
+        pytest.skip("the sanitizer runtimes are not available")
+    return out, [HOST, NATIVE], _archive(out, "mine", [HOST], MINE_SOURCES, SANITIZE)
+
+
+@pytest.fixture(scope="module")
 def reference():
     if not (REFERENCE / "miniprefix").exists():
         pytest.skip("reference tree not present")
@@ -96,6 +113,17 @@ def test_restatement(mine, test):
     proc = _run(_build(out, test, NATIVE / f"{test}.cpp", includes, archive))
     assert proc.returncode == 0, proc.stderr[-4000:]
     assert "passed" in proc.stdout
+
+
+@pytest.mark.parametrize("test", ["host_tests", "engine_tests", "staged_engine_tests"])
+def test_restatement_under_sanitizers(mine_sanitized, test):
+    out, includes, archive = mine_sanitized
+    exe = _build(out, test, NATIVE / f"{test}.cpp", includes, archive, SANITIZE)
+    proc = subprocess.run([str(exe)], capture_output=True, text=True, timeout=300,
+                          env={**os.environ, "ASAN_OPTIONS": "detect_leaks=1:abort_on_error=0"})
+    assert proc.returncode == 0, proc.stderr[-4000:]
+    assert "passed" in proc.stdout
+    assert "runtime error" not in proc.stderr and "AddressSanitizer" not in proc.stderr
 
 
 @needs_reference

@@ -6,7 +6,9 @@ CPU:
   response lines, a session transcript over a recording runner, end of input,
   a failed engine) on this repository's protocol and host runtime and, where
   the reference tree exists, on the reference's own protocol sources
-  (miniprefix/apps/protocol/*.cpp) and runtime: both must pass;
+  (miniprefix/apps/protocol/*.cpp) and runtime: both must pass; also on this
+  repository's protocol and runtime built with AddressSanitizer and
+  UndefinedBehaviorSanitizer;
 - the reference's own miniprefix/tests/worker_protocol_test.cpp compiled
   against this repository's protocol and runtime, with the same output as
   when built on the reference's;
@@ -25,8 +27,8 @@ import pytest
 from tinyinfer_amd.host import Engine, Runner, Weights
 
 from .helpers import reference_library, smollm_config
-from .test_host_native import GXX, MINE_SOURCES, REFERENCE, REF_OUT, _archive, _build, _run, needs_reference, \
-    reference_includes, reference_sources
+from .test_host_native import GXX, MINE_SOURCES, REFERENCE, REF_OUT, SANITIZE, _archive, _build, _run, \
+    needs_reference, reference_includes, reference_sources
 from .test_mpfx_loader import source_tensors, write_mpfx
 
 ROOT = Path(__file__).resolve().parent.parent
@@ -60,6 +62,22 @@ def test_protocol_restatement(mine_protocol):
     proc = _run(_build(out, "worker_tests", NATIVE / "worker_tests.cpp", includes, archive))
     assert proc.returncode == 0, proc.stderr[-4000:]
     assert "passed" in proc.stdout
+
+
+def test_protocol_restatement_under_sanitizers(tmp_path):
+    """The same restatement on the protocol and runtime built with
+    AddressSanitizer and UndefinedBehaviorSanitizer (host code only)."""
+    probe = subprocess.run([GXX, *SANITIZE, "-x", "c++", "-", "-o", str(tmp_path / "probe")], input="int main(){}",
+                           capture_output=True, text=True, timeout=120)
+    if probe.returncode != 0:
+        pytest.skip("the sanitizer runtimes are not available")
+    includes = [HOST, WORKER_SRC]
+    archive = _archive(tmp_path, "mine_worker", includes, MINE_SOURCES + [WORKER_SRC / "protocol.cpp"], SANITIZE)
+    exe = _build(tmp_path, "worker_tests", NATIVE / "worker_tests.cpp", includes, archive, SANITIZE)
+    proc = subprocess.run([str(exe)], capture_output=True, text=True, timeout=300)
+    assert proc.returncode == 0, proc.stderr[-4000:]
+    assert "passed" in proc.stdout
+    assert "runtime error" not in proc.stderr and "AddressSanitizer" not in proc.stderr
 
 
 @needs_reference
