@@ -7,9 +7,9 @@ the fast arithmetic, as bench.py runs it, and in the exact arithmetic. After eve
 sequence's committed page table and the step's token counts must equal the
 reference Engine's; the copy-on-write counters must equal its counts at the
 end; and the greedy tokens of the fixture's requests must equal the
-reference CpuRunner's at every recorded step (config 5A: the first 16
-decode steps of one request, the reference's 16,384-token CPU prefill being
-the cost; a fixture written with make_fixtures.py --engine-only holds no
+reference CpuRunner's at every recorded step (config 5A: six of its eight
+requests, the reference's 16,384-token CPU prefill of each being the cost;
+a fixture written with make_fixtures.py --engine-only holds no
 token streams, and then only the page tables and counts are checked). The
 fixtures also hold each step's top-2 logit margin, which tells how close a
 mismatch would have been to a tie.
