@@ -899,15 +899,18 @@ int mp_hip_forward(mp_hip* h, const mp_seq_step* steps, int32_t nseq, const int3
         // A one-token sequence q's row is m_last[q]. Whole splits first, then
         // each row's shorter last split (attention per layer: config 4 15.8-16.1
         // vs 17.2 us in row order, config 5B 80.1 vs 82.4, config 3 within
-        // noise).
+        // noise); a split's KV heads side by side, so that the waves of one
+        // work-group read the adjacent pages of one (block, layer) together
+        // (config 3 30.65-30.87 vs 30.86-30.96 us, config 5B 81.7-81.8 vs
+        // 82.2-82.6 with each KV head's splits in a run).
         size_t f = 0;
         for (int pass = 0; pass < 2; ++pass)
             for (int q = 0; q < nseq; ++q) {
                 const int length = steps[q].used + 1, split = mphip::fast_attention_split(length);
                 const int splits = (length + split - 1) / split;
                 if (steps[q].count != 1 || mphip::fast_attention_short(length)) continue;
-                for (int kvh = 0; kvh < c.kv_heads; ++kvh)
-                    for (int sp = 0; sp < splits; ++sp) {
+                for (int sp = 0; sp < splits; ++sp)
+                    for (int kvh = 0; kvh < c.kv_heads; ++kvh) {
                         const int n = std::min(split, length - sp * split);
                         if ((n == split) != (pass == 0)) continue;
                         m_fast[4 * f] = m_last[q];
