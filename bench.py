@@ -249,6 +249,7 @@ def gpu_leg(args, wl):
         value=batch * K / elapsed, ms_per_step=elapsed / K * 1e3, batch=batch, prefill_steps=setup_steps + prefill_steps,
         mean_context=attended(args.warmup, K) / (K * batch), decode_steps=remaining, roofline_steps=R,
         roofline_context=sum_t / (R * batch), times=times, cow=costs,
+        roofline_lengths=(min(used0.values()) + first_rof + 1, max(used0.values()) + first_rof + R),
         whole=dict(value=round(batch * len(clean) / whole_s, 2), steps=len(clean),
                    ms_per_step=round(whole_s / len(clean) * 1e3, 4), mean_context=round(whole_ctx, 1)),
         attention=dict(us=att_s / att_launches * 1e6, bytes=att_bytes / att_launches, gbs=att_bytes / att_s / 1e9),
@@ -364,11 +365,19 @@ def oracle_cpu_leg(args, wl, cfg, prompt, info):
                        f"{len(prompt) + 1}..{len(prompt) + decoded} ({spent:.1f}s)", **info)
 
 
+SHORT_ROW_TOKENS = 256  # decode rows of up to this many tokens take the one-work-group attention kernel
+GEMV_SEQUENCES = 4  # decode steps of up to this many sequences run their projections as GEMV
+
+
 def roofline(kind: str, g: dict, rec: dict | None):
     if kind == "attention":
         a = g["attention"]
         ratio = rec.get("attention_ratio") if rec else None
-        return {"bound": "hbm", "kernel": "paged attention (one layer: split kernel + merge kernel)",
+        shortest, longest = g["roofline_lengths"]
+        kernels = ("the short-row kernel" if longest <= SHORT_ROW_TOKENS else
+                   "split kernel + merge kernel" if shortest > SHORT_ROW_TOKENS else
+                   "split kernel + merge kernel, short-row kernel")
+        return {"bound": "hbm", "kernel": f"paged attention (one layer: {kernels})",
                 "achieved": round(a["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(a["gbs"] / HBM_PEAK_GBS, 4),
                 "traffic": int(round(ratio * a["bytes"])) if ratio else None, "traffic_ratio": ratio,
@@ -377,13 +386,17 @@ def roofline(kind: str, g: dict, rec: dict | None):
                                  f"mean context {g['roofline_context']:.1f}"}
     p = g["projections"]
     ratio = rec.get("projection_ratio") if rec else None
-    return {"bound": "hbm", "kernel": "projections (one layer: q|k|v+RoPE, o, gate/up+SwiGLU, down)",
+    gemv = g["batch"] <= GEMV_SEQUENCES
+    # GEMV runs on the vector ALUs, whose FP32 peak equals the matrix cores' on this chip.
+    flops = {"achieved": round(p["tflops"], 2), "peak": FP32_MATRIX_PEAK_TFLOPS, "unit": "TFLOP/s",
+             "frac": round(p["tflops"] / FP32_MATRIX_PEAK_TFLOPS, 4), "flops_per_launch": int(p["flops"])}
+    return {"bound": "hbm", "kernel": f"projections (one layer: q|k|v+RoPE, o, gate/up+SwiGLU, down"
+                                      f"{'; FP32 GEMV' if gemv else '; FP32 matrix cores'})",
             "achieved": round(p["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(p["gbs"] / HBM_PEAK_GBS, 4),
             "traffic": int(round(ratio * p["bytes"])) if ratio else None, "traffic_ratio": ratio,
             "algorithmic_bytes_per_launch": int(p["bytes"]), "us_per_launch": round(p["us"], 2),
-            "mfma": {"achieved": round(p["tflops"], 2), "peak": FP32_MATRIX_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(p["tflops"] / FP32_MATRIX_PEAK_TFLOPS, 4), "flops_per_launch": int(p["flops"])}}
+            ("fp32_vector" if gemv else "mfma"): flops}
 
 
 def decode_dispatches(rows: list, steps: int, path: str) -> range:
@@ -415,10 +428,13 @@ def summarise_counters(fetch_csv: str, write_csv: str, bench_json: str, out: str
     line = json.loads(Path(bench_json).read_text().strip().splitlines()[-1])
     fast = line["config"].get("arithmetic") == "fast"
     # The decode kernels (prefill runs other instantiations).
-    att_kernels = (("fast_attention_kernel<", "fast_attention_merge_kernel") if fast else
-                   ("attn_scores_kernel<16, 64, true>", "attn_decode_kernel<"))
+    att_kernels = (("fast_attention_kernel<", "fast_attention_merge_kernel", "fast_attention_short_kernel") if fast
+                   else ("attn_scores_kernel<16, 64, true>", "attn_decode_kernel<"))
+    # The matrix-core projections of B=64 (the residual one twice per layer),
+    # or the GEMV ones of steps of up to four sequences (each once).
     proj_kernels = (("fast_gemm_kernel<4, true, false, 1, 1, 12>", "fast_gemm_kernel<1, false, false, 1, 1, 12>",
-                     "fast_gemm_kernel<2, true, false, 2, 1, 6>") if fast else ("gemm_column",))
+                     "fast_gemm_kernel<2, true, false, 2, 1, 6>", "gemv_rope_kernel", "gemv_residual_kernel",
+                     "gemv_swiglu_kernel") if fast else ("gemm_column",))
 
     def read(path):
         rows = list(csv.DictReader(open(path)))
@@ -435,7 +451,8 @@ def summarise_counters(fetch_csv: str, write_csv: str, bench_json: str, out: str
         return per, probe
 
     result = {"workload": line["config"]["workload"], "seed": line["config"]["seed"],
-              "arithmetic": line["config"].get("arithmetic"), "window": line["roofline"]["measured_over"],
+              "arithmetic": line["config"].get("arithmetic"),
+              "window": line["roofline" if "attention" in line["roofline"]["kernel"] else "roofline_other"]["measured_over"],
               "steps": line["steps"], "warmup": line["warmup"]}
     for counter, path in (("fetch", fetch_csv), ("write", write_csv)):
         per, probe = read(path)
